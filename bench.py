@@ -1,0 +1,277 @@
+"""Decode-step benchmark on one MI355X: int8 (W8A16) linears + paged-attention decode.
+
+Workload: a Llama-3-8B-shaped int8 weight-only decoder
+(32 layers, hidden 4096, 32 q / 8 kv heads, head_dim 128, intermediate 14336,
+vocab 128256), batch 32, one token per row per step, paged fp16 KV with
+block_size 16 in a 16384-block pool, contexts ~ U[128, 4096] drawn with seed 0
+(config-2-like), block tables from one randperm of the pool. Weights are random
+N(0, 0.02) quantized on the device with the build's int8 format; K/V and
+embeddings are random. Inputs are resident in HBM before timing starts.
+
+Prints ONE JSON line. ``value`` = decode tokens/s of the whole step (B tokens per
+step), timed over ``--steps`` HIP-graph replays of the step after ``--warmup``
+eager steps. ``roofline`` is for the dominant kernel family, from HIP events
+around each of its launches during ``--kernel-steps`` eager steps of the same
+decode (same stream). ``cpu_baseline`` times the CPU oracle on a bounded sample
+(one decoder layer at the same batch and contexts, plus an lm_head slice),
+extrapolated to the full step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "llm-serving-runtime_amd"))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--model", choices=["llama3-8b", "qwen2-0.5b"], default="llama3-8b")
+    ap.add_argument("--layers", type=int, default=None, help="override layer count (diagnostics only)")
+    ap.add_argument("--ctx-lo", type=int, default=128)
+    ap.add_argument("--ctx-hi", type=int, default=4096)
+    ap.add_argument("--pool-blocks", type=int, default=16384)
+    ap.add_argument("--kernel-steps", type=int, default=3)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=1)
+    return ap.parse_args()
+
+
+def cpu_info() -> dict:
+    info = {"cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    info["model"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return info
+
+
+def cpu_baseline(shape, batch: int, lens, layers_total: int) -> dict:
+    """Time the CPU oracle on one decoder layer (4 dequantized fp32 linears + fp32 paged
+    attention over the same contexts) and an lm_head slice; extrapolate to the step."""
+    import numpy as np
+    import torch
+
+    from oracle import int8_quant, paged_attention
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(0)
+    s = shape
+    mats = {
+        "qkv": (s.qkv_out, s.hidden),
+        "o": (s.hidden, s.heads * s.head_dim),
+        "gate_up": (2 * s.intermediate, s.hidden),
+        "down": (s.hidden, s.intermediate),
+    }
+    weights = {}
+    for name, (n, k) in mats.items():
+        q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        sc = (np.abs(rng.standard_normal(n)) * 1e-3 + 1e-4).astype(np.float16)
+        weights[name] = torch.from_numpy(int8_quant.dequantize(q, sc))
+    vocab_slice = 16384
+    lm_q = rng.integers(-127, 128, size=(vocab_slice, s.hidden), dtype=np.int8)
+    lm_w = torch.from_numpy(int8_quant.dequantize(lm_q, np.full(vocab_slice, 1e-3, np.float16)))
+    bs = 16
+    lens = [int(x) for x in lens]
+    nblk = [math.ceil(x / bs) for x in lens]
+    tables = torch.zeros(batch, max(nblk), dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(nblk):
+        tables[b, :n] = torch.arange(used, used + n, dtype=torch.int32)
+        used += n
+    g = torch.Generator().manual_seed(1)
+    k_layer = torch.randn(used, s.kv_heads, bs, s.head_dim, generator=g).to(torch.float16)
+    v_layer = torch.randn(used, s.kv_heads, bs, s.head_dim, generator=g).to(torch.float16)
+    x = torch.randn(batch, s.hidden, generator=g)
+    q = torch.randn(batch, s.heads, 1, s.head_dim, generator=g).to(torch.float16)
+
+    def one_layer():
+        y = x @ weights["qkv"].T
+        attn = paged_attention.decode_rows_fp32(q, k_layer, v_layer, tables, lens, s.head_dim**-0.5, s.group)
+        y = attn.reshape(batch, -1) @ weights["o"].T
+        gu = x @ weights["gate_up"].T
+        a = torch.nn.functional.silu(gu[:, :s.intermediate]) * gu[:, s.intermediate:]
+        return a @ weights["down"].T
+
+    one_layer()  # warm
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        one_layer()
+    t_layer = (time.perf_counter() - t0) / reps
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        x @ lm_w.T
+    t_lm = (time.perf_counter() - t0) / reps * (s.vocab / vocab_slice)
+    t_step = t_layer * layers_total + t_lm
+    return {
+        "value": batch / t_step,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"CPU oracle, fp32: 1 decoder layer (4 pre-dequantized int8 linears + per-row fp32 paged "
+                   f"attention over the same {batch} contexts) x{reps} + lm_head on {vocab_slice}/{s.vocab} rows, "
+                   f"extrapolated to {layers_total} layers + full lm_head"),
+        "sec_per_step": t_step,
+        "host": cpu_info(),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path shards without exchange; see the design notes). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from runtime_amd.phase2 import _hip
+    from runtime_amd.phase2.decode_step import LLAMA3_8B, QWEN2_05B, Int8DecodeModel, make_contexts
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+    from oracle.paged_attention import attention_bytes
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    _hip.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    shape = LLAMA3_8B if args.model == "llama3-8b" else QWEN2_05B
+    n_layers = args.layers or shape.layers
+    bsz = args.batch
+    bs = 16
+    total_steps = args.warmup + args.steps + args.kernel_steps + 2
+    lens, tables = make_contexts(bsz, args.ctx_lo, args.ctx_hi, bs, args.pool_blocks, headroom=total_steps, seed=0)
+    t_setup = time.perf_counter()
+    model = Int8DecodeModel(shape, device=dev, seed=0, layers=n_layers)
+    pool = GpuKVBlockPool(num_blocks=args.pool_blocks, block_size_tokens=bs, num_layers=n_layers,
+                          num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16, device=dev)
+    pool._ensure_pools()
+    gk = torch.Generator(device=dev).manual_seed(1)
+    for t in (pool._k_pool, pool._v_pool):
+        flat = t.view(-1)
+        chunk = 1 << 28
+        for i in range(0, flat.numel(), chunk):
+            flat[i:i + chunk].normal_(generator=gk)
+    tables_d = tables.to(dev)
+    seq_lens = lens.to(dev).clone()
+    tokens = torch.randint(0, shape.vocab, (bsz,), generator=torch.Generator().manual_seed(2)).to(dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    def step():
+        nxt = model.step(tokens, pool, tables_d, seq_lens)
+        tokens.copy_(nxt)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    graph = None
+    if not args.no_graph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()  # one more eager step on the capture stream
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+
+    lens_before = seq_lens.cpu().tolist()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    lens_after = seq_lens.cpu().tolist()
+
+    # Per-kernel durations: eager steps with HIP events around each launch (same stream).
+    timers: dict = {}
+    for _ in range(args.kernel_steps):
+        nxt = model.step(tokens, pool, tables_d, seq_lens, timers=timers)
+        tokens.copy_(nxt)
+    torch.cuda.synchronize()
+    kdur = {k: [a.elapsed_time(b) * 1e-3 for a, b in v] for k, v in timers.items()}
+
+    # Algorithmic bytes.
+    lin = model.linear_bytes(bsz)
+    mid_lens = [(a + b) / 2 + 1 for a, b in zip(lens_before, lens_after)]
+    attn_b = attention_bytes([round(x) for x in mid_lens], shape.kv_heads, shape.head_dim, shape.heads, bs)
+    append_b = 2 * bsz * shape.kv_heads * shape.head_dim * 2
+    step_bytes = n_layers * (lin["qkv"] + lin["o"] + lin["gate_up"] + lin["down"] + attn_b + append_b) + lin["lm_head"]
+    step_bytes += bsz * shape.hidden * 2
+    per_launch = {"attn": attn_b, **lin}
+    fam = {k: (sum(v), len(v)) for k, v in kdur.items()}
+    dominant = max(fam, key=lambda k: fam[k][0])
+    avg = fam[dominant][0] / fam[dominant][1]
+    achieved = per_launch[dominant] / avg / 1e9
+    kernels = {k: {"avg_us": round(fam[k][0] / fam[k][1] * 1e6, 2), "launches": fam[k][1],
+                   "bytes_per_launch": per_launch[k],
+                   "gbps": round(per_launch[k] / (fam[k][0] / fam[k][1]) / 1e9, 1)} for k in fam}
+
+    value = bsz / (ms * 1e-3)
+    out = {
+        "metric": "decode tokens/sec + achieved HBM GB/s (% peak), int8-W linear + paged-attn",
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w8a16 (int8 weights, fp16 activations/KV, fp32 accumulate)",
+        "data": "synthetic (random-init weights quantized on device, random K/V)",
+        "config": {
+            "workload": f"{args.model}-shaped int8 decode step (int8 linears + paged-attn decode), batch {bsz}",
+            "batch": bsz, "layers": n_layers, "hidden": shape.hidden, "heads": shape.heads,
+            "kv_heads": shape.kv_heads, "head_dim": shape.head_dim, "intermediate": shape.intermediate,
+            "vocab": shape.vocab, "contexts": f"U[{args.ctx_lo},{args.ctx_hi}] seed 0", "block_size": bs,
+            "pool_blocks": args.pool_blocks, "hip_graph": graph is not None, "parallelism": "none (1 GPU)",
+        },
+        "step_hbm_bytes": step_bytes,
+        "step_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+        "step_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+        "kernels": kernels,
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(shape, bsz, lens.tolist(), n_layers)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

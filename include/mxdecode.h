@@ -1,0 +1,126 @@
+/*
+ * mxdecode - MI355X (gfx950) decode-step hot path: weight-only int8 linear
+ * layers and paged-attention decode. C ABI of libmxdecode.so.
+ *
+ * Conventions
+ *   - fp16 tensors are passed as `uint16_t*` (IEEE binary16 bit patterns).
+ *   - Every buffer is caller-owned device memory. No call allocates, frees or
+ *     synchronises. Work is enqueued on `stream` (a hipStream_t passed as
+ *     `void*`; NULL means the legacy default stream).
+ *   - Return value: MX_OK (0) or a negative mx_status. The message of the
+ *     last failure on the calling thread is returned by mx_last_error().
+ *     Nothing throws or aborts across this boundary.
+ *   - Strides are in elements.
+ */
+#ifndef MXDECODE_H
+#define MXDECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MX_ABI_VERSION 1
+
+typedef enum mx_status {
+    MX_OK = 0,
+    MX_ERR_INVALID = -1,     /* bad shape, stride or argument value */
+    MX_ERR_UNSUPPORTED = -2, /* valid but outside the supported envelope */
+    MX_ERR_ALIGNMENT = -3,   /* pointer or stride not suitably aligned */
+    MX_ERR_NULL = -4,        /* required pointer is NULL */
+    MX_ERR_LAUNCH = -5,      /* HIP launch error */
+    MX_ERR_WORKSPACE = -6    /* workspace missing or too small */
+} mx_status;
+
+/* ABI version of the loaded library (MX_ABI_VERSION at build time). */
+int mx_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mx_last_error(void);
+
+/* ----------------------------------------------------------------------------
+ * Weight-only int8 linear (W8A16).
+ *
+ * Replaces the reference's quantized-linear slot: the autoawq WQLinear module
+ * that runtime/phase2/worker_server.py:194-205 loads for PHASE2_QUANT=int4, i.e.
+ * the nn.Linear contract y[..., N] = x[..., K] W^T (+ b) of every decoder-layer
+ * projection (worker_server.py:199-203: the HF decoder layer calls
+ * q/k/v/o/gate/up/down_proj). The int8 format itself is defined by this
+ * build (per-output-channel symmetric absmax, fp16 scales); see
+ * oracle/int8_quant.py for the exact formula and the packed tile layout.
+ * ------------------------------------------------------------------------- */
+
+/* Quantize fp32 weights w[N, K] (row stride K) to int8 q[N, K] and fp16
+ * scales s[N]. Bit-exact with the CPU restatement. Reference: the slot's
+ * model-load step, runtime/phase2/worker_server.py:194-205. */
+int mx_w8a16_quantize(const float* w, int64_t N, int64_t K, int8_t* q, uint16_t* scale, void* stream);
+
+/* Pack q[N, K] (int8, row stride K) into the 1 KiB tile layout read by
+ * mx_w8a16_linear (N % 16 == 0, K % 64 == 0; N*K bytes). Bit-exact.
+ * Reference: same load step, worker_server.py:194-205. */
+int mx_w8a16_pack(const int8_t* q, int64_t N, int64_t K, uint8_t* packed, void* stream);
+
+/* Workspace bytes mx_w8a16_linear needs for this shape (0: none). */
+size_t mx_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* y[m, n] = fp16( scale[n] * sum_k x[m, k] * q[n, k] + bias[n] ), fp32
+ * accumulation. x: fp16 [M, K] with row stride x_stride (16-byte aligned rows);
+ * packed: from mx_w8a16_pack; scale: fp16 [N]; bias: fp16 [N] or NULL;
+ * y: fp16 [M, N] with row stride y_stride. Replaces the forward of the
+ * reference's quantized linear (autoawq WQLinear.forward, reached from the HF
+ * decoder layer; worker_server.py:194-205) and of nn.Linear on the decode path
+ * (worker_server.py:773). */
+int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
+                    const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t N, int64_t y_stride,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ----------------------------------------------------------------------------
+ * Paged-attention decode.
+ *
+ * Replaces paged_attention_decode_batched
+ * (runtime/phase2/paged_attention_triton.py:745-775) and the Triton kernels it
+ * dispatches to: _paged_attn_decode_direct_batched_kernel (:148-243),
+ * _paged_attn_decode_split_kernel (:245-336), _paged_attn_decode_direct_kernel
+ * (:338-412) and _paged_attn_combine_kernel (:414-457).
+ *
+ * q:   fp16 [B, Hq, D] with strides (q_sb, q_sh, 1)      (the [B,Hq,1,D] query)
+ * k,v: fp16 per-layer pool views [num_blocks, Hkv, block_size, D] with strides
+ *      (kv_sblk, kv_shead, D, 1) (GpuKVBlockPool.k_layer_view,
+ *      runtime/phase2/paged_kv_kernel.py:124-134)
+ * block_tables: int32 [B, max_blocks] with row stride bt_sb; entries past a
+ *      row's ceil(seq_len / block_size) blocks are never read
+ * seq_lens: int32 [B], KV length including the current token
+ *      (paged_attention_triton.py:43-50); the kernel reads
+ *      min(ceil(seq_len / block_size), max_blocks) blocks; seq_len <= 0 gives
+ *      a zero output row
+ * out: fp16 [B, Hq, D] with strides (o_sb, o_sh, 1)
+ * num_pool_blocks: block ids outside [0, num_pool_blocks) are skipped and
+ *      recorded in the workspace error word (mx_paged_attn_read_error)
+ * chunk_tokens: split-K chunk (multiple of 16); 0 picks the default. Must be
+ *      the value the workspace was sized for, or larger.
+ * Supported: D in {64, 128}; block_size in {16, 32}; Hq = G * Hkv, G in 1..8.
+ * The workspace must be zero-filled once when allocated; calls leave it
+ * ready for the next call. Concurrent calls must not share a workspace.
+ * ------------------------------------------------------------------------- */
+size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
+                                     int32_t block_size, int32_t chunk_tokens);
+
+int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k, const uint16_t* v,
+                         int64_t kv_sblk, int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb,
+                         int32_t max_blocks, const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                         int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out, int64_t o_sb,
+                         int64_t o_sh, void* workspace, size_t workspace_bytes, int32_t chunk_tokens, void* stream);
+
+/* Byte offset of the int32 error word inside a paged-attention workspace
+ * (nonzero after a call that met an out-of-range block id). Reading it needs a
+ * device-to-host copy by the caller; clearing it is the caller's choice. */
+size_t mx_paged_attn_error_offset(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
+                                  int32_t block_size, int32_t chunk_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXDECODE_H */

@@ -1,0 +1,88 @@
+"""Build libmxdecode.so (HIP, gfx950) in-tree with hipcc.
+
+Usage: ``python llm-serving-runtime_amd/build.py [-v]``. Produces
+``llm-serving-runtime_amd/runtime_amd/libmxdecode.so``. Every call compiles
+from source (no stale-artifact shortcut), one hipcc process per source file.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+OUT = os.path.join(HERE, "runtime_amd", "libmxdecode.so")
+SOURCES = ["status.hip", "w8a16.hip", "paged_attn.hip"]
+ARCH = os.environ.get("MX_OFFLOAD_ARCH", "gfx950")
+
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in generated code.
+# -fhip-fp32-correctly-rounded-divide-sqrt: IEEE fp32 division for the
+# bit-exact quantizer. No fast-math anywhere.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def _hipcc() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found; the HIP library cannot be built")
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in res.stdout.splitlines() if "is not a recognized feature for this target" not in line
+    )
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out, flush=True)
+
+
+def build(verbose: bool = False) -> str:
+    hipcc = _hipcc()
+    with tempfile.TemporaryDirectory(prefix="mxdecode_build_") as tmp:
+        objs = []
+        jobs = []
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as pool:
+            for src in SOURCES:
+                obj = os.path.join(tmp, src.replace(".hip", ".o"))
+                objs.append(obj)
+                cmd = [hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+                jobs.append(pool.submit(_run, cmd, verbose))
+            for j in jobs:
+                j.result()
+        tmp_out = OUT + ".tmp"
+        _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_out], verbose)
+        os.replace(tmp_out, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("-v", "--verbose", action="store_true")
+    args = ap.parse_args()
+    path = build(verbose=args.verbose)
+    print(path)
+    sys.exit(0)

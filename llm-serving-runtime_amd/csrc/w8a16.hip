@@ -1,0 +1,388 @@
+// Weight-only int8 linear (W8A16) for gfx950: quantize, tile pack, and the
+// fused-dequant GEMV (VALU, small M) / GEMM (MFMA) kernels.
+//
+// Replaces the reference's quantized-linear slot (autoawq WQLinear, loaded at
+// runtime/phase2/worker_server.py:194-205) with a build-defined int8 format:
+// per-output-channel symmetric absmax int8 weights, fp16 scales.
+//
+// Packed layout (also restated in oracle/int8_quant.py): tiles of 16 rows x 64
+// columns (1 KiB). Tile (nt, kt) is at byte (nt*KT + kt)*1024, KT = K/64. In a
+// tile, lane l = 16*g + r owns 16 bytes at 16*l: row nt*16 + r, columns
+// kt*64 + 16*g + [0, 16). One wave therefore streams a whole tile with one
+// coalesced 128-bit load per lane. Stored bytes are q ^ 0x80, so that
+// fp16(0x6400 | byte) = 1024 + q + 128 and one packed fp16 add of -1152
+// recovers q exactly: the dequant is 2 v_perm_b32 + 2 v_pk_add_f16 per 4 weights.
+//
+// Work split: a workgroup owns NPW n-tiles (16*NPW output channels) for the
+// whole K; its waves take interleaved k-tiles (wave w: w, w+WAVES, ...) so
+// concurrent waves read adjacent kilobytes; partial sums meet in LDS. The
+// per-channel scale and the bias are applied once, in the epilogue.
+#include "common.h"
+
+namespace mx {
+namespace w8a16 {
+
+constexpr int kTileN = 16;
+constexpr int kTileK = 64;
+constexpr uint32_t kMagic = 0x64646464u;
+constexpr uint32_t kSelLo = 0x04010400u;  // bytes 0,1 -> fp16 pair (0x64:b0, 0x64:b1)
+constexpr uint32_t kSelHi = 0x04030402u;  // bytes 2,3 -> fp16 pair (0x64:b2, 0x64:b3)
+
+struct U32x4 {
+    uint32_t a, b, c, d;
+};
+
+// 8 biased bytes (two dwords) -> 8 exact fp16 weights.
+__device__ __forceinline__ half8v dequant8(uint32_t d0, uint32_t d1) {
+    const U32x4 raw{__builtin_amdgcn_perm(kMagic, d0, kSelLo), __builtin_amdgcn_perm(kMagic, d0, kSelHi),
+                    __builtin_amdgcn_perm(kMagic, d1, kSelLo), __builtin_amdgcn_perm(kMagic, d1, kSelHi)};
+    const half8v bias = (_Float16)(-1152.0f);
+    return __builtin_bit_cast(half8v, raw) + bias;
+}
+
+__device__ __forceinline__ half8v load_half8(const _Float16* p) {
+    return __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(p));
+}
+
+__device__ __forceinline__ float dot8(half8v a, half8v b, float acc) {
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 0, 1), __builtin_shufflevector(b, b, 0, 1), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 2, 3), __builtin_shufflevector(b, b, 2, 3), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 4, 5), __builtin_shufflevector(b, b, 4, 5), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 6, 7), __builtin_shufflevector(b, b, 6, 7), acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ uint16_t f2h_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+__device__ __forceinline__ float h2f(const uint16_t* p, int64_t i) {
+    return (float)reinterpret_cast<const _Float16*>(p)[i];
+}
+
+// ---------------------------------------------------------------------------
+// Quantize: one workgroup of 256 threads per output channel.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ w, int64_t K, int8_t* __restrict__ q,
+                                                       uint16_t* __restrict__ scale) {
+    const int64_t row = blockIdx.x;
+    const float* wr = w + row * K;
+    float amax = 0.0f;
+    int bad = 0;
+    for (int64_t j = threadIdx.x; j < K; j += 256) {
+        const float a = fabsf(wr[j]);
+        bad |= !(a <= 3.4028235e38f);  // NaN or inf
+        amax = fmaxf(amax, a);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off));
+        bad |= __shfl_xor(bad, off);
+    }
+    __shared__ float s_max[4];
+    __shared__ int s_bad[4];
+    if ((threadIdx.x & 63) == 0) {
+        s_max[threadIdx.x >> 6] = amax;
+        s_bad[threadIdx.x >> 6] = bad;
+    }
+    __syncthreads();
+    amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    bad = s_bad[0] | s_bad[1] | s_bad[2] | s_bad[3];
+    // IEEE division (the library is built with correctly rounded fp32 divide).
+    const float s32 = fminf(amax / 127.0f, 65504.0f);
+    _Float16 sh = (_Float16)s32;
+    if (amax == 0.0f) {
+        sh = (_Float16)1.0f;
+    } else if (sh == (_Float16)0.0f) {
+        sh = __builtin_bit_cast(_Float16, (uint16_t)0x0001);
+    }
+    if (bad) sh = __builtin_bit_cast(_Float16, (uint16_t)0x7e00);  // NaN scale flags a non-finite row
+    if (threadIdx.x == 0) scale[row] = __builtin_bit_cast(uint16_t, sh);
+    const float sf = (float)sh;
+    for (int64_t j = threadIdx.x; j < K; j += 256) {
+        float v = __builtin_rintf(wr[j] / sf);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        q[row * K + j] = bad ? (int8_t)0 : (int8_t)(int)v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pack: one thread per 16-byte lane slot of the tile layout.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_kernel(const int8_t* __restrict__ q, int64_t K, int64_t KT, int64_t slots,
+                                                   uint8_t* __restrict__ packed) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= slots) return;
+    const int64_t tile = idx >> 6;
+    const int lane = (int)(idx & 63);
+    const int64_t nt = tile / KT, kt = tile % KT;
+    const int r = lane & 15, g = lane >> 4;
+    const uint4 src = *reinterpret_cast<const uint4*>(q + (nt * kTileN + r) * K + kt * kTileK + g * 16);
+    const uint32_t flip = 0x80808080u;
+    const uint4 dst{src.x ^ flip, src.y ^ flip, src.z ^ flip, src.w ^ flip};
+    *reinterpret_cast<uint4*>(packed + idx * 16) = dst;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV on the VALU for small M (x rows in registers, v_dot2_f32_f16).
+// ---------------------------------------------------------------------------
+template <int M, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* __restrict__ x, int64_t xs,
+                                                               const uint8_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ scale,
+                                                               const uint16_t* __restrict__ bias,
+                                                               uint16_t* __restrict__ y, int64_t ys, int KT) {
+    const int nt = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 4, r = lane & 15;
+    const uint4* wp = reinterpret_cast<const uint4*>(w) + (int64_t)nt * KT * 64 + lane;
+    const _Float16* xh = reinterpret_cast<const _Float16*>(x) + g * 16;
+
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+
+    for (int kt0 = wave; kt0 < KT; kt0 += WAVES * U) {
+        uint4 wr[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kt0 + u * WAVES;
+            if (kt < KT) wr[u] = wp[(int64_t)kt * 64];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kt0 + u * WAVES;
+            if (kt < KT) {
+                const half8v w0 = dequant8(wr[u].x, wr[u].y);
+                const half8v w1 = dequant8(wr[u].z, wr[u].w);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const _Float16* xp = xh + m * xs + kt * kTileK;
+                    acc[m] = dot8(load_half8(xp), w0, acc[m]);
+                    acc[m] = dot8(load_half8(xp + 8), w1, acc[m]);
+                }
+            }
+        }
+    }
+    // Lanes r, r+16, r+32, r+48 hold the four 16-column slices of row r.
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        acc[m] += __shfl_xor(acc[m], 16);
+        acc[m] += __shfl_xor(acc[m], 32);
+    }
+    __shared__ float red[WAVES][M][kTileN];
+    if (g == 0) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) red[wave][m][r] = acc[m];
+    }
+    __syncthreads();
+    if (threadIdx.x < M * kTileN) {
+        const int m = threadIdx.x / kTileN, rr = threadIdx.x % kTileN;
+        float s = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < WAVES; ++wv) s += red[wv][m][rr];
+        const int64_t n = (int64_t)nt * kTileN + rr;
+        float v = s * h2f(scale, n);
+        if (bias) v += h2f(bias, n);
+        y[m * ys + n] = f2h_bits(v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM on MFMA (v_mfma_f32_16x16x32_f16): A = x rows (16 per m-tile, zero
+// padded past M), B = dequantized weight tile (16 output channels), C =
+// y^T slice. Lane l feeds A row l%16 / B column l%16 with the 8 k-values
+// 16*(l/16) + 8*j + [0, 8) of the tile for MFMA j in {0, 1}; A and B use the
+// same k-assignment, so any k order the instruction applies is consistent.
+// C element i of lane l is row 4*(l/16) + i, column l%16.
+// ---------------------------------------------------------------------------
+template <int MT, int NPW, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
+                                                               const uint8_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ scale,
+                                                               const uint16_t* __restrict__ bias,
+                                                               uint16_t* __restrict__ y, int64_t ys, int KT) {
+    const int nt0 = blockIdx.x * NPW;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 4, r = lane & 15;
+    const uint4* wp = reinterpret_cast<const uint4*>(w) + (int64_t)nt0 * KT * 64 + lane;
+    const _Float16* xh = reinterpret_cast<const _Float16*>(x) + g * 16;
+
+    float4v acc[NPW][MT];
+#pragma unroll
+    for (int p = 0; p < NPW; ++p)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[p][mt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int kt0 = wave; kt0 < KT; kt0 += WAVES * U) {
+        uint4 wr[U][NPW];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kt0 + u * WAVES;
+            if (kt < KT) {
+#pragma unroll
+                for (int p = 0; p < NPW; ++p) wr[u][p] = wp[((int64_t)p * KT + kt) * 64];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kt0 + u * WAVES;
+            if (kt < KT) {
+                half8v xa[MT][2];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int m = mt * 16 + r;
+                    if (m < M) {
+                        const _Float16* xp = xh + (int64_t)m * xs + kt * kTileK;
+                        xa[mt][0] = load_half8(xp);
+                        xa[mt][1] = load_half8(xp + 8);
+                    } else {
+                        xa[mt][0] = (_Float16)0.0f;
+                        xa[mt][1] = (_Float16)0.0f;
+                    }
+                }
+#pragma unroll
+                for (int p = 0; p < NPW; ++p) {
+                    const half8v b0 = dequant8(wr[u][p].x, wr[u][p].y);
+                    const half8v b1 = dequant8(wr[u][p].z, wr[u][p].w);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][0], b0, acc[p][mt], 0, 0, 0);
+                        acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][1], b1, acc[p][mt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+
+    __shared__ float red[WAVES][NPW][MT][16][kTileN];
+#pragma unroll
+    for (int p = 0; p < NPW; ++p)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][p][mt][4 * g + i][r] = acc[p][mt][i];
+    __syncthreads();
+    constexpr int kOut = NPW * MT * 16 * kTileN;
+    for (int idx = threadIdx.x; idx < kOut; idx += WAVES * 64) {
+        const int p = idx / (MT * 256);
+        const int rem = idx % (MT * 256);
+        const int mt = rem / 256;
+        const int mm = (rem % 256) / kTileN;
+        const int rr = rem % kTileN;
+        const int m = mt * 16 + mm;
+        if (m >= M) continue;
+        float s = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < WAVES; ++wv) s += red[wv][p][mt][mm][rr];
+        const int64_t n = (int64_t)(nt0 + p) * kTileN + rr;
+        float v = s * h2f(scale, n);
+        if (bias) v += h2f(bias, n);
+        y[(int64_t)m * ys + n] = f2h_bits(v);
+    }
+}
+
+// Largest M handled by the VALU GEMV; above it the MFMA kernel runs.
+constexpr int kValuMaxM = 4;
+constexpr int kGemvWaves = 8;
+constexpr int kGemvUnroll = 8;
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaUnroll = 4;
+
+template <int M>
+static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const uint16_t* s, const uint16_t* b,
+                        uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
+    hipLaunchKernelGGL((gemv_valu_kernel<M, kGemvWaves, kGemvUnroll>), dim3(NT), dim3(kGemvWaves * 64), 0, st, x, xs,
+                       w, s, b, y, ys, KT);
+}
+
+template <int MT, int NPW>
+static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
+                        uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, kMfmaWaves, kMfmaUnroll>), dim3(NT / NPW), dim3(kMfmaWaves * 64), 0,
+                       st, x, xs, M, w, s, b, y, ys, KT);
+}
+
+template <int MT>
+static void launch_mfma_npw(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
+                            const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
+    // More n-tiles per workgroup reuse each x fragment more often; keep enough
+    // workgroups to cover the chip.
+    if (MT == 2 && NT % 2 == 0 && NT / 2 >= 256) {
+        launch_mfma<MT, 2>(x, xs, M, w, s, b, y, ys, NT, KT, st);
+    } else {
+        launch_mfma<MT, 1>(x, xs, M, w, s, b, y, ys, NT, KT, st);
+    }
+}
+
+}  // namespace w8a16
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_w8a16_quantize(const float* w, int64_t N, int64_t K, int8_t* q, uint16_t* scale, void* stream) {
+    if (!w || !q || !scale) return fail(MX_ERR_NULL, "mx_w8a16_quantize: null pointer");
+    if (N <= 0 || K <= 0) return fail(MX_ERR_INVALID, "mx_w8a16_quantize: N and K must be positive (N=%lld K=%lld)",
+                                      (long long)N, (long long)K);
+    if (N > 0x7fffffff) return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_quantize: N too large");
+    hipLaunchKernelGGL(w8a16::quantize_kernel, dim3((unsigned)N), dim3(256), 0, as_stream(stream), w, K, q, scale);
+    return check_launch("mx_w8a16_quantize");
+}
+
+extern "C" int mx_w8a16_pack(const int8_t* q, int64_t N, int64_t K, uint8_t* packed, void* stream) {
+    if (!q || !packed) return fail(MX_ERR_NULL, "mx_w8a16_pack: null pointer");
+    if (N <= 0 || K <= 0 || N % w8a16::kTileN || K % w8a16::kTileK)
+        return fail(MX_ERR_INVALID, "mx_w8a16_pack: need N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)",
+                    (long long)N, (long long)K);
+    if (!aligned(q, 16) || !aligned(packed, 16)) return fail(MX_ERR_ALIGNMENT, "mx_w8a16_pack: 16-byte alignment");
+    const int64_t slots = N * K / 16;
+    const int64_t blocks = ceil_div(slots, 256);
+    if (blocks > 0x7fffffff) return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_pack: matrix too large");
+    hipLaunchKernelGGL(w8a16::pack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), q, K,
+                       K / w8a16::kTileK, slots, packed);
+    return check_launch("mx_w8a16_pack");
+}
+
+extern "C" size_t mx_w8a16_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
+
+extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
+                               const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t N, int64_t y_stride,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    if (!x || !packed || !scale || !y) return fail(MX_ERR_NULL, "mx_w8a16_linear: null pointer");
+    if (M < 0 || N <= 0 || K <= 0) return fail(MX_ERR_INVALID, "mx_w8a16_linear: bad sizes M=%lld N=%lld K=%lld",
+                                               (long long)M, (long long)N, (long long)K);
+    if (N % w8a16::kTileN || K % w8a16::kTileK)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear: need N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)",
+                    (long long)N, (long long)K);
+    if (x_stride < K || y_stride < N)
+        return fail(MX_ERR_INVALID, "mx_w8a16_linear: row strides must cover K and N");
+    if (!aligned(x, 16) || (x_stride % 8) != 0 || !aligned(packed, 16))
+        return fail(MX_ERR_ALIGNMENT, "mx_w8a16_linear: x rows and packed weights must be 16-byte aligned");
+    if (N / w8a16::kTileN > 0x7fffffff || K / w8a16::kTileK > 0x7fffffff)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear: matrix too large");
+    if (M == 0) return MX_OK;
+    const int NT = (int)(N / w8a16::kTileN);
+    const int KT = (int)(K / w8a16::kTileK);
+    hipStream_t st = as_stream(stream);
+    for (int64_t m0 = 0; m0 < M; m0 += 64) {
+        const int mc = (int)((M - m0) < 64 ? (M - m0) : 64);
+        const uint16_t* xc = x + m0 * x_stride;
+        uint16_t* yc = y + m0 * y_stride;
+        if (mc <= w8a16::kValuMaxM) {
+            switch (mc) {
+                case 1: w8a16::launch_gemv<1>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+                case 2: w8a16::launch_gemv<2>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+                case 3: w8a16::launch_gemv<3>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+                default: w8a16::launch_gemv<4>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+            }
+        } else {
+            switch ((mc + 15) / 16) {
+                case 1: w8a16::launch_mfma_npw<1>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+                case 2: w8a16::launch_mfma_npw<2>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+                case 3: w8a16::launch_mfma_npw<3>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+                default: w8a16::launch_mfma_npw<4>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+            }
+        }
+        const int rc = check_launch("mx_w8a16_linear");
+        if (rc != MX_OK) return rc;
+    }
+    return MX_OK;
+}

@@ -1,0 +1,163 @@
+"""Weight-only int8 linear (W8A16) for the quantized-linear slot.
+
+The reference fills this slot with autoawq's int4 ``WQLinear``:
+``PHASE2_QUANT=int4`` (``runtime/phase2/worker_server.py:126-128``) loads
+``AutoAWQForCausalLM.from_quantized(...)`` (``:194-205``), whose modules keep
+the ``nn.Linear`` contract ``y[..., N] = x[..., K] W^T (+ b)`` inside every HF
+decoder layer. This module keeps that contract with a build-defined int8
+format (per-output-channel symmetric absmax, fp16 scales; see the C ABI in
+``include/mxdecode.h``) and runs the HIP kernels of libmxdecode:
+``mx_w8a16_quantize`` + ``mx_w8a16_pack`` at load, ``mx_w8a16_linear`` per call.
+
+``quantize_model_`` is the ``PHASE2_QUANT=int8`` counterpart of the reference's
+AWQ load: it swaps the decoder-layer projections of an HF model in place.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import _hip
+
+TILE_N = 16
+TILE_K = 64
+
+DEFAULT_TARGETS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def quantize_weight(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantize ``weight [N, K]`` on the device: returns ``(q int8 [N, K], scale fp16 [N])``.
+
+    Bit-exact with the CPU restatement of the format. Raises ValueError on
+    non-finite weights (one host sync; this runs at model load).
+    """
+    _hip.require_device_tensor(weight, "weight")
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be 2-D [N, K], got {tuple(weight.shape)}")
+    n, k = weight.shape
+    w = weight.detach().to(torch.float32).contiguous()
+    q = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    s = torch.empty((n,), dtype=torch.float16, device=w.device)
+    lib = _hip.load()
+    with torch.cuda.device(w.device):
+        _hip.check(
+            lib.mx_w8a16_quantize(w.data_ptr(), n, k, q.data_ptr(), s.data_ptr(), _hip.stream_handle(w.device)),
+            "mx_w8a16_quantize",
+        )
+    if bool(torch.isnan(s).any()):
+        raise ValueError("weight contains non-finite values")
+    return q, s
+
+
+def pack_weight(q: torch.Tensor) -> torch.Tensor:
+    """Pack ``q int8 [N, K]`` into the kernels' 1 KiB tile layout (uint8 ``[N*K]``)."""
+    _hip.require_device_tensor(q, "q")
+    if q.dtype != torch.int8 or q.dim() != 2:
+        raise ValueError("q must be a 2-D int8 tensor")
+    n, k = q.shape
+    if n % TILE_N or k % TILE_K:
+        raise ValueError(f"int8 linear needs out_features % {TILE_N} == 0 and in_features % {TILE_K} == 0, got {n}x{k}")
+    q = q.contiguous()
+    packed = torch.empty((n * k,), dtype=torch.uint8, device=q.device)
+    lib = _hip.load()
+    with torch.cuda.device(q.device):
+        _hip.check(lib.mx_w8a16_pack(q.data_ptr(), n, k, packed.data_ptr(), _hip.stream_handle(q.device)),
+                   "mx_w8a16_pack")
+    return packed
+
+
+def int8_linear(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+                out_features: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``y = x @ (q * s)^T + b`` for fp16 ``x [..., K]`` -> fp16 ``[..., N]``."""
+    _hip.require_device_tensor(x, "x")
+    if x.dtype != torch.float16:
+        raise ValueError(f"int8 linear expects fp16 activations, got {x.dtype}")
+    k = int(x.shape[-1])
+    n = int(out_features)
+    if packed.numel() != n * k:
+        raise ValueError(f"packed weight has {packed.numel()} bytes, expected {n}x{k}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    m = int(x2.shape[0])
+    if out is None:
+        y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    else:
+        y = out.view(m, n)
+    if m == 0:
+        return y.view(*lead, n)
+    lib = _hip.load()
+    _hip.check(
+        lib.mx_w8a16_linear(
+            x2.data_ptr(), m, k, x2.stride(0), packed.data_ptr(), scale.data_ptr(),
+            bias.data_ptr() if bias is not None else None, y.data_ptr(), n, y.stride(0),
+            None, 0, _hip.stream_handle(x.device),
+        ),
+        "mx_w8a16_linear",
+    )
+    return y.view(*lead, n)
+
+
+class Int8Linear(nn.Module):
+    """Drop-in for ``nn.Linear`` on the decode path with int8 weights and fp16 scales."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True,
+                 device: torch.device | str | None = None) -> None:
+        super().__init__()
+        if out_features % TILE_N or in_features % TILE_K:
+            raise ValueError(
+                f"Int8Linear needs out_features % {TILE_N} == 0 and in_features % {TILE_K} == 0, "
+                f"got {out_features}x{in_features}"
+            )
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self.register_buffer("packed_weight", torch.zeros(out_features * in_features, dtype=torch.uint8, device=device))
+        self.register_buffer("weight_scale", torch.ones(out_features, dtype=torch.float16, device=device))
+        if bias:
+            self.register_buffer("bias", torch.zeros(out_features, dtype=torch.float16, device=device))
+        else:
+            self.bias = None
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, device: torch.device | str | None = None) -> "Int8Linear":
+        dev = torch.device(device) if device is not None else linear.weight.device
+        if dev.type != "cuda":
+            raise ValueError("Int8Linear.from_linear quantizes on a ROCm device; pass device='cuda'")
+        mod = cls(linear.in_features, linear.out_features, bias=linear.bias is not None, device=dev)
+        q, s = quantize_weight(linear.weight.detach().to(dev))
+        mod.packed_weight.copy_(pack_weight(q))
+        mod.weight_scale.copy_(s)
+        if linear.bias is not None:
+            mod.bias.copy_(linear.bias.detach().to(dev, torch.float16))
+        return mod
+
+    @classmethod
+    def from_quantized(cls, q: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None) -> "Int8Linear":
+        n, k = q.shape
+        mod = cls(k, n, bias=bias is not None, device=q.device)
+        mod.packed_weight.copy_(pack_weight(q))
+        mod.weight_scale.copy_(scale.to(torch.float16))
+        if bias is not None:
+            mod.bias.copy_(bias.to(torch.float16))
+        return mod
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return int8_linear(x, self.packed_weight, self.weight_scale, self.bias, self.out_features)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, bias={self.bias is not None}, int8"
+
+
+def quantize_model_(model: nn.Module, targets: tuple[str, ...] = DEFAULT_TARGETS, include_lm_head: bool = False,
+                    device: torch.device | str | None = None) -> nn.Module:
+    """Replace the named ``nn.Linear`` projections of ``model`` with :class:`Int8Linear` in place."""
+    replace: list[tuple[nn.Module, str, nn.Linear]] = []
+    for parent in model.modules():
+        for name, child in parent.named_children():
+            if isinstance(child, nn.Linear) and (name in targets or (include_lm_head and name == "lm_head")):
+                replace.append((parent, name, child))
+    for parent, name, child in replace:
+        setattr(parent, name, Int8Linear.from_linear(child, device=device))
+    return model

@@ -1,0 +1,227 @@
+"""Block-paged KV storage read by the HIP paged-attention decode kernel.
+
+Keeps the reference's ``GpuKVBlockPool`` API (``runtime/phase2/paged_kv_kernel.py:24-315``)
+and its storage layout, which the kernel reads in place:
+
+* K and V are ``[num_blocks, num_layers, num_kv_heads, block_size, head_dim]``
+  (``:101-107``); ``k_layer_view(l)`` is ``pool[:, l]`` ->
+  ``[num_blocks, Hkv, bs, D]`` with strides ``(L*Hkv*bs*D, bs*D, D, 1)``
+  (``:124-134``), so every (block, layer, kv-head) is one contiguous
+  ``bs*D`` run (4 KiB at bs=16, D=128, fp16);
+* token ``pos`` of a row is stored in block ``table[pos // bs]`` at offset
+  ``pos % bs`` (``:163-174``, ``:217-227``).
+
+MI355X-first difference: the reference grows its slabs lazily 8 blocks at a time
+and copies the whole slab on every growth (``:86-115``). Here the first use
+allocates all ``num_blocks`` at once (288 GB of HBM per GPU makes that the
+cheap choice), so tensor addresses never change after ``_ensure_pools`` and a
+captured HIP graph stays valid. Block usage accounting
+(``allocated_block_count`` / ``peak_allocated_block_count``) is unchanged.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class PoolShape:
+    num_blocks: int
+    block_size_tokens: int
+    num_layers: int
+    num_kv_heads: int
+    head_dim: int
+
+
+class GpuKVBlockPool:
+    """Shared block pool; same constructor and methods as the reference's."""
+
+    def __init__(self, *, num_blocks: int, block_size_tokens: int, num_layers: int, num_kv_heads: int, head_dim: int,
+                 dtype: torch.dtype, device: str | torch.device) -> None:
+        if num_blocks <= 0 or block_size_tokens <= 0:
+            raise ValueError("num_blocks and block_size_tokens must be positive")
+        self.shape = PoolShape(num_blocks=num_blocks, block_size_tokens=block_size_tokens, num_layers=num_layers,
+                               num_kv_heads=num_kv_heads, head_dim=head_dim)
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self._block_shape = (num_layers, num_kv_heads, block_size_tokens, head_dim)
+        self._k_pool: torch.Tensor | None = None
+        self._v_pool: torch.Tensor | None = None
+        self._used_blocks: set[int] = set()
+        self._peak_allocated_blocks = 0
+
+    @property
+    def block_size_tokens(self) -> int:
+        return self.shape.block_size_tokens
+
+    def allocated_block_count(self) -> int:
+        return len(self._used_blocks)
+
+    def peak_allocated_block_count(self) -> int:
+        return self._peak_allocated_blocks
+
+    def bytes_per_block(self) -> int:
+        s = self.shape
+        elems = s.num_layers * s.num_kv_heads * s.block_size_tokens * s.head_dim * 2
+        return elems * torch.empty((), dtype=self.dtype).element_size()
+
+    def bytes_for_blocks(self, block_count: int) -> int:
+        return block_count * self.bytes_per_block()
+
+    def peak_allocated_bytes(self) -> int:
+        return self.bytes_for_blocks(self._peak_allocated_blocks)
+
+    def _ensure_pools(self) -> None:
+        if self._k_pool is not None:
+            return
+        s = self.shape
+        shape = (s.num_blocks, s.num_layers, s.num_kv_heads, s.block_size_tokens, s.head_dim)
+        self._k_pool = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        self._v_pool = torch.zeros(shape, dtype=self.dtype, device=self.device)
+
+    def _touch_block(self, physical: int) -> None:
+        if physical < 0 or physical >= self.shape.num_blocks:
+            raise IndexError(f"physical block id out of range: {physical}")
+        self._used_blocks.add(physical)
+        self._peak_allocated_blocks = max(self._peak_allocated_blocks, len(self._used_blocks))
+
+    def _touch_blocks(self, physical_ids: torch.Tensor) -> None:
+        for physical in physical_ids.unique().tolist():
+            self._touch_block(int(physical))
+
+    def k_layer_view(self, layer_idx: int) -> torch.Tensor:
+        """Per-layer K blocks: ``[num_blocks, num_kv_heads, block_size, head_dim]``."""
+        self._ensure_pools()
+        assert self._k_pool is not None
+        return self._k_pool[:, layer_idx]
+
+    def v_layer_view(self, layer_idx: int) -> torch.Tensor:
+        """Per-layer V blocks: ``[num_blocks, num_kv_heads, block_size, head_dim]``."""
+        self._ensure_pools()
+        assert self._v_pool is not None
+        return self._v_pool[:, layer_idx]
+
+    def write_tokens(self, layer_idx: int, block_ids: list[int], start_pos: int, key_states: torch.Tensor,
+                     value_states: torch.Tensor) -> None:
+        """Write K/V for positions ``[start_pos, start_pos + kv_len)`` of one row (``:136-174``)."""
+        if key_states.dim() == 3:
+            key_states = key_states.unsqueeze(0)
+            value_states = value_states.unsqueeze(0)
+        if key_states.shape[0] != 1:
+            raise ValueError("write_tokens takes a single row; use write_tokens_batch")
+        kv_len = int(key_states.shape[-2])
+        block_size = self.block_size_tokens
+        n_logical = math.ceil((start_pos + kv_len) / block_size)
+        if n_logical > len(block_ids):
+            raise IndexError(f"block table underrun at pos={start_pos + kv_len - 1}: need block {n_logical - 1}, "
+                             f"have {len(block_ids)}")
+        table = torch.tensor([list(block_ids)], device=self.device, dtype=torch.int32)
+        starts = torch.tensor([start_pos], device=self.device, dtype=torch.int64)
+        self.write_tokens_batch(layer_idx, table, starts, key_states, value_states)
+
+    def write_tokens_batch(self, layer_idx: int, block_tables: torch.Tensor, start_positions: torch.Tensor,
+                           key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        """Vectorised KV write: tables ``[B, max_blocks]``, starts ``[B]``, states ``[B, Hkv, kv_len, D]``.
+
+        Same semantics as the reference (``:176-227``), written as one indexed
+        store per call instead of a per-token loop. Outside graph capture the
+        block table bounds are checked on the host as in the reference
+        (``:221-222``).
+        """
+        if key_states.shape != value_states.shape:
+            raise ValueError("key_states and value_states must match shape")
+        batch_size = int(key_states.shape[0])
+        kv_len = int(key_states.shape[-2])
+        if block_tables.shape[0] != batch_size or start_positions.shape[0] != batch_size:
+            raise ValueError("batch dimension mismatch in write_tokens_batch")
+        self._ensure_pools()
+        assert self._k_pool is not None and self._v_pool is not None
+        device = self.device
+        capturing = bool(device.type == "cuda" and torch.cuda.is_available() and torch.cuda.is_current_stream_capturing())
+        bs = self.block_size_tokens
+        tables = block_tables.to(device=device, dtype=torch.int64)
+        pos = start_positions.to(device=device, dtype=torch.int64).view(-1, 1) + torch.arange(
+            kv_len, device=device, dtype=torch.int64).view(1, -1)  # [B, T]
+        logical = torch.div(pos, bs, rounding_mode="floor")
+        if not capturing:
+            if kv_len > 0 and int(logical.max().item()) >= tables.shape[1]:
+                raise IndexError("block table underrun during batched write")
+        physical = torch.gather(tables, 1, logical)  # [B, T]
+        offset = pos % bs
+        if not capturing:
+            if int(physical.min().item()) < 0 or int(physical.max().item()) >= self.shape.num_blocks:
+                raise IndexError("physical block id out of range during batched write")
+            self._touch_blocks(physical)
+        # pool[physical, layer, :, offset, :] = states[b, :, t, :]
+        k_src = key_states.to(self.dtype).permute(0, 2, 1, 3).reshape(-1, key_states.shape[1], key_states.shape[3])
+        v_src = value_states.to(self.dtype).permute(0, 2, 1, 3).reshape(-1, value_states.shape[1], value_states.shape[3])
+        k_layer = self._k_pool[:, layer_idx]
+        v_layer = self._v_pool[:, layer_idx]
+        k_layer[physical.reshape(-1), :, offset.reshape(-1), :] = k_src
+        v_layer[physical.reshape(-1), :, offset.reshape(-1), :] = v_src
+
+    def copy_blocks(self, src_block_ids: list[int], dst_block_ids: list[int]) -> None:
+        """Copy full physical blocks (all layers) from src ids to dst ids (``:233-250``)."""
+        if len(src_block_ids) != len(dst_block_ids):
+            raise ValueError(f"copy_blocks length mismatch: src={len(src_block_ids)} dst={len(dst_block_ids)}")
+        if not src_block_ids:
+            return
+        self._ensure_pools()
+        assert self._k_pool is not None and self._v_pool is not None
+        pairs = [(int(s), int(d)) for s, d in zip(src_block_ids, dst_block_ids) if int(s) != int(d)]
+        for s, d in pairs:
+            self._touch_block(s)
+            self._touch_block(d)
+        if not pairs:
+            return
+        src = torch.tensor([s for s, _ in pairs], device=self.device, dtype=torch.long)
+        dst = torch.tensor([d for _, d in pairs], device=self.device, dtype=torch.long)
+        self._k_pool[dst] = self._k_pool[src]
+        self._v_pool[dst] = self._v_pool[src]
+
+    def gather_layer(self, layer_idx: int, block_ids: list[int], seq_len: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Gather one row as ``[1, Hkv, seq_len, D]`` (prefill / parity, ``:252-283``)."""
+        if seq_len <= 0:
+            raise ValueError("seq_len must be positive")
+        bs = self.block_size_tokens
+        n_logical = math.ceil(seq_len / bs)
+        if n_logical > len(block_ids):
+            raise IndexError("block table underrun during gather")
+        self._ensure_pools()
+        assert self._k_pool is not None and self._v_pool is not None
+        ids_list = [int(b) for b in list(block_ids)[:n_logical]]
+        for b in ids_list:
+            self._touch_block(b)
+        ids = torch.tensor(ids_list, device=self.device, dtype=torch.long)
+        s = self.shape
+        k = self._k_pool[ids, layer_idx].permute(1, 0, 2, 3).reshape(s.num_kv_heads, n_logical * bs, s.head_dim)
+        v = self._v_pool[ids, layer_idx].permute(1, 0, 2, 3).reshape(s.num_kv_heads, n_logical * bs, s.head_dim)
+        return k[:, :seq_len].unsqueeze(0), v[:, :seq_len].unsqueeze(0)
+
+    def gather_layer_batch(self, layer_idx: int, block_tables: torch.Tensor, seq_lens: torch.Tensor
+                           ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Gather rows as zero-padded ``[B, Hkv, max_seq, D]`` (batched prefill, ``:285-309``)."""
+        batch_size = int(block_tables.shape[0])
+        lens = [int(x) for x in seq_lens.tolist()]
+        max_seq = max(lens) if lens else 0
+        if max_seq <= 0:
+            raise ValueError("seq_len must be positive")
+        s = self.shape
+        keys = torch.zeros(batch_size, s.num_kv_heads, max_seq, s.head_dim, device=self.device, dtype=self.dtype)
+        values = torch.zeros_like(keys)
+        for b in range(batch_size):
+            n_logical = math.ceil(lens[b] / self.block_size_tokens)
+            row_ids = [int(x) for x in block_tables[b, :n_logical].tolist()]
+            k, v = self.gather_layer(layer_idx, row_ids, lens[b])
+            keys[b, :, : lens[b]] = k[0]
+            values[b, :, : lens[b]] = v[0]
+        return keys, values
+
+    def reset(self) -> None:
+        self._k_pool = None
+        self._v_pool = None
+        self._used_blocks.clear()
+        self._peak_allocated_blocks = 0

@@ -1,0 +1,25 @@
+"""CPU oracle for the decode-step hot path.
+
+TEST INFRASTRUCTURE ONLY. Nothing in the product package imports this
+package. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import, call or link anything here, and only as the
+checker or as the timed CPU baseline, never as the thing measured or shipped.
+
+Modules:
+
+* ``int8_quant``      - weight-only int8 format: per-output-channel symmetric
+                        absmax quantizer, tile pack/unpack, dequant linear
+                        (numpy; bit-exact integer/byte work).
+* ``int8_quant.c``    - an independent C restatement of the same quantizer and
+                        pack, built by ``oracle/Makefile`` and cross-checked
+                        against the numpy one.
+* ``paged_attention`` - paged decode attention: SDPA on gathered K/V, the
+                        block-loop online softmax, and the fp32 per-row target
+                        (torch fp32 on the CPU).
+* ``kv_pool``         - the paged KV pool layout and its write/gather
+                        (torch on the CPU).
+* ``model``           - a small fp32 decoder-step oracle used by the greedy
+                        decode tests.
+
+Parity status of each function is stated in its module header.
+"""

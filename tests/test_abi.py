@@ -1,0 +1,104 @@
+"""CPU checks of the C ABI: the library loads, exports what the header declares,
+and rejects bad arguments with status codes before touching the device."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from runtime_amd.phase2 import _hip
+from runtime_amd.phase2.int8_linear import Int8Linear, int8_linear
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "mxdecode.h")
+
+
+def _declared() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mx_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _hip.load()
+    names = _declared()
+    assert "mx_paged_attn_decode" in names and "mx_w8a16_linear" in names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_hip.SIGNATURES), "ctypes prototypes must mirror the header"
+    assert lib.mx_abi_version() == _hip.ABI_VERSION
+
+
+def test_paged_attn_workspace_layout_is_host_computable():
+    lib = _hip.load()
+    small = lib.mx_paged_attn_workspace_bytes(4, 8, 2, 64, 8, 16, 0)
+    big = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 0)
+    assert 0 < small < big
+    assert big >= 32 * 8 * (4096 // 256) * 4 * 128 * 4  # fp32 partial accumulators
+    assert lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 512) < big
+    assert lib.mx_paged_attn_error_offset(4, 8, 2, 64, 8, 16, 0) % 256 == 0
+    assert lib.mx_w8a16_workspace_bytes(32, 4096, 4096) == 0
+
+
+def _status(rc: int, expected: int) -> None:
+    assert rc == expected, (rc, _hip.load().mx_last_error())
+    assert _hip.load().mx_last_error().decode()
+
+
+def test_invalid_arguments_return_status_codes():
+    lib = _hip.load()
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    _status(lib.mx_w8a16_linear(None, 1, 64, 64, fake, fake, None, fake, 16, 16, None, 0, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_w8a16_linear(fake, 1, 60, 64, fake, fake, None, fake, 16, 16, None, 0, None),
+            _hip.MX_ERR_UNSUPPORTED)
+    _status(lib.mx_w8a16_linear(fake, 1, 64, 32, fake, fake, None, fake, 16, 16, None, 0, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_w8a16_linear(ctypes.c_void_p(4098), 1, 64, 64, fake, fake, None, fake, 16, 16, None, 0, None),
+            _hip.MX_ERR_ALIGNMENT)
+    _status(lib.mx_w8a16_pack(fake, 15, 64, fake, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_w8a16_quantize(None, 4, 4, fake, fake, None), _hip.MX_ERR_NULL)
+    args = dict(q=fake, q_sb=256, q_sh=64, k=fake, v=fake, kv_sblk=2048, kv_shead=1024, bt=fake, bt_sb=4, mb=4,
+                sl=fake, B=1, Hq=8, Hkv=2, D=64, bs=16, npool=8, scale=0.125, out=fake, o_sb=512, o_sh=64,
+                ws=None, wsb=0, ct=0, st=None)
+
+    def call(**over):
+        a = dict(args, **over)
+        return lib.mx_paged_attn_decode(a["q"], a["q_sb"], a["q_sh"], a["k"], a["v"], a["kv_sblk"], a["kv_shead"],
+                                        a["bt"], a["bt_sb"], a["mb"], a["sl"], a["B"], a["Hq"], a["Hkv"], a["D"],
+                                        a["bs"], a["npool"], a["scale"], a["out"], a["o_sb"], a["o_sh"], a["ws"],
+                                        a["wsb"], a["ct"], a["st"])
+
+    assert call(B=0) == _hip.MX_OK
+    _status(call(q=None), _hip.MX_ERR_NULL)
+    _status(call(Hq=7), _hip.MX_ERR_INVALID)
+    _status(call(Hq=36, Hkv=2), _hip.MX_ERR_UNSUPPORTED)  # G = 18
+    _status(call(D=96), _hip.MX_ERR_UNSUPPORTED)
+    _status(call(bs=8), _hip.MX_ERR_UNSUPPORTED)
+    _status(call(ct=40), _hip.MX_ERR_INVALID)
+    _status(call(), _hip.MX_ERR_WORKSPACE)
+    _status(call(q_sh=60), _hip.MX_ERR_ALIGNMENT)
+    with pytest.raises(ValueError):
+        _hip.check(_hip.MX_ERR_INVALID, "probe")
+    with pytest.raises(RuntimeError):
+        _hip.check(_hip.MX_ERR_LAUNCH, "probe")
+
+
+def test_python_wrappers_refuse_cpu_tensors():
+    """No CPU fallback: host tensors are rejected before any launch."""
+    from runtime_amd.phase2.paged_attention_hip import PagedDecodeBatchMetadata, paged_attention_decode_batched
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    with pytest.raises(ValueError):
+        int8_linear(torch.zeros(1, 64, dtype=torch.float16), torch.zeros(1024, dtype=torch.uint8),
+                    torch.ones(16, dtype=torch.float16), None, 16)
+    pool = GpuKVBlockPool(num_blocks=2, block_size_tokens=16, num_layers=1, num_kv_heads=1, head_dim=64,
+                          dtype=torch.float16, device="cpu")
+    meta = PagedDecodeBatchMetadata(pool=pool, layer_idx=0, block_tables=torch.zeros(1, 1, dtype=torch.int32),
+                                    seq_lens=torch.ones(1, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        paged_attention_decode_batched(torch.zeros(1, 2, 1, 64, dtype=torch.float16), meta, 2, 0.125)
+    with pytest.raises(ValueError):
+        Int8Linear(100, 64)
+    with pytest.raises(ValueError):
+        Int8Linear.from_linear(torch.nn.Linear(64, 16), device="cpu")

@@ -1,0 +1,143 @@
+"""GPU parity of the int8 quantize / pack / linear kernels against the CPU oracle.
+
+Bar: quantize and pack bit-exact; fp16 linear outputs within atol 1e-2 and
+rtol 1e-2 of the fp32-accumulated oracle (oracle/int8_quant.py).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import int8_quant
+from runtime_amd.phase2.int8_linear import Int8Linear, int8_linear, pack_weight, quantize_model_, quantize_weight
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+ATOL = 1e-2
+RTOL = 1e-2
+
+
+def _cuda(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _quantized(seed: int, n: int, k: int, scale: float = 0.02):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n, k, generator=g) * scale).numpy().astype(np.float32)
+    q, s = int8_quant.quantize_per_channel(w)
+    return q, s
+
+
+def test_quantize_and_pack_bit_exact_on_edge_rows():
+    d = np.load(os.path.join(GOLDEN, "int8_edge.npz"))
+    q, s = quantize_weight(_cuda(d["w"]))
+    assert np.array_equal(q.cpu().numpy(), d["q"])
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), d["s"].view(np.uint16))
+    assert np.array_equal(pack_weight(q).cpu().numpy(), d["packed"])
+
+
+def test_quantize_rejects_non_finite():
+    w = torch.zeros(16, 64, device="cuda")
+    w[3, 5] = float("inf")
+    with pytest.raises(ValueError):
+        quantize_weight(w)
+
+
+def test_quantize_and_pack_bit_exact_config1():
+    doc = json.load(open(os.path.join(GOLDEN, "int8_config1.json")))
+    g = torch.Generator().manual_seed(0)
+    torch.randn(1, 4096, generator=g)
+    w = torch.randn(4096, 4096, generator=g) * 0.02
+    q, s = quantize_weight(w.cuda())
+    qn, sn = q.cpu().numpy(), s.cpu().numpy()
+    assert hashlib.sha256(qn.tobytes()).hexdigest() == doc["q_sha256"]
+    assert hashlib.sha256(sn.tobytes()).hexdigest() == doc["s_sha256"]
+    assert hashlib.sha256(pack_weight(q).cpu().numpy().tobytes()).hexdigest() == doc["packed_sha256"]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 48, 64, 65, 100])
+def test_linear_matches_oracle_across_batch(m):
+    n, k = 256, 512
+    q, s = _quantized(100 + m, n, k)
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float16)
+    want = int8_quant.linear_ref_fp32(x, q, s, bias)
+    got = int8_linear(_cuda(x), pack_weight(_cuda(q)), _cuda(s), _cuda(bias), n).float().cpu().numpy()
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+def test_linear_edge_fixture_and_no_bias():
+    d = np.load(os.path.join(GOLDEN, "int8_edge.npz"))
+    packed = _cuda(d["packed"])
+    got = int8_linear(_cuda(d["x"]), packed, _cuda(d["s"]), _cuda(d["bias"]), 48).float().cpu().numpy()
+    np.testing.assert_allclose(got, d["y"], atol=ATOL, rtol=RTOL)
+    got_nb = int8_linear(_cuda(d["x"]), packed, _cuda(d["s"]), None, 48).float().cpu().numpy()
+    np.testing.assert_allclose(got_nb, int8_quant.linear_ref_fp32(d["x"], d["q"], d["s"]), atol=ATOL, rtol=RTOL)
+
+
+def test_linear_config1_golden():
+    doc = json.load(open(os.path.join(GOLDEN, "int8_config1.json")))
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 4096, generator=g).to(torch.float16)
+    w = torch.randn(4096, 4096, generator=g) * 0.02
+    lin = torch.nn.Linear(4096, 4096, bias=False)
+    lin.weight.data.copy_(w)
+    mod = Int8Linear.from_linear(lin, device="cuda")
+    y = mod(x.cuda()).float().cpu().numpy()
+    np.testing.assert_allclose(y[0, :16], doc["y_head"], atol=ATOL, rtol=RTOL)
+    q, s = int8_quant.quantize_per_channel(w.numpy())
+    np.testing.assert_allclose(y, int8_quant.linear_ref_fp32(x.numpy(), q, s), atol=ATOL, rtol=RTOL)
+
+
+LLAMA_SHAPES = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 28672), ("down", 14336, 4096)]
+
+
+@pytest.mark.parametrize("name,k,n", LLAMA_SHAPES)
+def test_linear_llama_shapes(name, k, n):
+    idx = [s[0] for s in LLAMA_SHAPES].index(name)
+    q, s = _quantized(1000 + idx, n, k)
+    packed, sd = pack_weight(_cuda(q)), _cuda(s)
+    for m in (1, 8, 32, 64):
+        x = np.random.default_rng(m + idx).standard_normal((m, k)).astype(np.float16)
+        got = int8_linear(_cuda(x), packed, sd, None, n).float().cpu().numpy()
+        np.testing.assert_allclose(got, int8_quant.linear_ref_fp32(x, q, s), atol=ATOL, rtol=RTOL,
+                                   err_msg=f"{name} M={m}")
+
+
+def test_linear_strided_rows_and_preallocated_out():
+    n, k, m = 128, 256, 6
+    q, s = _quantized(7, n, k)
+    big = torch.randn(m, k + 64, dtype=torch.float16, device="cuda")
+    x = big[:, 32:32 + k]  # row stride k + 64, 16-byte aligned start
+    out_big = torch.zeros(m, n + 16, dtype=torch.float16, device="cuda")
+    got = int8_linear(x, pack_weight(_cuda(q)), _cuda(s), None, n)
+    want = int8_quant.linear_ref_fp32(x.cpu().numpy(), q, s)
+    np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+    y3 = int8_linear(x.reshape(2, 3, k), pack_weight(_cuda(q)), _cuda(s), None, n)
+    assert y3.shape == (2, 3, n)
+    assert torch.equal(y3.reshape(m, n), got)
+    int8_linear(x, pack_weight(_cuda(q)), _cuda(s), None, n, out=out_big[:, :n])  # row stride n + 16
+    assert torch.equal(out_big[:, :n], got)
+    assert out_big[:, n:].abs().sum().item() == 0
+
+
+def test_quantize_model_swaps_linears():
+    model = torch.nn.Sequential()
+    model.add_module("q_proj", torch.nn.Linear(128, 64, bias=True))
+    model.add_module("other", torch.nn.Linear(128, 64))
+    w = model.q_proj.weight.detach().numpy().copy()
+    b = model.q_proj.bias.detach().numpy().astype(np.float16)
+    quantize_model_(model, device="cuda")
+    assert isinstance(model.q_proj, Int8Linear) and isinstance(model.other, torch.nn.Linear)
+    x = np.random.default_rng(3).standard_normal((3, 128)).astype(np.float16)
+    y = model.q_proj(_cuda(x))
+    assert y.shape == (3, 64) and y.dtype == torch.float16
+    q, s = int8_quant.quantize_per_channel(w)
+    np.testing.assert_allclose(y.float().cpu().numpy(), int8_quant.linear_ref_fp32(x, q, s, b), atol=ATOL, rtol=RTOL)

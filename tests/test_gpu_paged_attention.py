@@ -1,0 +1,261 @@
+"""GPU parity of the HIP paged-attention decode kernel against the CPU oracle.
+
+Bar: fp16 outputs within atol 1e-2 and rtol 1e-2 of the fp32 per-row oracle
+(oracle/paged_attention.py: decode_rows_fp32), on the reference's own test
+shapes (tests/test_paged_attention_kernel_parity.py:103-198 of the reference),
+the full config-2 shape, and the edge cases (ragged, zero-length, clamped,
+GQA 1..8, D 64/128, block size 16/32, split chunk sizes).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_attention as oracle_pa
+from runtime_amd.phase2 import _hip
+from runtime_amd.phase2.block_paged_attention import block_paged_attention_forward
+from runtime_amd.phase2.paged_attention_hip import (
+    PagedDecodeBatchMetadata,
+    paged_attention_decode,
+    paged_attention_decode_batched,
+    reset_paged_decode_batch_metadata,
+    set_paged_decode_batch_metadata,
+    workspace_error_flag,
+)
+from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+pytestmark = pytest.mark.gpu
+ATOL = 1e-2
+RTOL = 1e-2
+
+
+def oracle_out(q, k_layer, v_layer, tables, seq_lens, scale, grp):
+    """Copy only the referenced blocks to the host and run the fp32 per-row oracle."""
+    lens = [int(s) for s in torch.as_tensor(seq_lens).cpu().tolist()]
+    t_cpu = tables.cpu()
+    bs = k_layer.shape[2]
+    max_blocks = t_cpu.shape[1]
+    ids = sorted({int(x) for b, s in enumerate(lens) if s > 0
+                  for x in t_cpu[b, :min(math.ceil(s / bs), max_blocks)].tolist()})
+    if not ids:
+        ids = [0]
+    remap = {old: i for i, old in enumerate(ids)}
+    idx = torch.tensor(ids, device=k_layer.device, dtype=torch.long)
+    kc = k_layer.index_select(0, idx).cpu()
+    vc = v_layer.index_select(0, idx).cpu()
+    t2 = torch.zeros_like(t_cpu)
+    for b, s in enumerate(lens):
+        for j in range(min(math.ceil(max(s, 0) / bs), max_blocks)):
+            t2[b, j] = remap[int(t_cpu[b, j])]
+    return oracle_pa.decode_rows_fp32(q.cpu(), kc, vc, t2, lens, scale, grp)
+
+
+def _check(got, want, msg=""):
+    np.testing.assert_allclose(got.float().cpu().numpy(), want.numpy(), atol=ATOL, rtol=RTOL, err_msg=msg)
+
+
+def _random_case(seed, bsz, hkv, grp, d, bs, seq_lens, num_blocks=None, pad_value=0):
+    g = torch.Generator().manual_seed(seed)
+    nblk = [math.ceil(max(s, 0) / bs) for s in seq_lens]
+    max_blocks = max(max(nblk), 1)
+    num_blocks = num_blocks or (sum(nblk) + 3)
+    perm = torch.randperm(num_blocks, generator=g)
+    tables = torch.full((bsz, max_blocks), pad_value, dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(nblk):
+        tables[b, :n] = perm[used:used + n].to(torch.int32)
+        used += n
+    k = torch.randn(num_blocks, hkv, bs, d, generator=g).to(torch.float16).cuda()
+    v = torch.randn(num_blocks, hkv, bs, d, generator=g).to(torch.float16).cuda()
+    q = torch.randn(bsz, hkv * grp, 1, d, generator=g).to(torch.float16).cuda()
+    return q, k, v, tables.cuda(), torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
+
+
+class _Pool:
+    """Minimal pool stand-in exposing the views the decode entry point reads."""
+
+    def __init__(self, k, v):
+        self.k, self.v = k, v
+
+    def _ensure_pools(self):
+        pass
+
+    def k_layer_view(self, layer):
+        return self.k
+
+    def v_layer_view(self, layer):
+        return self.v
+
+
+def _decode(q, k, v, tables, lens, scale, grp):
+    meta = PagedDecodeBatchMetadata(pool=_Pool(k, v), layer_idx=0, block_tables=tables, seq_lens=lens)
+    return paged_attention_decode_batched(q, meta, grp, scale)
+
+
+@pytest.mark.parametrize("seq_len", [128, 768])
+def test_reference_single_row_cases(seq_len):
+    """tests/test_paged_attention_kernel_parity.py:103-125 and :187-198 (Hkv=2, G=4, D=64, bs=16)."""
+    hkv, grp, d, bs = 2, 4, 64, 16
+    num_blocks = math.ceil(seq_len / bs) + 1
+    pool = GpuKVBlockPool(num_blocks=num_blocks, block_size_tokens=bs, num_layers=1, num_kv_heads=hkv, head_dim=d,
+                          dtype=torch.float16, device="cuda")
+    ids = list(range(num_blocks))
+    torch.manual_seed(42)
+    k = torch.randn(1, hkv, seq_len, d, device="cuda", dtype=torch.float16)
+    v = torch.randn(1, hkv, seq_len, d, device="cuda", dtype=torch.float16)
+    pool.write_tokens(0, ids, 0, k, v)
+    query = torch.randn(1, hkv * grp, 1, d, device="cuda", dtype=torch.float16)
+    scale = d**-0.5
+    got = paged_attention_decode(query=query, pool=pool, layer_idx=0, block_ids=ids, seq_len=seq_len,
+                                 num_kv_groups=grp, scaling=scale)
+    keys, values = pool.gather_layer(0, ids, seq_len)
+    want = oracle_pa.reference_sdpa_attention(query.cpu().float(), keys.cpu().float(), values.cpu().float(), scale,
+                                              grp)
+    assert (got.float().cpu() - want).abs().max().item() < 1e-2
+    table = torch.tensor(ids, dtype=torch.int32, device="cuda").view(1, -1)
+    _check(got, oracle_out(query, pool.k_layer_view(0), pool.v_layer_view(0), table, [seq_len], scale, grp))
+
+
+def test_reference_batched_ragged():
+    """tests/test_paged_attention_kernel_parity.py:127-185: B=4, seq_lens 7/15/31/63, seed 99."""
+    hkv, grp, d, bs, bsz = 2, 4, 64, 16, 4
+    seq_lens = [7, 15, 31, 63]
+    num_blocks = math.ceil(max(seq_lens) / bs) + 2
+    pool = GpuKVBlockPool(num_blocks=num_blocks * bsz, block_size_tokens=bs, num_layers=1, num_kv_heads=hkv,
+                          head_dim=d, dtype=torch.float16, device="cuda")
+    torch.manual_seed(99)
+    scale = d**-0.5
+    tables = torch.zeros(bsz, num_blocks, device="cuda", dtype=torch.int32)
+    for b in range(bsz):
+        ids = list(range(b * num_blocks, (b + 1) * num_blocks))
+        nlog = math.ceil(seq_lens[b] / bs)
+        tables[b, :nlog] = torch.tensor(ids[:nlog], device="cuda", dtype=torch.int32)
+        k = torch.randn(1, hkv, seq_lens[b], d, device="cuda", dtype=torch.float16)
+        v = torch.randn(1, hkv, seq_lens[b], d, device="cuda", dtype=torch.float16)
+        pool.write_tokens(0, ids, 0, k, v)
+    query = torch.randn(bsz, hkv * grp, 1, d, device="cuda", dtype=torch.float16)
+    meta = PagedDecodeBatchMetadata(pool=pool, layer_idx=0, block_tables=tables,
+                                    seq_lens=torch.tensor(seq_lens, device="cuda", dtype=torch.int32))
+    got = paged_attention_decode_batched(query, meta, grp, scale)
+    _check(got, oracle_out(query, pool.k_layer_view(0), pool.v_layer_view(0), tables, seq_lens, scale, grp))
+
+
+def _config2(seed=0):
+    """B=32, Hq=32, Hkv=8, D=128, bs=16, ctx ~ U[128, 4096], one randperm(16384) pool."""
+    g = torch.Generator().manual_seed(seed)
+    bsz, hkv, grp, d, bs, nb = 32, 8, 4, 128, 16, 16384
+    lens = torch.randint(128, 4097, (bsz,), generator=g)
+    perm = torch.randperm(nb, generator=g)
+    max_blocks = 4096 // bs
+    tables = torch.zeros(bsz, max_blocks, dtype=torch.int32)
+    used = 0
+    for b in range(bsz):
+        n = math.ceil(int(lens[b]) / bs)
+        tables[b, :n] = perm[used:used + n].to(torch.int32)
+        used += n
+    gd = torch.Generator(device="cuda").manual_seed(seed)
+    k = torch.randn(nb, hkv, bs, d, generator=gd, device="cuda", dtype=torch.float16)
+    v = torch.randn(nb, hkv, bs, d, generator=gd, device="cuda", dtype=torch.float16)
+    q = torch.randn(bsz, hkv * grp, 1, d, generator=gd, device="cuda", dtype=torch.float16)
+    return q, k, v, tables.cuda(), lens.to(torch.int32).cuda(), grp, d**-0.5
+
+
+def test_config2_full_shape_and_repeatability():
+    q, k, v, tables, lens, grp, scale = _config2()
+    got = _decode(q, k, v, tables, lens, scale, grp)
+    again = _decode(q, k, v, tables, lens, scale, grp)
+    assert torch.equal(got, again), "decode must be deterministic and leave its workspace reusable"
+    _check(got, oracle_out(q, k, v, tables, lens, scale, grp))
+    assert workspace_error_flag() == 0
+
+
+def _abi_decode(q, k, v, tables, lens, scale, grp, chunk_tokens, num_pool_blocks=None):
+    lib = _hip.load()
+    bsz, hq, _, d = q.shape
+    nb, hkv, bs, _ = k.shape
+    mb = tables.shape[1]
+    nbytes = lib.mx_paged_attn_workspace_bytes(bsz, hq, hkv, d, mb, bs, chunk_tokens)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    _hip.check(lib.mx_paged_attn_decode(
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+        tables.data_ptr(), tables.stride(0), mb, lens.data_ptr(), bsz, hq, hkv, d, bs,
+        num_pool_blocks if num_pool_blocks is not None else nb, scale, out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), nbytes, chunk_tokens, _hip.stream_handle(q.device)), "decode")
+    torch.cuda.synchronize()
+    err = int(ws[lib.mx_paged_attn_error_offset(bsz, hq, hkv, d, mb, bs, chunk_tokens):][:4].view(torch.int32).item())
+    return out, err
+
+
+def test_split_chunk_size_invariance():
+    q, k, v, tables, lens, grp, scale = _random_case(3, 6, 2, 4, 128, 16, [1, 16, 17, 255, 1000, 2049])
+    want = oracle_out(q, k, v, tables, lens, scale, grp)
+    outs = []
+    for ct in (16, 64, 256, 1024, 4096):
+        out, err = _abi_decode(q, k, v, tables, lens, scale, grp, ct)
+        assert err == 0
+        _check(out, want, f"chunk_tokens={ct}")
+        outs.append(out.float())
+    for o in outs[1:]:
+        assert (o - outs[0]).abs().max().item() < 2e-3
+
+
+@pytest.mark.parametrize("hkv,grp,d,bs", [(2, 7, 64, 16), (4, 1, 128, 16), (2, 8, 128, 16), (3, 2, 64, 32),
+                                          (8, 4, 128, 32), (1, 3, 64, 16), (2, 5, 128, 16), (1, 6, 64, 16)])
+def test_gqa_dims_and_block_sizes(hkv, grp, d, bs):
+    lens = [1, 15, 16, 17, 300, 1000]
+    q, k, v, tables, sl = _random_case(11 + grp + d + bs, len(lens), hkv, grp, d, bs, lens)
+    scale = d**-0.5
+    _check(_decode(q, k, v, tables, sl, scale, grp), oracle_out(q, k, v, tables, sl, scale, grp))
+
+
+def test_zero_length_rows_and_table_clamp():
+    lens = [0, 40, 0, 100]
+    q, k, v, tables, sl = _random_case(21, 4, 2, 4, 64, 16, lens)
+    out = _decode(q, k, v, tables, sl, 0.125, 4)
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2]) == 0
+    _check(out, oracle_out(q, k, v, tables, sl, 0.125, 4))
+    # seq_len beyond the table width: only max_blocks blocks are read.
+    narrow = tables[:, :2].contiguous()
+    clamp = _decode(q, k, v, narrow, sl, 0.125, 4)
+    _check(clamp, oracle_out(q, k, v, narrow, sl, 0.125, 4))
+
+
+def test_padding_entries_and_unused_blocks_never_read():
+    lens = [5, 33, 130]
+    q, k, v, tables, sl = _random_case(31, 3, 2, 4, 128, 16, lens, num_blocks=40, pad_value=-7)
+    base = oracle_out(q, k, v, tables.clamp(min=0), sl, 0.0883, 4)
+    used = set()
+    for b, s in enumerate(lens):
+        used.update(tables[b, :math.ceil(s / 16)].tolist())
+    k2, v2 = k.clone(), v.clone()
+    for blk in range(k.shape[0]):
+        if blk not in used:
+            k2[blk] = float("nan")
+            v2[blk] = float("nan")
+    out, err = _abi_decode(q, k2, v2, tables, sl, 0.0883, 4, 0)
+    assert err == 0
+    assert torch.isfinite(out.float()).all()
+    _check(out, base)
+
+
+def test_hook_contract():
+    lens = [9, 70]
+    q, k, v, tables, sl = _random_case(41, 2, 2, 4, 64, 16, lens)
+
+    class Mod:
+        num_key_value_groups = 4
+        training = False
+
+    meta = PagedDecodeBatchMetadata(pool=_Pool(k, v), layer_idx=0, block_tables=tables, seq_lens=sl)
+    tok = set_paged_decode_batch_metadata(meta)
+    try:
+        out, weights = block_paged_attention_forward(Mod(), q, None, None, None, 0.125)
+    finally:
+        reset_paged_decode_batch_metadata(tok)
+    assert weights is None and out.shape == (2, 1, 8, 64)
+    _check(out.transpose(1, 2), oracle_out(q, k, v, tables, sl, 0.125, 4))
