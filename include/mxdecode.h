@@ -97,12 +97,16 @@ int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, c
  *      a zero output row
  * out: fp16 [B, Hq, D] with strides (o_sb, o_sh, 1)
  * num_pool_blocks: block ids outside [0, num_pool_blocks) are skipped and
- *      recorded in the workspace error word (mx_paged_attn_read_error)
- * chunk_tokens: split-K chunk (multiple of 16); 0 picks the default. Must be
- *      the value the workspace was sized for, or larger.
+ *      recorded in the workspace error word (see mx_paged_attn_error_offset)
+ * chunk_tokens: split-K chunk (multiple of 16, at most 4096); 0 picks one
+ *      from B, Hkv and max_blocks (256..2048 tokens, about one workgroup per
+ *      CU). Must be the value the workspace was sized for.
+ *      Rows longer than one chunk are merged by a second, small kernel on
+ *      the same stream. At most 1024 chunks per row (max_blocks*block_size).
  * Supported: D in {64, 128}; block_size in {16, 32}; Hq = G * Hkv, G in 1..8.
- * The workspace must be zero-filled once when allocated; calls leave it
- * ready for the next call. Concurrent calls must not share a workspace.
+ * The workspace holds fp32 split partials and the error word; zero it once at
+ * allocation so the error word starts clear. Concurrent calls must not share
+ * a workspace.
  * ------------------------------------------------------------------------- */
 size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                      int32_t block_size, int32_t chunk_tokens);

@@ -43,4 +43,38 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Cross-lane butterflies on gfx950 row swaps. v_permlane16_swap_b32 exchanges
+// the odd 16-lane rows of its first operand with the even rows of its second;
+// v_permlane32_swap_b32 exchanges the upper 32 lanes of the first with the
+// lower 32 of the second. Started from two copies of v, a symmetric op of the
+// two outputs gives op(v[l], v[l^16]) / op(v[l], v[l^32]) in every lane. They
+// are issued as inline asm with two distinct read-write operands: with one
+// shared input value the compiler folds the builtin's second result into the
+// first. The s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void row_swap16(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void row_swap32(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+// Sum / max over lanes l, l^16, l^32, l^48 (all lanes get the result).
+__device__ __forceinline__ float xor_sum_16_32(float v) {
+    float a = v, b = v;
+    row_swap16(a, b);
+    float c = a + b, d = a + b;
+    row_swap32(c, d);
+    return c + d;
+}
+__device__ __forceinline__ float xor_max_16_32(float v) {
+    float a = v, b = v;
+    row_swap16(a, b);
+    float c = fmaxf(a, b), d = fmaxf(a, b);
+    row_swap32(c, d);
+    return fmaxf(c, d);
+}
+// v + v[l^8] inside each 16-lane row (DPP row_ror:8).
+__device__ __forceinline__ float xor8_sum(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+}
+
 }  // namespace mx

@@ -120,52 +120,106 @@ __global__ __launch_bounds__(256) void pack_kernel(const int8_t* __restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
-// GEMV on the VALU for small M (x rows in registers, v_dot2_f32_f16).
+// Per-wave software pipeline. A wave owns the k-tiles kt = wave + j*WAVES,
+// j < nj, of the workgroup's n-tiles. Stage s of P holds the weight tiles and
+// the x fragments of one k-tile; the loads for k-tile j+P are issued as soon
+// as k-tile j has been consumed, so P k-tiles (P*NPW KiB of weights plus their
+// x fragments) stay in flight per wave.
+//
+// Every load is issued unconditionally: past the last k-tile the index is
+// clamped (the reload hits L2), and x rows past M read row M-1 (MFMA rows are
+// independent, those C rows are discarded). With no loads under a branch the
+// compiler can wait for exactly the oldest stage (s_waitcnt vmcnt(N)) instead
+// of draining every load in flight. Addresses are a wave-uniform base plus a
+// fixed 32-bit lane offset.
 // ---------------------------------------------------------------------------
-template <int M, int WAVES, int U>
+// Workgroups start their k-sweep at different k-tiles so that concurrently
+// running workgroups read different x lines (the activation rows are shared
+// by every workgroup and would otherwise all hit the same L2 lines at once).
+__device__ __forceinline__ int kt_rotation(int block, int KT) { return (int)(((int64_t)block * 5) % KT); }
+__device__ __forceinline__ int rotate_kt(int pos, int rot, int KT) {
+    const int kt = pos + rot;
+    return kt >= KT ? kt - KT : kt;
+}
+
+// The stage loop shared by both kernels. Prologue: stages 0..P-1 (indices
+// clamped when nj < P). Full rounds issue the loads of tile j+P right after
+// tile j is consumed, unconditionally. The last round and a half issue only
+// the loads still in range, then drain.
+#define PIPELINE_BODY(P, nj, st, load, COMPUTE)                  \
+    _Pragma("unroll") for (int s = 0; s < P; ++s) load(s, st[s]); \
+    int j0 = 0;                                                     \
+    for (; j0 + 2 * P <= nj; j0 += P) {                             \
+        _Pragma("unroll") for (int s = 0; s < P; ++s) {             \
+            COMPUTE;                                                \
+            load(j0 + s + P, st[s]);                                \
+        }                                                           \
+    }                                                               \
+    _Pragma("unroll") for (int s = 0; s < P; ++s) {                 \
+        if (j0 + s < nj) {                                          \
+            COMPUTE;                                                \
+            if (j0 + s + P < nj) load(j0 + s + P, st[s]);           \
+        }                                                           \
+    }                                                               \
+    _Pragma("unroll") for (int s = 0; s < P; ++s) {                 \
+        if (j0 + P + s < nj) { COMPUTE; }                           \
+    }
+
+template <int NPW, int XV>
+struct Stage {
+    uint4 w[NPW];
+    half8v x[XV];
+};
+
+// GEMV on the VALU for small M (v_dot2_f32_f16 against exact fp16 weights).
+template <int M, int WAVES, int P>
 __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* __restrict__ x, int64_t xs,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
                                                                const uint16_t* __restrict__ bias,
                                                                uint16_t* __restrict__ y, int64_t ys, int KT) {
     const int nt = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int g = lane >> 4, r = lane & 15;
-    const uint4* wp = reinterpret_cast<const uint4*>(w) + (int64_t)nt * KT * 64 + lane;
-    const _Float16* xh = reinterpret_cast<const _Float16*>(x) + g * 16;
+    const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt * KT * 64;
+    const _Float16* xbase = reinterpret_cast<const _Float16*>(x);
+    const int nj = wave < KT ? (KT - wave + WAVES - 1) / WAVES : 0;
+    const int rot = kt_rotation(blockIdx.x, KT);
+    int xoff[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) xoff[m] = (int)(m * xs) + g * 16;
+
+    auto load = [&](int j, Stage<1, 2 * M>& st) {
+        const int kt = rotate_kt(wave + (j < nj ? j : nj - 1) * WAVES, rot, KT);
+        st.w[0] = (wbase + (int64_t)kt * 64)[lane];
+        const _Float16* xk = xbase + kt * kTileK;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            st.x[2 * m] = load_half8(xk + xoff[m]);
+            st.x[2 * m + 1] = load_half8(xk + xoff[m] + 8);
+        }
+    };
+    auto compute = [&](const Stage<1, 2 * M>& st, float (&acc)[M]) {
+        const half8v w0 = dequant8(st.w[0].x, st.w[0].y);
+        const half8v w1 = dequant8(st.w[0].z, st.w[0].w);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            acc[m] = dot8(st.x[2 * m], w0, acc[m]);
+            acc[m] = dot8(st.x[2 * m + 1], w1, acc[m]);
+        }
+    };
 
     float acc[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
-
-    for (int kt0 = wave; kt0 < KT; kt0 += WAVES * U) {
-        uint4 wr[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int kt = kt0 + u * WAVES;
-            if (kt < KT) wr[u] = wp[(int64_t)kt * 64];
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int kt = kt0 + u * WAVES;
-            if (kt < KT) {
-                const half8v w0 = dequant8(wr[u].x, wr[u].y);
-                const half8v w1 = dequant8(wr[u].z, wr[u].w);
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const _Float16* xp = xh + m * xs + kt * kTileK;
-                    acc[m] = dot8(load_half8(xp), w0, acc[m]);
-                    acc[m] = dot8(load_half8(xp + 8), w1, acc[m]);
-                }
-            }
-        }
+    if (nj > 0) {
+        Stage<1, 2 * M> st[P];
+        PIPELINE_BODY(P, nj, st, load, compute(st[s], acc))
     }
     // Lanes r, r+16, r+32, r+48 hold the four 16-column slices of row r.
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        acc[m] += __shfl_xor(acc[m], 16);
-        acc[m] += __shfl_xor(acc[m], 32);
-    }
+    for (int m = 0; m < M; ++m) acc[m] = xor_sum_16_32(acc[m]);
     __shared__ float red[WAVES][M][kTileN];
     if (g == 0) {
 #pragma unroll
@@ -185,70 +239,66 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 }
 
 // ---------------------------------------------------------------------------
-// GEMM on MFMA (v_mfma_f32_16x16x32_f16): A = x rows (16 per m-tile, zero
-// padded past M), B = dequantized weight tile (16 output channels), C =
-// y^T slice. Lane l feeds A row l%16 / B column l%16 with the 8 k-values
-// 16*(l/16) + 8*j + [0, 8) of the tile for MFMA j in {0, 1}; A and B use the
-// same k-assignment, so any k order the instruction applies is consistent.
-// C element i of lane l is row 4*(l/16) + i, column l%16.
+// GEMM on MFMA (v_mfma_f32_16x16x32_f16): A = x rows (16 per m-tile), B =
+// dequantized weight tile (16 output channels), C = y^T slice. Lane l feeds A
+// row l%16 / B column l%16 with the 8 k-values 16*(l/16) + 8*j + [0, 8) of the
+// tile for MFMA j in {0, 1}; A and B use the same k-assignment, so any k order
+// the instruction applies is consistent. C element i of lane l is row
+// 4*(l/16) + i, column l%16.
 // ---------------------------------------------------------------------------
-template <int MT, int NPW, int WAVES, int U>
+template <int MT, int NPW, int WAVES, int P>
 __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
                                                                const uint16_t* __restrict__ bias,
                                                                uint16_t* __restrict__ y, int64_t ys, int KT) {
     const int nt0 = blockIdx.x * NPW;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int g = lane >> 4, r = lane & 15;
-    const uint4* wp = reinterpret_cast<const uint4*>(w) + (int64_t)nt0 * KT * 64 + lane;
-    const _Float16* xh = reinterpret_cast<const _Float16*>(x) + g * 16;
+    const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt0 * KT * 64;
+    const _Float16* xbase = reinterpret_cast<const _Float16*>(x);
+    const int nj = wave < KT ? (KT - wave + WAVES - 1) / WAVES : 0;
+    const int rot = kt_rotation(blockIdx.x, KT);
+    int xoff[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = (mt * 16 + r) < M ? (mt * 16 + r) : (M - 1);
+        xoff[mt] = (int)(m * xs) + g * 16;
+    }
+
+    auto load = [&](int j, Stage<NPW, 2 * MT>& st) {
+        const int kt = rotate_kt(wave + (j < nj ? j : nj - 1) * WAVES, rot, KT);
+#pragma unroll
+        for (int p = 0; p < NPW; ++p) st.w[p] = (wbase + ((int64_t)p * KT + kt) * 64)[lane];
+        const _Float16* xk = xbase + kt * kTileK;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            st.x[2 * mt] = load_half8(xk + xoff[mt]);
+            st.x[2 * mt + 1] = load_half8(xk + xoff[mt] + 8);
+        }
+    };
 
     float4v acc[NPW][MT];
 #pragma unroll
     for (int p = 0; p < NPW; ++p)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[p][mt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (int kt0 = wave; kt0 < KT; kt0 += WAVES * U) {
-        uint4 wr[U][NPW];
+    auto compute = [&](const Stage<NPW, 2 * MT>& st) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int kt = kt0 + u * WAVES;
-            if (kt < KT) {
+        for (int p = 0; p < NPW; ++p) {
+            const half8v b0 = dequant8(st.w[p].x, st.w[p].y);
+            const half8v b1 = dequant8(st.w[p].z, st.w[p].w);
 #pragma unroll
-                for (int p = 0; p < NPW; ++p) wr[u][p] = wp[((int64_t)p * KT + kt) * 64];
+            for (int mt = 0; mt < MT; ++mt) {
+                acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[2 * mt], b0, acc[p][mt], 0, 0, 0);
+                acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[2 * mt + 1], b1, acc[p][mt], 0, 0, 0);
             }
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int kt = kt0 + u * WAVES;
-            if (kt < KT) {
-                half8v xa[MT][2];
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const int m = mt * 16 + r;
-                    if (m < M) {
-                        const _Float16* xp = xh + (int64_t)m * xs + kt * kTileK;
-                        xa[mt][0] = load_half8(xp);
-                        xa[mt][1] = load_half8(xp + 8);
-                    } else {
-                        xa[mt][0] = (_Float16)0.0f;
-                        xa[mt][1] = (_Float16)0.0f;
-                    }
-                }
-#pragma unroll
-                for (int p = 0; p < NPW; ++p) {
-                    const half8v b0 = dequant8(wr[u][p].x, wr[u][p].y);
-                    const half8v b1 = dequant8(wr[u][p].z, wr[u][p].w);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][0], b0, acc[p][mt], 0, 0, 0);
-                        acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][1], b1, acc[p][mt], 0, 0, 0);
-                    }
-                }
-            }
-        }
+    };
+    if (nj > 0) {
+        Stage<NPW, 2 * MT> st[P];
+        PIPELINE_BODY(P, nj, st, load, compute(st[s]))
     }
 
     __shared__ float red[WAVES][NPW][MT][16][kTileN];
@@ -281,30 +331,35 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
 // Largest M handled by the VALU GEMV; above it the MFMA kernel runs.
 constexpr int kValuMaxM = 4;
 constexpr int kGemvWaves = 8;
-constexpr int kGemvUnroll = 8;
 constexpr int kMfmaWaves = 8;
-constexpr int kMfmaUnroll = 4;
+
+// Pipeline depth from the VGPRs one stage costs (4 per 1 KiB weight tile, 8
+// per x row fragment of 32 bytes), within a budget that leaves room for the
+// accumulators below the 256 VGPRs a 512-thread workgroup allows per wave.
+constexpr int clamp_depth(int d) { return d < 2 ? 2 : (d > 8 ? 8 : d); }
+constexpr int gemv_depth(int M) { return clamp_depth(160 / (4 + 8 * M)); }
+constexpr int mfma_depth(int MT, int NPW) { return clamp_depth(160 / (4 * NPW + 8 * MT)); }
 
 template <int M>
 static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_valu_kernel<M, kGemvWaves, kGemvUnroll>), dim3(NT), dim3(kGemvWaves * 64), 0, st, x, xs,
-                       w, s, b, y, ys, KT);
+    hipLaunchKernelGGL((gemv_valu_kernel<M, kGemvWaves, gemv_depth(M)>), dim3(NT), dim3(kGemvWaves * 64), 0, st, x,
+                       xs, w, s, b, y, ys, KT);
 }
 
 template <int MT, int NPW>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, kMfmaWaves, kMfmaUnroll>), dim3(NT / NPW), dim3(kMfmaWaves * 64), 0,
-                       st, x, xs, M, w, s, b, y, ys, KT);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, kMfmaWaves, mfma_depth(MT, NPW)>), dim3(NT / NPW),
+                       dim3(kMfmaWaves * 64), 0, st, x, xs, M, w, s, b, y, ys, KT);
 }
 
 template <int MT>
 static void launch_mfma_npw(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
                             const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
-    // More n-tiles per workgroup reuse each x fragment more often; keep enough
-    // workgroups to cover the chip.
-    if (MT == 2 && NT % 2 == 0 && NT / 2 >= 256) {
+    // Two n-tiles per workgroup share each x fragment; keep at least one
+    // workgroup per CU.
+    if (MT <= 2 && NT % 2 == 0 && NT / 2 >= 256) {
         launch_mfma<MT, 2>(x, xs, M, w, s, b, y, ys, NT, KT, st);
     } else {
         launch_mfma<MT, 1>(x, xs, M, w, s, b, y, ys, NT, KT, st);

@@ -82,8 +82,8 @@ def hip_kernel_available() -> bool:
 
 
 # --------------------------------------------------------------------------
-# Workspace: fp32 split partials + per-(row, kv-head) arrival counters. Zeroed
-# once at allocation; the kernel leaves the counters at zero after each call.
+# Workspace: fp32 split partials and the error word, keyed by shape like the
+# reference's scratch caches (:90-115). Zeroed once at allocation.
 # --------------------------------------------------------------------------
 _workspaces: dict[tuple, torch.Tensor] = {}
 _ws_lock = threading.Lock()

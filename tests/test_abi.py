@@ -34,10 +34,15 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_paged_attn_workspace_layout_is_host_computable():
     lib = _hip.load()
     small = lib.mx_paged_attn_workspace_bytes(4, 8, 2, 64, 8, 16, 0)
-    big = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 0)
+    big = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 256)
     assert 0 < small < big
-    assert big >= 32 * 8 * (4096 // 256) * 4 * 128 * 4  # fp32 partial accumulators
+    assert big >= 32 * 8 * (4096 // 256) * 4 * 128 * 4  # fp32 partial accumulators, 16 chunks per row
     assert lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 512) < big
+    # Default chunk: 2048 tokens for B*Hkv = 256 rows of up to 4096 tokens, 256 for a single short row.
+    assert lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 0) == \
+        lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 2048)
+    assert lib.mx_paged_attn_workspace_bytes(1, 8, 2, 64, 8, 16, 0) == \
+        lib.mx_paged_attn_workspace_bytes(1, 8, 2, 64, 8, 16, 256)
     assert lib.mx_paged_attn_error_offset(4, 8, 2, 64, 8, 16, 0) % 256 == 0
     assert lib.mx_w8a16_workspace_bytes(32, 4096, 4096) == 0
 

@@ -77,9 +77,14 @@ def test_linear_edge_fixture_and_no_bias():
     d = np.load(os.path.join(GOLDEN, "int8_edge.npz"))
     packed = _cuda(d["packed"])
     got = int8_linear(_cuda(d["x"]), packed, _cuda(d["s"]), _cuda(d["bias"]), 48).float().cpu().numpy()
-    np.testing.assert_allclose(got, d["y"], atol=ATOL, rtol=RTOL)
+    # Row 35 (scale clamped at 65504) overflows fp16 to +-inf in both the kernel and the fp16-rounded oracle.
+    want16 = int8_quant.linear_ref(d["x"], d["q"], d["s"], d["bias"]).astype(np.float32)
+    assert np.array_equal(np.isinf(got), np.isinf(want16)) and np.isinf(got).any()
+    finite = np.isfinite(want16)
+    np.testing.assert_allclose(got[finite], d["y"][finite], atol=ATOL, rtol=RTOL)
     got_nb = int8_linear(_cuda(d["x"]), packed, _cuda(d["s"]), None, 48).float().cpu().numpy()
-    np.testing.assert_allclose(got_nb, int8_quant.linear_ref_fp32(d["x"], d["q"], d["s"]), atol=ATOL, rtol=RTOL)
+    want_nb = int8_quant.linear_ref(d["x"], d["q"], d["s"]).astype(np.float32)
+    np.testing.assert_allclose(got_nb, want_nb, atol=ATOL, rtol=RTOL)
 
 
 def test_linear_config1_golden():

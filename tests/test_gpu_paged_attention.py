@@ -192,7 +192,8 @@ def _abi_decode(q, k, v, tables, lens, scale, grp, chunk_tokens, num_pool_blocks
 
 
 def test_split_chunk_size_invariance():
-    q, k, v, tables, lens, grp, scale = _random_case(3, 6, 2, 4, 128, 16, [1, 16, 17, 255, 1000, 2049])
+    q, k, v, tables, lens = _random_case(3, 6, 2, 4, 128, 16, [1, 16, 17, 255, 1000, 2049])
+    grp, scale = 4, 128**-0.5
     want = oracle_out(q, k, v, tables, lens, scale, grp)
     outs = []
     for ct in (16, 64, 256, 1024, 4096):
