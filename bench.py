@@ -10,11 +10,13 @@ embeddings are random. Inputs are resident in HBM before timing starts.
 
 Prints ONE JSON line. ``value`` = decode tokens/s of the whole step (B tokens per
 step), timed over ``--steps`` HIP-graph replays of the step after ``--warmup``
-eager steps. ``roofline`` is for the dominant kernel family, from HIP events
-around each of its launches during ``--kernel-steps`` eager steps of the same
-decode (same stream). ``cpu_baseline`` times the CPU oracle on a bounded sample
-(one decoder layer at the same batch and contexts, plus an lm_head slice),
-extrapolated to the full step.
+eager steps. ``roofline`` is for the kernel family with the most time per
+step: each family's launches of one step (same inputs, same stream) are captured
+into their own graph and replayed ``--kernel-steps`` times back-to-back between
+two HIP events, which gives its average launch duration without host launch
+latency inside the interval. ``cpu_baseline`` times the CPU oracle on a bounded
+sample (one decoder layer at the same batch and contexts, plus an lm_head
+slice), extrapolated to the full step.
 """
 
 from __future__ import annotations
@@ -44,7 +46,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--ctx-lo", type=int, default=128)
     ap.add_argument("--ctx-hi", type=int, default=4096)
     ap.add_argument("--pool-blocks", type=int, default=16384)
-    ap.add_argument("--kernel-steps", type=int, default=3)
+    ap.add_argument("--kernel-steps", type=int, default=5, help="graph replays per kernel family for kernel timing")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=1)
@@ -136,6 +138,75 @@ def cpu_baseline(shape, batch: int, lens, layers_total: int) -> dict:
     }
 
 
+def family_launches(model, pool, tables, seq_lens, bsz, dev) -> dict:
+    """Per kernel family: (callable issuing that family's launches of one decode step, launches per call)."""
+    import torch
+
+    from runtime_amd.phase2.int8_linear import int8_linear
+    from runtime_amd.phase2.paged_attention_hip import _decode
+
+    s = model.shape
+    g = torch.Generator(device=dev).manual_seed(3)
+    x_h = torch.randn(bsz, s.hidden, generator=g, device=dev).half()
+    x_i = torch.randn(bsz, s.intermediate, generator=g, device=dev).half()
+    x_a = torch.randn(bsz, s.heads * s.head_dim, generator=g, device=dev).half()
+    q = torch.randn(bsz, s.heads, 1, s.head_dim, generator=g, device=dev).half()
+    lens = (seq_lens + 1).to(torch.int32)
+    out = {}
+
+    def lin(name, x):
+        outs = [torch.empty(bsz, getattr(layer, name)[2], device=dev, dtype=torch.float16) for layer in model.layers]
+
+        def run():
+            for layer, y in zip(model.layers, outs):
+                packed, scale, n, bias = getattr(layer, name)
+                int8_linear(x, packed, scale, bias, n, out=y)
+        return run
+
+    nl = len(model.layers)
+    out["qkv"] = (lin("qkv", x_h), nl)
+    out["o"] = (lin("o", x_a), nl)
+    out["gate_up"] = (lin("gate_up", x_h), nl)
+    out["down"] = (lin("down", x_i), nl)
+
+    def attn():
+        for li in range(len(model.layers)):
+            _decode(q, pool.k_layer_view(li), pool.v_layer_view(li), tables, lens, s.head_dim**-0.5, s.group)
+    out["attn"] = (attn, nl)
+    lm_y = torch.empty(bsz, s.vocab, device=dev, dtype=torch.float16)
+
+    def lm():
+        packed, scale, n, bias = model.lm_head
+        int8_linear(x_h, packed, scale, bias, n, out=lm_y)
+    out["lm_head"] = (lm, 1)
+    return out
+
+
+def time_family(run, launches: int, reps: int) -> float:
+    """Average seconds per launch of one family, from graph replays between HIP events."""
+    import torch
+
+    run()  # eager warm-up (workspaces)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(graph):
+        run()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3 / (reps * launches)
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -214,13 +285,12 @@ def main() -> int:
     ms = start.elapsed_time(end) / args.steps
     lens_after = seq_lens.cpu().tolist()
 
-    # Per-kernel durations: eager steps with HIP events around each launch (same stream).
-    timers: dict = {}
-    for _ in range(args.kernel_steps):
-        nxt = model.step(tokens, pool, tables_d, seq_lens, timers=timers)
-        tokens.copy_(nxt)
-    torch.cuda.synchronize()
-    kdur = {k: [a.elapsed_time(b) * 1e-3 for a, b in v] for k, v in timers.items()}
+    # Per-kernel durations. Each family's launches of one step (e.g. the 32 paged
+    # decode calls, one per layer, on the same inputs the step uses) are captured
+    # into their own graph and replayed back-to-back between two HIP events on
+    # the current stream, so host launch latency never lands inside the interval.
+    kdur = {name: time_family(run, launches, args.kernel_steps)
+            for name, (run, launches) in family_launches(model, pool, tables_d, seq_lens, bsz, dev).items()}
 
     # Algorithmic bytes.
     lin = model.linear_bytes(bsz)
@@ -229,14 +299,16 @@ def main() -> int:
     append_b = 2 * bsz * shape.kv_heads * shape.head_dim * 2
     step_bytes = n_layers * (lin["qkv"] + lin["o"] + lin["gate_up"] + lin["down"] + attn_b + append_b) + lin["lm_head"]
     step_bytes += bsz * shape.hidden * 2
-    per_launch = {"attn": attn_b, **lin}
-    fam = {k: (sum(v), len(v)) for k, v in kdur.items()}
-    dominant = max(fam, key=lambda k: fam[k][0])
-    avg = fam[dominant][0] / fam[dominant][1]
+    # The family graphs ran after the timed steps, at contexts lens_after (+1 token).
+    attn_kernel_b = attention_bytes([x + 1 for x in lens_after], shape.kv_heads, shape.head_dim, shape.heads, bs)
+    per_launch = {"attn": attn_kernel_b, **lin}
+    per_step = {k: (n_layers if k != "lm_head" else 1) for k in kdur}
+    dominant = max(kdur, key=lambda k: kdur[k] * per_step[k])
+    avg = kdur[dominant]
     achieved = per_launch[dominant] / avg / 1e9
-    kernels = {k: {"avg_us": round(fam[k][0] / fam[k][1] * 1e6, 2), "launches": fam[k][1],
-                   "bytes_per_launch": per_launch[k],
-                   "gbps": round(per_launch[k] / (fam[k][0] / fam[k][1]) / 1e9, 1)} for k in fam}
+    kernels = {k: {"avg_us": round(kdur[k] * 1e6, 2), "launches_per_step": per_step[k],
+                   "bytes_per_launch": per_launch[k], "gbps": round(per_launch[k] / kdur[k] / 1e9, 1),
+                   "frac": round(per_launch[k] / kdur[k] / 1e9 / HBM_PEAK_GBPS, 4)} for k in kdur}
 
     value = bsz / (ms * 1e-3)
     out = {

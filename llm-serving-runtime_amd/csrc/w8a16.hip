@@ -245,21 +245,32 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 // tile for MFMA j in {0, 1}; A and B use the same k-assignment, so any k order
 // the instruction applies is consistent. C element i of lane l is row
 // 4*(l/16) + i, column l%16.
+//
+// Each x fragment a wave loads (from L2: every workgroup reads all of x) is
+// reused for NPW weight tiles; at M=32 the x bytes a wave loads per weight byte
+// are 4/NPW, and that L2->L1 traffic, not the weight stream, limits the kernel
+// at NPW=1. With NPW=4 a small-N matrix has too few n-blocks to fill the chip,
+// so K is split over gridDim.y workgroups: each writes its scaled fp32 partial
+// to the workspace and reduce_kernel adds the splits and the bias.
 // ---------------------------------------------------------------------------
 template <int MT, int NPW, int WAVES, int P>
 __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
                                                                const uint16_t* __restrict__ bias,
-                                                               uint16_t* __restrict__ y, int64_t ys, int KT) {
+                                                               uint16_t* __restrict__ y, int64_t ys, int KT, int N,
+                                                               float* __restrict__ partial) {
     const int nt0 = blockIdx.x * NPW;
+    const int ks = blockIdx.y, KS = gridDim.y;
+    const int kt_lo = (int)((int64_t)ks * KT / KS);
+    const int KTL = (int)((int64_t)(ks + 1) * KT / KS) - kt_lo;  // k-tiles of this split
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, r = lane & 15;
     const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt0 * KT * 64;
     const _Float16* xbase = reinterpret_cast<const _Float16*>(x);
-    const int nj = wave < KT ? (KT - wave + WAVES - 1) / WAVES : 0;
-    const int rot = kt_rotation(blockIdx.x, KT);
+    const int nj = wave < KTL ? (KTL - wave + WAVES - 1) / WAVES : 0;
+    const int rot = kt_rotation(blockIdx.x, KTL);
     int xoff[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -268,7 +279,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
     }
 
     auto load = [&](int j, Stage<NPW, 2 * MT>& st) {
-        const int kt = rotate_kt(wave + (j < nj ? j : nj - 1) * WAVES, rot, KT);
+        const int kt = kt_lo + rotate_kt(wave + (j < nj ? j : nj - 1) * WAVES, rot, KTL);
 #pragma unroll
         for (int p = 0; p < NPW; ++p) st.w[p] = (wbase + ((int64_t)p * KT + kt) * 64)[lane];
         const _Float16* xk = xbase + kt * kTileK;
@@ -301,13 +312,27 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
         PIPELINE_BODY(P, nj, st, load, compute(st[s]))
     }
 
-    __shared__ float red[WAVES][NPW][MT][16][kTileN];
+    // Cross-wave sum in LDS, in two halves to bound the buffer: the upper half
+    // of the waves stores, the lower half adds its own tile and stores back.
+    constexpr int HW = WAVES / 2;
+    __shared__ float red[HW][NPW][MT][16][kTileN];
+    if (wave >= HW) {
 #pragma unroll
-    for (int p = 0; p < NPW; ++p)
+        for (int p = 0; p < NPW; ++p)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave][p][mt][4 * g + i][r] = acc[p][mt][i];
+                for (int i = 0; i < 4; ++i) red[wave - HW][p][mt][4 * g + i][r] = acc[p][mt][i];
+    }
+    __syncthreads();
+    if (wave < HW) {
+#pragma unroll
+        for (int p = 0; p < NPW; ++p)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave][p][mt][4 * g + i][r] += acc[p][mt][i];
+    }
     __syncthreads();
     constexpr int kOut = NPW * MT * 16 * kTileN;
     for (int idx = threadIdx.x; idx < kOut; idx += WAVES * 64) {
@@ -320,25 +345,85 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
         if (m >= M) continue;
         float s = 0.0f;
 #pragma unroll
-        for (int wv = 0; wv < WAVES; ++wv) s += red[wv][p][mt][mm][rr];
+        for (int wv = 0; wv < HW; ++wv) s += red[wv][p][mt][mm][rr];
         const int64_t n = (int64_t)(nt0 + p) * kTileN + rr;
-        float v = s * h2f(scale, n);
-        if (bias) v += h2f(bias, n);
-        y[(int64_t)m * ys + n] = f2h_bits(v);
+        const float v = s * h2f(scale, n);
+        if (KS == 1) {
+            y[(int64_t)m * ys + n] = f2h_bits(bias ? v + h2f(bias, n) : v);
+        } else {
+            partial[((int64_t)ks * M + m) * N + n] = v;
+        }
     }
+}
+
+// y[m, n] = fp16(sum over splits of partial[ks][m][n] + bias[n]).
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ partial, int KS, int M, int N,
+                                                     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+                                                     int64_t ys) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)M * N) return;
+    const int m = (int)(idx / N), n = (int)(idx % N);
+    float v = bias ? h2f(bias, n) : 0.0f;
+    for (int k = 0; k < KS; ++k) v += partial[(int64_t)k * M * N + idx];
+    y[(int64_t)m * ys + n] = f2h_bits(v);
 }
 
 // Largest M handled by the VALU GEMV; above it the MFMA kernel runs.
 constexpr int kValuMaxM = 4;
 constexpr int kGemvWaves = 8;
 constexpr int kMfmaWaves = 8;
+constexpr int kMinBlocks = 160;     // fewest workgroups a wider n-block may leave (measured: qkv at M=32)
+constexpr int kTargetBlocks = 256;  // about one workgroup per CU, for split-K
+constexpr int kMaxSplits = 8;
 
 // Pipeline depth from the VGPRs one stage costs (4 per 1 KiB weight tile, 8
-// per x row fragment of 32 bytes), within a budget that leaves room for the
-// accumulators below the 256 VGPRs a 512-thread workgroup allows per wave.
+// per x row fragment of 32 bytes) after the accumulators, within the 256 VGPRs
+// a 512-thread workgroup allows per wave.
 constexpr int clamp_depth(int d) { return d < 2 ? 2 : (d > 8 ? 8 : d); }
 constexpr int gemv_depth(int M) { return clamp_depth(160 / (4 + 8 * M)); }
-constexpr int mfma_depth(int MT, int NPW) { return clamp_depth(160 / (4 * NPW + 8 * MT)); }
+constexpr int mfma_depth(int MT, int NPW) { return clamp_depth((176 - 4 * NPW * MT) / (4 * NPW + 8 * MT)); }
+
+// Launch plan for one chunk of at most 64 rows.
+struct Plan {
+    bool valu;
+    int MT, NPW, KS;
+};
+
+// Output tiles per wave: 4 at M 17..32 (x fragment reused 4x), 2 otherwise,
+// shrunk while that leaves fewer than kMinBlocks workgroups. A long K
+// (>= 8192) keeps the preferred width and splits K over workgroups instead;
+// for K = 4096 the extra reduce launch costs more than the split saves.
+static Plan plan_for(int M, int NT, int KT) {
+    Plan pl{};
+    pl.KS = 1;
+    if (M <= kValuMaxM) {
+        pl.valu = true;
+        pl.MT = M;
+        pl.NPW = 1;
+        return pl;
+    }
+    pl.valu = false;
+    pl.MT = (M + 15) / 16;
+    const int want = pl.MT == 2 ? 4 : 2;
+    int npw = want;
+    while (npw > 1 && (NT % npw || NT / npw < kMinBlocks)) npw /= 2;
+    pl.NPW = npw;
+    if (npw < want && NT % want == 0 && KT >= 128) {
+        const int blocks = NT / want;
+        int ks = (kTargetBlocks + blocks - 1) / blocks;
+        while (ks > 1 && (ks > kMaxSplits || KT / ks < 32)) --ks;
+        if (ks > 1) {
+            pl.NPW = want;
+            pl.KS = ks;
+        }
+    }
+    return pl;
+}
+
+static size_t workspace_for(int M, int NT, int KT) {
+    const Plan pl = plan_for(M, NT, KT);
+    return pl.KS > 1 ? (size_t)pl.KS * M * NT * kTileN * sizeof(float) : 0;
+}
 
 template <int M>
 static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const uint16_t* s, const uint16_t* b,
@@ -349,20 +434,25 @@ static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const u
 
 template <int MT, int NPW>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
-                        uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, kMfmaWaves, mfma_depth(MT, NPW)>), dim3(NT / NPW),
-                       dim3(kMfmaWaves * 64), 0, st, x, xs, M, w, s, b, y, ys, KT);
+                        uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
+    const int N = NT * kTileN;
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, kMfmaWaves, mfma_depth(MT, NPW)>), dim3(NT / NPW, KS),
+                       dim3(kMfmaWaves * 64), 0, st, x, xs, M, w, s, b, y, ys, KT, N, partial);
+    if (KS > 1) {
+        const int64_t total = (int64_t)M * N;
+        hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, partial, KS, M, N, b,
+                           y, ys);
+    }
 }
 
 template <int MT>
-static void launch_mfma_npw(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
-                            const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
-    // Two n-tiles per workgroup share each x fragment; keep at least one
-    // workgroup per CU.
-    if (MT <= 2 && NT % 2 == 0 && NT / 2 >= 256) {
-        launch_mfma<MT, 2>(x, xs, M, w, s, b, y, ys, NT, KT, st);
-    } else {
-        launch_mfma<MT, 1>(x, xs, M, w, s, b, y, ys, NT, KT, st);
+static void launch_mfma_npw(const Plan& pl, const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
+                            const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, float* partial,
+                            hipStream_t st) {
+    switch (pl.NPW) {
+        case 4: launch_mfma<MT, 4>(x, xs, M, w, s, b, y, ys, NT, KT, pl.KS, partial, st); break;
+        case 2: launch_mfma<MT, 2>(x, xs, M, w, s, b, y, ys, NT, KT, pl.KS, partial, st); break;
+        default: launch_mfma<MT, 1>(x, xs, M, w, s, b, y, ys, NT, KT, pl.KS, partial, st); break;
     }
 }
 
@@ -394,13 +484,15 @@ extern "C" int mx_w8a16_pack(const int8_t* q, int64_t N, int64_t K, uint8_t* pac
     return check_launch("mx_w8a16_pack");
 }
 
-extern "C" size_t mx_w8a16_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
+extern "C" size_t mx_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || N % w8a16::kTileN || K % w8a16::kTileK) return 0;
+    const int mc = (int)(M < 64 ? M : 64);  // rows are processed in chunks of at most 64
+    return w8a16::workspace_for(mc, (int)(N / w8a16::kTileN), (int)(K / w8a16::kTileK));
+}
 
 extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                                const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t N, int64_t y_stride,
                                void* workspace, size_t workspace_bytes, void* stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     if (!x || !packed || !scale || !y) return fail(MX_ERR_NULL, "mx_w8a16_linear: null pointer");
     if (M < 0 || N <= 0 || K <= 0) return fail(MX_ERR_INVALID, "mx_w8a16_linear: bad sizes M=%lld N=%lld K=%lld",
                                                (long long)M, (long long)N, (long long)K);
@@ -411,17 +503,23 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
         return fail(MX_ERR_INVALID, "mx_w8a16_linear: row strides must cover K and N");
     if (!aligned(x, 16) || (x_stride % 8) != 0 || !aligned(packed, 16))
         return fail(MX_ERR_ALIGNMENT, "mx_w8a16_linear: x rows and packed weights must be 16-byte aligned");
-    if (N / w8a16::kTileN > 0x7fffffff || K / w8a16::kTileK > 0x7fffffff)
+    if (N / w8a16::kTileN > 0x7fffffff || K / w8a16::kTileK > 0x7fffffff || K * 64 > 0x7fffffff)
         return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear: matrix too large");
+    if (workspace && !aligned(workspace, 16))
+        return fail(MX_ERR_ALIGNMENT, "mx_w8a16_linear: workspace must be 16-byte aligned");
     if (M == 0) return MX_OK;
     const int NT = (int)(N / w8a16::kTileN);
     const int KT = (int)(K / w8a16::kTileK);
     hipStream_t st = as_stream(stream);
+    float* partial = static_cast<float*>(workspace);
     for (int64_t m0 = 0; m0 < M; m0 += 64) {
         const int mc = (int)((M - m0) < 64 ? (M - m0) : 64);
         const uint16_t* xc = x + m0 * x_stride;
         uint16_t* yc = y + m0 * y_stride;
-        if (mc <= w8a16::kValuMaxM) {
+        w8a16::Plan pl = w8a16::plan_for(mc, NT, KT);
+        // Split-K needs the caller's workspace; without enough of it run unsplit.
+        if (pl.KS > 1 && (!workspace || workspace_bytes < w8a16::workspace_for(mc, NT, KT))) pl.KS = 1;
+        if (pl.valu) {
             switch (mc) {
                 case 1: w8a16::launch_gemv<1>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
                 case 2: w8a16::launch_gemv<2>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
@@ -429,11 +527,11 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
                 default: w8a16::launch_gemv<4>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
             }
         } else {
-            switch ((mc + 15) / 16) {
-                case 1: w8a16::launch_mfma_npw<1>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
-                case 2: w8a16::launch_mfma_npw<2>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
-                case 3: w8a16::launch_mfma_npw<3>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
-                default: w8a16::launch_mfma_npw<4>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, st); break;
+            switch (pl.MT) {
+                case 1: w8a16::launch_mfma_npw<1>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
+                case 2: w8a16::launch_mfma_npw<2>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
+                case 3: w8a16::launch_mfma_npw<3>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
+                default: w8a16::launch_mfma_npw<4>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
             }
         }
         const int rc = check_launch("mx_w8a16_linear");

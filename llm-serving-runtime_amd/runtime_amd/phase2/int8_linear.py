@@ -25,6 +25,23 @@ TILE_K = 64
 
 DEFAULT_TARGETS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
+# Split-K partials of mx_w8a16_linear: one growable buffer per device, shared by
+# every call on that device (calls on one stream are serialised; concurrent
+# streams must not use this module's cache at the same time).
+_workspaces: dict[torch.device, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> tuple[int | None, int]:
+    if nbytes == 0:
+        return None, 0
+    ws = _workspaces.get(device)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("int8 linear workspace must be sized before graph capture; run the step once eagerly")
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[device] = ws
+    return ws.data_ptr(), ws.numel()
+
 
 def quantize_weight(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Quantize ``weight [N, K]`` on the device: returns ``(q int8 [N, K], scale fp16 [N])``.
@@ -89,11 +106,12 @@ def int8_linear(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias
     if m == 0:
         return y.view(*lead, n)
     lib = _hip.load()
+    ws_ptr, ws_bytes = _workspace(x.device, int(lib.mx_w8a16_workspace_bytes(m, n, k)))
     _hip.check(
         lib.mx_w8a16_linear(
             x2.data_ptr(), m, k, x2.stride(0), packed.data_ptr(), scale.data_ptr(),
             bias.data_ptr() if bias is not None else None, y.data_ptr(), n, y.stride(0),
-            None, 0, _hip.stream_handle(x.device),
+            ws_ptr, ws_bytes, _hip.stream_handle(x.device),
         ),
         "mx_w8a16_linear",
     )

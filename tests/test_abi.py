@@ -44,7 +44,13 @@ def test_paged_attn_workspace_layout_is_host_computable():
     assert lib.mx_paged_attn_workspace_bytes(1, 8, 2, 64, 8, 16, 0) == \
         lib.mx_paged_attn_workspace_bytes(1, 8, 2, 64, 8, 16, 256)
     assert lib.mx_paged_attn_error_offset(4, 8, 2, 64, 8, 16, 0) % 256 == 0
+    # Split-K partials only for a long K with few n-blocks: 4 splits x 32 rows x 4096 fp32 for the
+    # 4096x14336 down projection at M=32; none for K=4096, where n-blocks fill the chip, or the GEMV.
+    assert lib.mx_w8a16_workspace_bytes(32, 4096, 14336) == 4 * 32 * 4096 * 4
     assert lib.mx_w8a16_workspace_bytes(32, 4096, 4096) == 0
+    assert lib.mx_w8a16_workspace_bytes(32, 28672, 4096) == 0
+    assert lib.mx_w8a16_workspace_bytes(1, 4096, 14336) == 0
+    assert lib.mx_w8a16_workspace_bytes(200, 4096, 14336) == lib.mx_w8a16_workspace_bytes(64, 4096, 14336)
 
 
 def _status(rc: int, expected: int) -> None:

@@ -101,6 +101,29 @@ def test_linear_config1_golden():
     np.testing.assert_allclose(y, int8_quant.linear_ref_fp32(x.numpy(), q, s), atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("m", [5, 8, 16, 32, 48, 64, 80])
+def test_linear_split_k_path_and_unsplit_fallback(m):
+    """N=256, K=8192: few n-blocks and a long K, so the planner splits K over workgroups (fp32 partials +
+    reduce); calling without a workspace must give the same answer through the unsplit kernel."""
+    from runtime_amd.phase2 import _hip
+
+    n, k = 256, 8192
+    q, s = _quantized(300 + m, n, k)
+    rng = np.random.default_rng(300 + m)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float16)
+    lib = _hip.load()
+    assert lib.mx_w8a16_workspace_bytes(m, n, k) > 0
+    packed, sd, bd, xd = pack_weight(_cuda(q)), _cuda(s), _cuda(bias), _cuda(x)
+    want = int8_quant.linear_ref_fp32(x, q, s, bias)
+    got = int8_linear(xd, packed, sd, bd, n)
+    np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+    y = torch.empty(m, n, dtype=torch.float16, device="cuda")
+    _hip.check(lib.mx_w8a16_linear(xd.data_ptr(), m, k, k, packed.data_ptr(), sd.data_ptr(), bd.data_ptr(),
+                                   y.data_ptr(), n, n, None, 0, _hip.stream_handle(xd.device)), "linear")
+    np.testing.assert_allclose(y.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+
+
 LLAMA_SHAPES = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 28672), ("down", 14336, 4096)]
 
 
