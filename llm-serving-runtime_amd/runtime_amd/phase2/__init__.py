@@ -1,4 +1,4 @@
-"""Decode-path modules: int8 linear, paged KV pool, paged-attention decode, HF hook."""
+"""Decode-path modules: int8 linear, paged KV pool, paged-attention decode, HF hook and cache adapters."""
 
 from .int8_linear import Int8Linear, int8_linear, pack_weight, quantize_model_, quantize_weight
 from .paged_attention_hip import (

@@ -6,6 +6,13 @@ registered as ``ALL_ATTENTION_FUNCTIONS["block_paged"]`` with
 When decode metadata is set, ``q_len == 1`` and the query is on a device, the
 fused HIP kernel runs and ``[B, 1, Hq, D]`` is returned (``:37-48``); otherwise
 eager attention on the gathered K/V (prefill, ``:50-60``).
+
+Difference kept on purpose: transformers 5.x hands a custom attention
+implementation that has no registered mask function ``attention_mask=None``
+(``masking_utils._preprocess_mask_arguments`` returns early for it), so the
+reference's eager branch, which only adds a mask when one is given, attends
+bidirectionally during prefill. Here a missing mask with ``q_len > 1`` is
+replaced by the causal mask (query ``i`` sees keys ``0 .. kv_len - q_len + i``).
 """
 
 from __future__ import annotations
@@ -24,6 +31,12 @@ def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
     return hidden_states.reshape(batch, num_key_value_heads * n_rep, slen, head_dim)
 
 
+def _causal_block(q_len: int, kv_len: int, device: torch.device) -> torch.Tensor:
+    """``True`` where query ``i`` (the last ``q_len`` of ``kv_len`` positions) must not see key ``j``."""
+    qpos = torch.arange(kv_len - q_len, kv_len, device=device).view(-1, 1)
+    return torch.arange(kv_len, device=device).view(1, -1) > qpos
+
+
 def block_paged_attention_forward(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                                   attention_mask: torch.Tensor | None, scaling: float, dropout: float = 0.0, **kwargs):
     num_kv_groups = getattr(module, "num_key_value_groups", 1)
@@ -38,6 +51,9 @@ def block_paged_attention_forward(module, query: torch.Tensor, key: torch.Tensor
     attn_weights = torch.matmul(query, key_states.transpose(2, 3).contiguous()) * scaling
     if attention_mask is not None:
         attn_weights = attn_weights + attention_mask
+    elif query.shape[-2] > 1:
+        attn_weights = attn_weights.masked_fill(_causal_block(query.shape[-2], key.shape[-2], query.device),
+                                                float("-inf"))
     attn_weights = F.softmax(attn_weights, dim=-1, dtype=torch.float32).to(query.dtype)
     if dropout > 0.0 and module.training:
         attn_weights = F.dropout(attn_weights, p=dropout)

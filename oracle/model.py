@@ -1,0 +1,155 @@
+"""fp32 CPU oracle for greedy decode of an HF decoder with int8 projections.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+What it restates: the greedy decode loop of ``TransformersBackend``
+(``runtime/phase2/worker_server.py:733-794``: one token per row per step,
+``argmax`` over the last logits, ``:786``) on a model whose quantized-linear
+slot (``:194-205``) holds the build's int8 format. The model math itself is the
+transformers library's Qwen2 / Llama modelling code (third-party: 5.15.0
+installed, the reference pins 5.8.1 in ``runtime/requirements-transformers.txt:4``),
+run in fp32 on the CPU with eager attention.
+
+Weights are made identical to the device model's:
+
+* every projection the device path quantizes (``q/k/v/o/gate/up/down_proj``)
+  becomes ``q * s`` from :func:`oracle.int8_quant.quantize_per_channel`, which
+  is bit-exact with the device quantizer;
+* every other parameter (embeddings, norms, biases, ``lm_head``) is rounded
+  through fp16, the dtype the device model stores it in.
+
+What remains different is activation precision only (fp16 on the device,
+fp32 here), which is what the greedy-decode tolerance covers.
+
+Teacher forcing: :func:`teacher_forced_logits` runs one causal forward over
+``prompt + generated[:-1]`` and returns the logits every generated token was
+chosen from. If the device's tokens are the argmax of these logits at every
+step, the oracle's own free-running greedy decode produces the same tokens.
+
+Parity pins (``tests/test_oracle_model.py``): teacher-forced logits equal a
+step-by-step ``DynamicCache`` decode of the same model (an off-by-one in the
+window fails it); projection weights equal ``dequantize(quantize_per_channel(W))``
+exactly; a planted fp16 rounding of a projection weight is detected.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import torch
+from torch import nn
+
+from .int8_quant import dequantize, quantize_per_channel
+
+PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+# Config 3: Qwen2-0.5B-shaped decoder (hidden 896, 24 layers, 14 Q / 2 KV heads,
+# head_dim 64, SwiGLU 4864, vocab 151936, RMSNorm, RoPE theta 1e6).
+QWEN2_05B = dict(hidden_size=896, num_hidden_layers=24, num_attention_heads=14, num_key_value_heads=2,
+                 intermediate_size=4864, vocab_size=151936, rope_theta=1000000.0, rms_norm_eps=1e-6,
+                 max_position_embeddings=32768, tie_word_embeddings=False)
+
+
+def random_qwen2(seed: int = 0, **overrides):
+    """A random-init ``Qwen2ForCausalLM`` in fp32 on the CPU (eager attention).
+
+    Weights come from one numpy PCG64 stream in parameter order: matrices and
+    embeddings ~ N(0, 0.02), biases ~ N(0, 0.02), norm weights ~ 1 + N(0, 0.05).
+    (HF's own initializer is not used: it takes minutes at this size and zeroes
+    the biases, which would leave the bias path untested.)
+    """
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    from transformers.initialization import no_init_weights
+
+    kwargs = dict(QWEN2_05B)
+    kwargs.update(overrides)
+    config = Qwen2Config(**kwargs)
+    config._attn_implementation = "eager"
+    with no_init_weights():
+        model = Qwen2ForCausalLM(config)
+    rng = np.random.default_rng(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            noise = rng.standard_normal(p.shape, dtype=np.float32)
+            if name.endswith("norm.weight"):
+                p.copy_(torch.from_numpy(1.0 + 0.05 * noise))
+            else:
+                p.copy_(torch.from_numpy(0.02 * noise))
+    return model.float().eval()
+
+
+def _round_fp16_(t: torch.Tensor) -> None:
+    t.copy_(t.to(torch.float16).to(torch.float32))
+
+
+def quantized_reference(model: nn.Module, targets: tuple[str, ...] = PROJECTIONS) -> nn.Module:
+    """Deep copy of ``model`` (fp32, CPU) holding exactly the device model's weights."""
+    ref = copy.deepcopy(model).float().cpu().eval()
+    projected: set[int] = set()
+    with torch.no_grad():
+        for parent in ref.modules():
+            for name, child in parent.named_children():
+                if isinstance(child, nn.Linear) and name in targets:
+                    q, s = quantize_per_channel(child.weight.detach().numpy())
+                    child.weight.copy_(torch.from_numpy(dequantize(q, s)))
+                    projected.add(id(child.weight))
+        for p in ref.parameters():
+            if id(p) not in projected:
+                _round_fp16_(p)
+    ref.config._attn_implementation = "eager"
+    return ref
+
+
+@torch.no_grad()
+def teacher_forced_logits(model: nn.Module, prompt: torch.Tensor, generated: torch.Tensor) -> torch.Tensor:
+    """Logits ``[len(generated), V]`` (fp32) that each of ``generated`` was chosen from.
+
+    ``generated[0]`` follows ``prompt``; ``generated[i]`` follows
+    ``prompt + generated[:i]``. One causal forward over
+    ``prompt + generated[:-1]`` keeping the last ``len(generated)`` positions.
+    """
+    prompt = prompt.reshape(-1).to(torch.long).cpu()
+    generated = generated.reshape(-1).to(torch.long).cpu()
+    n = int(generated.numel())
+    ids = torch.cat([prompt, generated[:-1]]).view(1, -1)
+    out = model(input_ids=ids, use_cache=False, logits_to_keep=n)
+    return out.logits[0].float()
+
+
+@torch.no_grad()
+def greedy_reference(model: nn.Module, prompt: torch.Tensor, steps: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Free-running greedy decode with a ``DynamicCache``: ``steps + 1`` tokens and their logits."""
+    ids = prompt.reshape(1, -1).to(torch.long).cpu()
+    out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
+    cache = out.past_key_values
+    logits = [out.logits[0, -1].float()]
+    tokens = [int(logits[-1].argmax())]
+    for _ in range(steps):
+        out = model(input_ids=torch.tensor([[tokens[-1]]]), past_key_values=cache, use_cache=True)
+        cache = out.past_key_values
+        logits.append(out.logits[0, -1].float())
+        tokens.append(int(logits[-1].argmax()))
+    return torch.tensor(tokens), torch.stack(logits)
+
+
+def greedy_agreement(logits_ref: torch.Tensor, tokens: torch.Tensor, tie_tol: float) -> dict:
+    """Compare device greedy ``tokens [T]`` with the teacher-forced oracle ``logits_ref [T, V]``.
+
+    A step agrees when the token is the oracle's argmax. A step that does not
+    agree is a near tie when the oracle prefers its argmax by at most
+    ``tie_tol`` over the chosen token. Returns counts, the index of the first
+    disagreement (or -1) and the largest gap seen at a disagreement.
+    """
+    tokens = tokens.reshape(-1).to(torch.long).cpu()
+    best = logits_ref.argmax(dim=-1)
+    gap = logits_ref.max(dim=-1).values - logits_ref.gather(1, tokens.view(-1, 1)).squeeze(1)
+    miss = best != tokens
+    idx = torch.nonzero(miss).flatten()
+    return {
+        "steps": int(tokens.numel()),
+        "mismatches": int(miss.sum()),
+        "first_mismatch": int(idx[0]) if idx.numel() else -1,
+        "max_gap_at_mismatch": float(gap[miss].max()) if idx.numel() else 0.0,
+        "ties_ok": bool((gap[miss] <= tie_tol).all()) if idx.numel() else True,
+    }

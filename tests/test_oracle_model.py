@@ -1,0 +1,84 @@
+"""Pins of the greedy-decode model oracle (CPU).
+
+The model math is transformers' own; what these tests pin is what the oracle
+adds on top: the teacher-forcing window, the weight substitution and the
+agreement rule used by the GPU greedy-decode tests.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from oracle.int8_quant import dequantize, quantize_per_channel
+
+TINY = dict(hidden_size=128, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+            intermediate_size=256, vocab_size=512, max_position_embeddings=256)
+
+
+@pytest.fixture(scope="module")
+def tiny_pair():
+    model = om.random_qwen2(seed=3, **TINY)
+    return model, om.quantized_reference(model)
+
+
+def test_random_qwen2_is_seeded_and_has_biases():
+    a = om.random_qwen2(seed=5, **TINY)
+    b = om.random_qwen2(seed=5, **TINY)
+    c = om.random_qwen2(seed=6, **TINY)
+    for (na, pa), (_, pb), (_, pc) in zip(a.named_parameters(), b.named_parameters(), c.named_parameters()):
+        assert torch.equal(pa, pb), na
+        assert not torch.equal(pa, pc), na
+    bias = a.model.layers[0].self_attn.q_proj.bias
+    assert bias is not None and float(bias.detach().abs().max()) > 0
+
+
+def test_quantized_reference_holds_device_weights(tiny_pair):
+    model, ref = tiny_pair
+    named = dict(ref.named_parameters())
+    for name, p in model.named_parameters():
+        r = named[name]
+        leaf = name.split(".")[-2]
+        if leaf in om.PROJECTIONS and name.endswith("weight"):
+            q, s = quantize_per_channel(p.detach().numpy())
+            assert torch.equal(r, torch.from_numpy(dequantize(q, s))), name
+            # A plausible slip, storing the projection as fp16 instead of q*s, differs.
+            assert not torch.equal(r, p.detach().half().float()), name
+        else:
+            assert torch.equal(r, p.detach().half().float()), name
+    # The source model is untouched.
+    assert not torch.equal(model.model.layers[0].mlp.down_proj.weight, ref.model.layers[0].mlp.down_proj.weight)
+
+
+def test_teacher_forcing_equals_stepwise_decode(tiny_pair):
+    _, ref = tiny_pair
+    prompt = torch.randint(0, TINY["vocab_size"], (37,), generator=torch.Generator().manual_seed(0))
+    tokens, logits = om.greedy_reference(ref, prompt, steps=12)
+    tf = om.teacher_forced_logits(ref, prompt, tokens)
+    assert tf.shape == logits.shape == (13, TINY["vocab_size"])
+    torch.testing.assert_close(tf, logits, atol=1e-4, rtol=1e-4)
+    assert torch.equal(tf.argmax(dim=-1), tokens)
+    # Planted off-by-one: a window shifted by one token no longer matches.
+    shifted = om.teacher_forced_logits(ref, prompt[:-1], tokens)
+    assert (shifted - logits).abs().max() > 1e-2
+
+
+def test_greedy_agreement_rule():
+    logits = torch.tensor([[0.0, 1.0, 0.5], [2.0, 1.99, 0.0], [0.0, 0.0, 3.0]])
+    exact = om.greedy_agreement(logits, torch.tensor([1, 0, 2]), tie_tol=0.05)
+    assert exact == {"steps": 3, "mismatches": 0, "first_mismatch": -1, "max_gap_at_mismatch": 0.0, "ties_ok": True}
+    tie = om.greedy_agreement(logits, torch.tensor([1, 1, 2]), tie_tol=0.05)
+    assert tie["mismatches"] == 1 and tie["first_mismatch"] == 1 and tie["ties_ok"]
+    assert abs(tie["max_gap_at_mismatch"] - 0.01) < 1e-6
+    wrong = om.greedy_agreement(logits, torch.tensor([2, 0, 2]), tie_tol=0.05)
+    assert wrong["first_mismatch"] == 0 and not wrong["ties_ok"]
+
+
+def test_config3_shape_constants():
+    cfg = om.QWEN2_05B
+    assert (cfg["hidden_size"], cfg["num_hidden_layers"], cfg["num_attention_heads"], cfg["num_key_value_heads"],
+            cfg["intermediate_size"], cfg["vocab_size"]) == (896, 24, 14, 2, 4864, 151936)
+    assert cfg["hidden_size"] // cfg["num_attention_heads"] == 64
+    assert np.isclose(cfg["rope_theta"], 1e6)
