@@ -1,6 +1,7 @@
 /*
  * mxdecode - MI355X (gfx950) decode-step hot path: weight-only int8 linear
- * layers and paged-attention decode. C ABI of libmxdecode.so.
+ * layers, paged-attention decode and the per-layer glue around them (KV append,
+ * rotary embedding, residual + RMSNorm, SwiGLU). C ABI of libmxdecode.so.
  *
  * Conventions
  *   - fp16 tensors are passed as `uint16_t*` (IEEE binary16 bit patterns).
@@ -22,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 1
+#define MX_ABI_VERSION 2
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -122,6 +123,65 @@ int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const ui
  * device-to-host copy by the caller; clearing it is the caller's choice. */
 size_t mx_paged_attn_error_offset(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                   int32_t block_size, int32_t chunk_tokens);
+
+/* ----------------------------------------------------------------------------
+ * Decode-step glue.
+ *
+ * The element-wise work of a decoder layer around the linears and the
+ * attention call. In the reference these are torch ops inside the HF decoder
+ * layer (transformers' RMSNorm, apply_rotary_pos_emb and SwiGLU MLP, a
+ * third-party library reached from the batched decode forward,
+ * runtime/phase2/worker_server.py:771-775) and the KV scatter of
+ * GpuKVBlockPool.write_tokens_batch (runtime/phase2/paged_kv_kernel.py:176-227),
+ * called by BlockPagedBatchLayer.update (runtime/phase2/paged_kv_cache.py:121-157).
+ * Out-of-range slots are skipped, never written, and OR-ed into *err when err
+ * is not NULL (bit 0: logical block past max_blocks or physical id outside
+ * [0, num_pool_blocks); bit 1: position outside the rotary table).
+ * ------------------------------------------------------------------------- */
+
+/* Scatter new K/V states [B, Hkv, T, D] (strides new_sb, new_sh, new_st; D
+ * contiguous) into per-layer pool views [num_blocks, Hkv, block_size, D]
+ * (strides kv_sblk, kv_shead, D, 1): token t of row b goes to position
+ * start_pos[b] + t, i.e. block block_tables[b, pos / block_size] at offset
+ * pos % block_size. Replaces write_tokens_batch (paged_kv_kernel.py:176-227;
+ * the reference loops over tokens on the host and checks bounds with host
+ * syncs, :217-227). D % 8 == 0; rows 16-byte aligned. */
+int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_t new_sb, int64_t new_sh, int64_t new_st,
+                 int32_t B, int32_t T, int32_t Hkv, int32_t D, const int32_t* block_tables, int64_t bt_sb,
+                 int32_t max_blocks, const int32_t* start_pos, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk,
+                 int64_t kv_shead, int32_t block_size, int32_t num_pool_blocks, int32_t* err, void* stream);
+
+/* From one fused QKV projection row per sequence (fp16 [B, (Hq + 2*Hkv) * D],
+ * row stride qkv_stride; heads in the order q, k, v): rotate q and k with
+ * rotate-half RoPE at position positions[b] (pairs i, i + D/2 use
+ * rope[pos][i] = (cos, sin), an fp32 table of max_pos rows), write q to
+ * q_out [B, Hq * D] (row stride q_stride) and k, v to the pool slot of
+ * position positions[b] (as mx_kv_append). Replaces HF's
+ * apply_rotary_pos_emb (transformers, reached from worker_server.py:771-775)
+ * followed by BlockPagedBatchLayer.update's write (paged_kv_cache.py:121-157).
+ * A position outside the table writes q = 0 and no K/V. */
+int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                       const float* rope, int32_t max_pos, const int32_t* positions, uint16_t* q_out,
+                       int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
+                       const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, int32_t block_size,
+                       int32_t num_pool_blocks, int32_t* err, void* stream);
+
+/* h = residual ? fp16(x + residual) : x;  residual_out (if not NULL) = h;
+ * out = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * weight), per row of H
+ * (H % 8 == 0, H <= 16384). The decoder layer's residual add and the
+ * following RMSNorm (transformers' Qwen2/Llama RMSNorm, reached from
+ * worker_server.py:771-775) in one pass. out may alias x and residual_out may
+ * alias residual; out must not alias residual_out. */
+int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride,
+                   const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out, int64_t out_stride,
+                   uint16_t* residual_out, int64_t ro_stride, void* stream);
+
+/* out[m, i] = fp16(fp16(silu(gate_up[m, i])) * gate_up[m, I + i]) for i < I
+ * (I % 8 == 0): the SwiGLU product between the fused gate||up projection and
+ * the down projection (transformers' MLP act_fn(gate_proj(x)) * up_proj(x),
+ * reached from worker_server.py:771-775). */
+int mx_silu_mul(const uint16_t* gate_up, int64_t gu_stride, int32_t M, int32_t I, uint16_t* out,
+                int64_t out_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,321 @@
+// Decode-step glue on gfx950: KV append into the block pool, rotary embedding fused with the
+// append, residual add fused with RMSNorm, and SwiGLU's SiLU * up.
+//
+// These replace the per-layer torch ops around the int8 linears and the paged-attention
+// kernel (the reference runs them as separate HF / torch ops inside every decoder layer,
+// and its KV write is a per-token Python loop, runtime/phase2/paged_kv_kernel.py:176-227).
+// Every kernel is HBM/latency bound element-wise work: one thread per 16-byte chunk,
+// 128-bit loads and stores, no LDS except the RMSNorm row reduction.
+#include "common.h"
+
+namespace mx {
+namespace glue {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+__device__ __forceinline__ half8v as_h8(uint4 v) { return __builtin_bit_cast(half8v, v); }
+__device__ __forceinline__ uint4 as_u4(half8v v) { return __builtin_bit_cast(uint4, v); }
+
+// Where token `pos` of row `b` lives in the pool, or -1 when its logical block is past the
+// table or its physical id is outside the pool (the token is then skipped and flagged).
+__device__ __forceinline__ int64_t slot_offset(const int32_t* bt, int64_t bt_sb, int max_blocks, int b, int pos,
+                                               int bs, int num_pool_blocks, int64_t sblk, int64_t shead, int head,
+                                               int D) {
+    if (pos < 0) return -1;
+    const int lb = pos / bs;
+    if (lb >= max_blocks) return -1;
+    const int phys = bt[(int64_t)b * bt_sb + lb];
+    if (phys < 0 || phys >= num_pool_blocks) return -1;
+    return (int64_t)phys * sblk + (int64_t)head * shead + (int64_t)(pos - lb * bs) * D;
+}
+
+struct AppendParams {
+    const uint16_t* k_new;
+    const uint16_t* v_new;
+    int64_t sb, sh, st;  // element strides of the new states [B, Hkv, T, D]
+    int T, Hkv, D;
+    const int32_t* bt;
+    int64_t bt_sb;
+    int max_blocks;
+    const int32_t* start;
+    uint16_t* k_pool;
+    uint16_t* v_pool;
+    int64_t sblk, shead;
+    int bs, num_pool_blocks;
+    int32_t* err;
+};
+
+// One thread per 8-element chunk of one (row, token, kv-head); K and V share the slot.
+__global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendParams p, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= total) return;
+    const int chunks = p.D >> 3;
+    const int c = (int)(i % chunks);
+    int64_t r = i / chunks;
+    const int h = (int)(r % p.Hkv);
+    r /= p.Hkv;
+    const int t = (int)(r % p.T);
+    const int b = (int)(r / p.T);
+    const int64_t dst = slot_offset(p.bt, p.bt_sb, p.max_blocks, b, p.start[b] + t, p.bs, p.num_pool_blocks, p.sblk,
+                                    p.shead, h, p.D);
+    if (dst < 0) {
+        if (p.err && c == 0) atomicOr(p.err, 1);
+        return;
+    }
+    const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)t * p.st + c * 8;
+    st16(p.k_pool + dst + c * 8, ld16(p.k_new + src));
+    st16(p.v_pool + dst + c * 8, ld16(p.v_new + src));
+}
+
+struct RopeAppendParams {
+    const uint16_t* qkv;
+    int64_t qkv_stride;
+    int Hq, Hkv, D;
+    const float2* rope;  // [max_pos][D/2] (cos, sin)
+    int max_pos;
+    const int32_t* positions;
+    uint16_t* q_out;
+    int64_t q_stride;
+    uint16_t* k_pool;
+    uint16_t* v_pool;
+    int64_t sblk, shead;
+    const int32_t* bt;
+    int64_t bt_sb;
+    int max_blocks, bs, num_pool_blocks;
+    int32_t* err;
+};
+
+// Rotate-half RoPE (pairs i and i + D/2 share frequency i) on the q and k heads of one
+// fused-QKV output row, then q -> q_out and k, v -> the pool slot of position `pos`.
+// One thread per 4 pairs of a q/k head (two 8-byte loads) or per 8 elements of a v head.
+__global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendParams p, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= total) return;
+    const int per_head = p.D >> 3;
+    const int heads = p.Hq + 2 * p.Hkv;
+    const int c = (int)(i % per_head);
+    const int hs = (int)((i / per_head) % heads);
+    const int b = (int)(i / ((int64_t)per_head * heads));
+    const uint16_t* row = p.qkv + (int64_t)b * p.qkv_stride + (int64_t)hs * p.D;
+    const int pos = p.positions[b];
+    if (hs < p.Hq + p.Hkv) {
+        const int half = p.D >> 1;
+        const int j = c * 4;
+        const bool pos_ok = pos >= 0 && pos < p.max_pos;
+        half4v o1 = {0, 0, 0, 0}, o2 = {0, 0, 0, 0};
+        if (pos_ok) {
+            const half4v x1 = __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(row + j));
+            const half4v x2 = __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(row + half + j));
+            const float2* cs = p.rope + (int64_t)pos * half + j;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float2 f = cs[e];
+                const float a = (float)x1[e], bb = (float)x2[e];
+                o1[e] = (_Float16)(a * f.x - bb * f.y);
+                o2[e] = (_Float16)(bb * f.x + a * f.y);
+            }
+        } else if (p.err && c == 0) {
+            atomicOr(p.err, 2);
+        }
+        if (hs < p.Hq) {
+            uint16_t* q = p.q_out + (int64_t)b * p.q_stride + (int64_t)hs * p.D;
+            *reinterpret_cast<uint2*>(q + j) = __builtin_bit_cast(uint2, o1);
+            *reinterpret_cast<uint2*>(q + half + j) = __builtin_bit_cast(uint2, o2);
+            return;
+        }
+        if (!pos_ok) return;
+        const int64_t dst = slot_offset(p.bt, p.bt_sb, p.max_blocks, b, pos, p.bs, p.num_pool_blocks, p.sblk,
+                                        p.shead, hs - p.Hq, p.D);
+        if (dst < 0) {
+            if (p.err && c == 0) atomicOr(p.err, 1);
+            return;
+        }
+        *reinterpret_cast<uint2*>(p.k_pool + dst + j) = __builtin_bit_cast(uint2, o1);
+        *reinterpret_cast<uint2*>(p.k_pool + dst + half + j) = __builtin_bit_cast(uint2, o2);
+        return;
+    }
+    if (pos >= p.max_pos) return;  // flagged by the q/k threads of the row
+    const int64_t dst = slot_offset(p.bt, p.bt_sb, p.max_blocks, b, pos, p.bs, p.num_pool_blocks, p.sblk, p.shead,
+                                    hs - p.Hq - p.Hkv, p.D);
+    if (dst < 0) return;  // flagged by the k thread of the same chunk
+    st16(p.v_pool + dst + c * 8, ld16(row + c * 8));
+}
+
+constexpr int kNormMaxChunks = 8;  // H <= kThreads * 8 * kNormMaxChunks = 16384
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    return s;
+}
+
+// h = x (+ residual, rounded to fp16); residual_out = h; out = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * w).
+// The two roundings of the output follow HF's RMSNorm (normalise in fp32, cast, scale in fp16).
+// out may alias x and residual_out may alias residual (each thread reads its chunks before
+// it writes them); out must not alias residual_out.
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(const uint16_t* x, int64_t xs, const uint16_t* res,
+                                                               int64_t rs, const uint16_t* w, int H, float eps,
+                                                               uint16_t* out, int64_t os, uint16_t* res_out,
+                                                               int64_t ros) {
+    __shared__ float red[kThreads / 64];
+    const int m = blockIdx.x;
+    const int chunks = H >> 3;
+    half8v h[kNormMaxChunks];
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kNormMaxChunks; ++u) {
+        const int c = threadIdx.x + u * kThreads;
+        if (c < chunks) {
+            half8v v = as_h8(ld16(x + (int64_t)m * xs + c * 8));
+            if (res) {
+                const half8v r = as_h8(ld16(res + (int64_t)m * rs + c * 8));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] + (float)r[e]);
+            }
+            if (res_out) st16(res_out + (int64_t)m * ros + c * 8, as_u4(v));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
+            h[u] = v;
+        }
+    }
+    const float scale = rsqrtf(block_sum(ss, red) / (float)H + eps);
+#pragma unroll
+    for (int u = 0; u < kNormMaxChunks; ++u) {
+        const int c = threadIdx.x + u * kThreads;
+        if (c < chunks) {
+            const half8v g = as_h8(ld16(w + c * 8));
+            half8v o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 n = (_Float16)((float)h[u][e] * scale);
+                o[e] = (_Float16)((float)n * (float)g[e]);
+            }
+            st16(out + (int64_t)m * os + c * 8, as_u4(o));
+        }
+    }
+}
+
+// out[m, i] = fp16(fp16(silu(gate[m, i])) * up[m, i]) with gate = gu[m, :I], up = gu[m, I:2I].
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, int64_t gs, int I, uint16_t* out,
+                                                            int64_t os, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= total) return;
+    const int chunks = I >> 3;
+    const int c = (int)(i % chunks);
+    const int64_t m = i / chunks;
+    const half8v g = as_h8(ld16(gu + m * gs + c * 8));
+    const half8v u = as_h8(ld16(gu + m * gs + I + c * 8));
+    half8v o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float gf = (float)g[e];
+        const _Float16 s = (_Float16)(gf / (1.0f + expf(-gf)));
+        o[e] = (_Float16)((float)s * (float)u[e]);
+    }
+    st16(out + m * os + c * 8, as_u4(o));
+}
+
+inline bool a16(const void* p) { return aligned(p, 16); }
+
+}  // namespace glue
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_t new_sb, int64_t new_sh,
+                            int64_t new_st, int32_t B, int32_t T, int32_t Hkv, int32_t D, const int32_t* block_tables,
+                            int64_t bt_sb, int32_t max_blocks, const int32_t* start_pos, uint16_t* k_pool,
+                            uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead, int32_t block_size,
+                            int32_t num_pool_blocks, int32_t* err, void* stream) {
+    clear_error();
+    if (B < 0 || T < 0) return fail(MX_ERR_INVALID, "mx_kv_append: B and T must be >= 0 (B=%d T=%d)", B, T);
+    if (B == 0 || T == 0) return MX_OK;
+    if (!k_new || !v_new || !block_tables || !start_pos || !k_pool || !v_pool)
+        return fail(MX_ERR_NULL, "mx_kv_append: null pointer");
+    if (Hkv <= 0 || D <= 0 || D % 8 || block_size <= 0 || max_blocks <= 0 || num_pool_blocks <= 0)
+        return fail(MX_ERR_INVALID, "mx_kv_append: need Hkv, max_blocks, block_size, pool > 0 and D %% 8 == 0 "
+                                    "(Hkv=%d D=%d bs=%d max_blocks=%d pool=%d)", Hkv, D, block_size, max_blocks,
+                    num_pool_blocks);
+    if (new_sb % 8 || new_sh % 8 || new_st % 8 || kv_sblk % 8 || kv_shead % 8 || !glue::a16(k_new) ||
+        !glue::a16(v_new) || !glue::a16(k_pool) || !glue::a16(v_pool))
+        return fail(MX_ERR_ALIGNMENT, "mx_kv_append: states and pool need 16-byte aligned rows");
+    glue::AppendParams p{k_new, v_new, new_sb, new_sh, new_st, T, Hkv, D, block_tables, bt_sb, max_blocks,
+                         start_pos, k_pool, v_pool, kv_sblk, kv_shead, block_size, num_pool_blocks, err};
+    const int64_t total = (int64_t)B * T * Hkv * (D / 8);
+    hipLaunchKernelGGL(glue::kv_append_kernel, dim3((unsigned)ceil_div(total, glue::kThreads)), dim3(glue::kThreads),
+                       0, as_stream(stream), p, total);
+    return check_launch("mx_kv_append");
+}
+
+extern "C" int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32_t B, int32_t Hq, int32_t Hkv,
+                                  int32_t D, const float* rope, int32_t max_pos, const int32_t* positions,
+                                  uint16_t* q_out, int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool,
+                                  int64_t kv_sblk, int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb,
+                                  int32_t max_blocks, int32_t block_size, int32_t num_pool_blocks, int32_t* err,
+                                  void* stream) {
+    clear_error();
+    if (B < 0) return fail(MX_ERR_INVALID, "mx_qkv_rope_append: B must be >= 0");
+    if (B == 0) return MX_OK;
+    if (!qkv || !rope || !positions || !q_out || !k_pool || !v_pool || !block_tables)
+        return fail(MX_ERR_NULL, "mx_qkv_rope_append: null pointer");
+    if (Hq <= 0 || Hkv <= 0 || D <= 0 || D % 8 || max_pos <= 0 || block_size <= 0 || max_blocks <= 0 ||
+        num_pool_blocks <= 0)
+        return fail(MX_ERR_INVALID, "mx_qkv_rope_append: need positive sizes and D %% 8 == 0 (Hq=%d Hkv=%d D=%d)",
+                    Hq, Hkv, D);
+    if (qkv_stride % 8 || q_stride % 8 || kv_sblk % 8 || kv_shead % 8 || !glue::a16(qkv) || !glue::a16(q_out) ||
+        !glue::a16(k_pool) || !glue::a16(v_pool) || !aligned(rope, 8))
+        return fail(MX_ERR_ALIGNMENT, "mx_qkv_rope_append: rows need 16-byte alignment");
+    if (qkv_stride < (int64_t)(Hq + 2 * Hkv) * D || q_stride < (int64_t)Hq * D)
+        return fail(MX_ERR_INVALID, "mx_qkv_rope_append: row strides shorter than the rows");
+    glue::RopeAppendParams p{qkv, qkv_stride, Hq, Hkv, D, reinterpret_cast<const float2*>(rope), max_pos, positions,
+                             q_out, q_stride, k_pool, v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks,
+                             block_size, num_pool_blocks, err};
+    const int64_t total = (int64_t)B * (Hq + 2 * Hkv) * (D / 8);
+    hipLaunchKernelGGL(glue::qkv_rope_append_kernel, dim3((unsigned)ceil_div(total, glue::kThreads)),
+                       dim3(glue::kThreads), 0, as_stream(stream), p, total);
+    return check_launch("mx_qkv_rope_append");
+}
+
+extern "C" int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride,
+                              const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out,
+                              int64_t out_stride, uint16_t* residual_out, int64_t ro_stride, void* stream) {
+    clear_error();
+    if (M < 0) return fail(MX_ERR_INVALID, "mx_add_rmsnorm: M must be >= 0");
+    if (M == 0) return MX_OK;
+    if (!x || !weight || !out) return fail(MX_ERR_NULL, "mx_add_rmsnorm: null pointer");
+    if (H <= 0 || H % 8 || H > glue::kThreads * 8 * glue::kNormMaxChunks)
+        return fail(MX_ERR_INVALID, "mx_add_rmsnorm: need H %% 8 == 0 and H <= %d (H=%d)",
+                    glue::kThreads * 8 * glue::kNormMaxChunks, H);
+    if (x_stride % 8 || out_stride % 8 || (residual && r_stride % 8) || (residual_out && ro_stride % 8) ||
+        !glue::a16(x) || !glue::a16(weight) || !glue::a16(out) || (residual && !glue::a16(residual)) ||
+        (residual_out && !glue::a16(residual_out)))
+        return fail(MX_ERR_ALIGNMENT, "mx_add_rmsnorm: rows need 16-byte alignment");
+    hipLaunchKernelGGL(glue::add_rmsnorm_kernel, dim3(M), dim3(glue::kThreads), 0, as_stream(stream), x, x_stride,
+                       residual, r_stride, weight, H, eps, out, out_stride, residual_out, ro_stride);
+    return check_launch("mx_add_rmsnorm");
+}
+
+extern "C" int mx_silu_mul(const uint16_t* gate_up, int64_t gu_stride, int32_t M, int32_t I, uint16_t* out,
+                           int64_t out_stride, void* stream) {
+    clear_error();
+    if (M < 0) return fail(MX_ERR_INVALID, "mx_silu_mul: M must be >= 0");
+    if (M == 0) return MX_OK;
+    if (!gate_up || !out) return fail(MX_ERR_NULL, "mx_silu_mul: null pointer");
+    if (I <= 0 || I % 8) return fail(MX_ERR_INVALID, "mx_silu_mul: need I %% 8 == 0 (I=%d)", I);
+    if (gu_stride % 8 || out_stride % 8 || !glue::a16(gate_up) || !glue::a16(out))
+        return fail(MX_ERR_ALIGNMENT, "mx_silu_mul: rows need 16-byte alignment");
+    if (gu_stride < 2 * (int64_t)I) return fail(MX_ERR_INVALID, "mx_silu_mul: gate_up row stride < 2*I");
+    const int64_t total = (int64_t)M * (I / 8);
+    hipLaunchKernelGGL(glue::silu_mul_kernel, dim3((unsigned)ceil_div(total, glue::kThreads)), dim3(glue::kThreads),
+                       0, as_stream(stream), gate_up, gu_stride, I, out, out_stride, total);
+    return check_launch("mx_silu_mul");
+}

@@ -1,0 +1,153 @@
+"""Host wrappers of the decode-step glue kernels of libmxdecode.
+
+* :func:`kv_append` — scatter new K/V states into a layer of a
+  :class:`GpuKVBlockPool` (``GpuKVBlockPool.write_tokens_batch`` semantics,
+  ``runtime/phase2/paged_kv_kernel.py:176-227``) in one launch;
+* :func:`qkv_rope_append` — rotate q and k of a fused QKV projection output and
+  append k, v at each row's position (the HF decoder layer's
+  ``apply_rotary_pos_emb`` + ``BlockPagedBatchLayer.update`` write,
+  ``runtime/phase2/paged_kv_cache.py:121-157``);
+* :func:`add_rmsnorm` — residual add fused with RMSNorm;
+* :func:`silu_mul` — SwiGLU's ``silu(gate) * up``;
+* :func:`rope_table` — the fp32 ``(cos, sin)`` table the fused RoPE reads,
+  computed like transformers' default rotary embedding
+  (``inv_freq = theta ** -(2i / D)``, angle ``pos * inv_freq`` in fp32).
+
+All take device tensors and enqueue on the current stream; no call
+synchronises or allocates except for the returned outputs when ``out`` is
+omitted. Errors raise ``ValueError`` (bad arguments) or ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _hip
+
+
+def _i32(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    if t.dtype != torch.int32 or t.device != device or not t.is_contiguous():
+        t = t.to(device=device, dtype=torch.int32).contiguous()
+    return t
+
+
+def _rows16(t: torch.Tensor) -> torch.Tensor:
+    """2-D fp16 view with unit inner stride and 16-byte aligned rows (copy if needed)."""
+    if t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def rope_table(max_pos: int, head_dim: int, theta: float, device: torch.device | str) -> torch.Tensor:
+    """``[max_pos, head_dim // 2, 2]`` fp32 ``(cos, sin)`` of ``pos * theta ** -(2i / head_dim)``."""
+    half = head_dim // 2
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).to(torch.float32) / head_dim))
+    pos = torch.arange(max_pos, dtype=torch.float32)
+    ang = pos[:, None] * inv_freq[None, :half]
+    return torch.stack((ang.cos(), ang.sin()), dim=-1).contiguous().to(device)
+
+
+def kv_append(k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor, start_pos: torch.Tensor,
+              key_states: torch.Tensor, value_states: torch.Tensor, err: torch.Tensor | None = None) -> None:
+    """Write ``key/value_states [B, Hkv, T, D]`` at positions ``start_pos[b] + t`` of each row.
+
+    ``k_layer``/``v_layer`` are per-layer pool views ``[num_blocks, Hkv, bs, D]``.
+    Slots outside the table or the pool are skipped and flagged in ``err``
+    (an int32 device word, OR-ed with 1) when given.
+    """
+    _hip.require_device_tensor(key_states, "key_states")
+    dev = k_layer.device
+    if key_states.shape != value_states.shape or key_states.dim() != 4:
+        raise ValueError("key_states and value_states must both be [B, Hkv, T, D]")
+    if key_states.dtype != k_layer.dtype or k_layer.dtype != torch.float16:
+        raise ValueError("kv_append supports fp16 states and pools")
+    b, hkv, t, d = key_states.shape
+    nb, hkv_p, bs, d_p = k_layer.shape
+    if (hkv, d) != (hkv_p, d_p) or k_layer.stride() != v_layer.stride():
+        raise ValueError("states do not match the pool layout")
+    if k_layer.stride(3) != 1 or k_layer.stride(2) != d:
+        raise ValueError("pool layer views must be contiguous within a (block, kv-head) run")
+    if key_states.stride(3) != 1 or value_states.stride() != key_states.stride():
+        key_states = key_states.contiguous()
+        value_states = value_states.contiguous()
+    tables = _i32(block_tables, dev)
+    if tables.dim() != 2 or tables.shape[0] != b:
+        raise ValueError("block_tables must be [B, max_blocks]")
+    starts = _i32(start_pos.reshape(-1), dev)
+    lib = _hip.load()
+    _hip.check(lib.mx_kv_append(
+        key_states.data_ptr(), value_states.data_ptr(), key_states.stride(0), key_states.stride(1),
+        key_states.stride(2), b, t, hkv, d, tables.data_ptr(), tables.stride(0), int(tables.shape[1]),
+        starts.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), bs, nb,
+        err.data_ptr() if err is not None else None, _hip.stream_handle(dev)), "mx_kv_append")
+
+
+def qkv_rope_append(qkv: torch.Tensor, rope: torch.Tensor, positions: torch.Tensor, q_out: torch.Tensor,
+                    k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int,
+                    num_kv_heads: int, err: torch.Tensor | None = None) -> torch.Tensor:
+    """Rotate q, k of ``qkv [B, (Hq + 2 Hkv) * D]`` at ``positions [B]``; q -> ``q_out``, k, v -> the pool."""
+    _hip.require_device_tensor(qkv, "qkv")
+    dev = qkv.device
+    nb, hkv, bs, d = k_layer.shape
+    if hkv != num_kv_heads or qkv.shape[-1] != (num_heads + 2 * num_kv_heads) * d:
+        raise ValueError("qkv width does not match (Hq + 2 Hkv) * D of the pool")
+    if rope.dtype != torch.float32 or rope.dim() != 3 or rope.shape[1:] != (d // 2, 2) or not rope.is_contiguous():
+        raise ValueError("rope must be a contiguous fp32 [max_pos, D/2, 2] table")
+    if q_out.shape[-1] != num_heads * d:
+        raise ValueError("q_out must be [B, Hq * D]")
+    tables = _i32(block_tables, dev)
+    pos = _i32(positions.reshape(-1), dev)
+    qkv2 = _rows16(qkv.reshape(-1, qkv.shape[-1]))
+    b = int(qkv2.shape[0])
+    if tables.shape[0] != b or pos.shape[0] != b or q_out.reshape(-1, q_out.shape[-1]).shape[0] != b:
+        raise ValueError("batch dimension mismatch")
+    q2 = q_out.reshape(b, -1)
+    if q2.data_ptr() != q_out.data_ptr() or q2.stride(-1) != 1:
+        raise ValueError("q_out must be a row-major [B, Hq * D] buffer")
+    lib = _hip.load()
+    _hip.check(lib.mx_qkv_rope_append(
+        qkv2.data_ptr(), qkv2.stride(0), b, num_heads, num_kv_heads, d, rope.data_ptr(), int(rope.shape[0]),
+        pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0),
+        k_layer.stride(1), tables.data_ptr(), tables.stride(0), int(tables.shape[1]), bs, nb,
+        err.data_ptr() if err is not None else None, _hip.stream_handle(dev)), "mx_qkv_rope_append")
+    return q_out
+
+
+def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
+                out: torch.Tensor | None = None, residual_out: torch.Tensor | None = None) -> torch.Tensor:
+    """``h = x (+ residual)``; ``residual_out = h``; returns ``RMSNorm(h) * weight`` (fp16 ``[M, H]``)."""
+    _hip.require_device_tensor(x, "x")
+    if x.dtype != torch.float16 or weight.dtype != torch.float16:
+        raise ValueError("add_rmsnorm supports fp16")
+    x2 = _rows16(x.reshape(-1, x.shape[-1]))
+    m, h = x2.shape
+    r2 = _rows16(residual.reshape(m, h)) if residual is not None else None
+    out = torch.empty_like(x2) if out is None else out
+    o2 = out.view(m, h)
+    ro2 = residual_out.view(m, h) if residual_out is not None else None
+    w = weight.contiguous()
+    lib = _hip.load()
+    _hip.check(lib.mx_add_rmsnorm(
+        x2.data_ptr(), x2.stride(0), r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0,
+        w.data_ptr(), m, h, float(eps), o2.data_ptr(), o2.stride(0),
+        ro2.data_ptr() if ro2 is not None else None, ro2.stride(0) if ro2 is not None else 0,
+        _hip.stream_handle(x.device)), "mx_add_rmsnorm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate_up[:, :I]) * gate_up[:, I:]`` for fp16 ``gate_up [M, 2I]``."""
+    _hip.require_device_tensor(gate_up, "gate_up")
+    if gate_up.dtype != torch.float16:
+        raise ValueError("silu_mul supports fp16")
+    g2 = _rows16(gate_up.reshape(-1, gate_up.shape[-1]))
+    m, two_i = g2.shape
+    if two_i % 2:
+        raise ValueError("gate_up width must be even")
+    i = two_i // 2
+    out = torch.empty((m, i), dtype=torch.float16, device=gate_up.device) if out is None else out
+    o2 = out.view(m, i)
+    lib = _hip.load()
+    _hip.check(lib.mx_silu_mul(g2.data_ptr(), g2.stride(0), m, i, o2.data_ptr(), o2.stride(0),
+                               _hip.stream_handle(gate_up.device)), "mx_silu_mul")
+    return out

@@ -1,18 +1,29 @@
 """One batched decode step of an int8 (W8A16) decoder over the paged KV pool.
 
 This is the path ``TransformersBackend._paged_decode_step`` drives through an HF
-model (``runtime/phase2/worker_server.py:733-794``): per decoder layer the
-q/k/v, o, gate/up and down projections (the quantized-linear slot,
-``:194-205``), the K/V write of the new token into its block
-(``paged_kv_cache.py:121-170`` -> ``paged_kv_kernel.py:176-227``) and paged
-decode attention (``block_paged_attention.py:37-48``), then greedy argmax
-(``worker_server.py:786``). Projections and attention run on the HIP kernels
-of libmxdecode; normalisation, rotary embedding, the KV write and SwiGLU are
-torch glue on the same stream. Every tensor the step touches is allocated
-before the first step, so a whole step can be captured in one HIP graph.
+model (``runtime/phase2/worker_server.py:733-794``), without the HF module
+tree: per decoder layer the fused q/k/v, o, gate/up and down projections (the
+quantized-linear slot, ``:194-205``), the K/V write of the new token into its
+block (``paged_kv_cache.py:121-170`` -> ``paged_kv_kernel.py:176-227``) and
+paged decode attention (``block_paged_attention.py:37-48``), then greedy
+argmax (``worker_server.py:786``). Every op is a libmxdecode kernel on the
+current stream:
 
-Architecture is Llama / Qwen2 style: RMSNorm, fused QKV (optional bias, as in
-Qwen2), RoPE, GQA, fused gate||up with SiLU, untied int8 lm_head.
+    x = RMSNorm(h)                         mx_add_rmsnorm (fused with the residual add
+                                           of the previous layer's MLP)
+    qkv = x Wqkv^T (+b)                    mx_w8a16_linear
+    q, K/V slot <- RoPE(qkv), v            mx_qkv_rope_append
+    a = paged_attention(q, pool)           mx_paged_attn_decode
+    h += a Wo^T;  x = RMSNorm(h)           mx_w8a16_linear, mx_add_rmsnorm
+    gu = x Wgu^T;  m = silu(g) * u         mx_w8a16_linear, mx_silu_mul
+    h += m Wdown^T                         mx_w8a16_linear (+ the next add_rmsnorm)
+    logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, torch argmax
+
+Activations live in per-batch-size buffers allocated on the first step, so a
+whole step can be captured in one HIP graph and replayed. Architecture is
+Llama / Qwen2 style (pre-norm, rotate-half RoPE, GQA, SwiGLU, untied int8
+lm_head); :meth:`Int8DecodeModel.from_hf` loads the weights of an HF
+``LlamaForCausalLM`` / ``Qwen2ForCausalLM``.
 """
 
 from __future__ import annotations
@@ -22,6 +33,7 @@ from dataclasses import dataclass
 
 import torch
 
+from .decode_glue import add_rmsnorm, qkv_rope_append, rope_table, silu_mul
 from .int8_linear import int8_linear, pack_weight, quantize_weight
 from .paged_attention_hip import _decode as _paged_decode
 
@@ -64,43 +76,109 @@ class _Layer:
     down: tuple
 
 
-def _quantized(n: int, k: int, gen: torch.Generator, device: torch.device, std: float) -> tuple:
+@dataclass
+class _Buffers:
+    h: torch.Tensor       # residual stream [B, hidden]
+    x: torch.Tensor       # normalised input of the next projection [B, hidden]
+    qkv: torch.Tensor     # [B, qkv_out]
+    q: torch.Tensor       # rotated queries [B, heads * head_dim]
+    attn: torch.Tensor    # attention output [B, heads, 1, head_dim]
+    o: torch.Tensor       # [B, hidden]
+    gu: torch.Tensor      # [B, 2 * intermediate]
+    act: torch.Tensor     # [B, intermediate]
+    mlp: torch.Tensor     # [B, hidden]
+    logits: torch.Tensor  # [B, vocab]
+    attn_lens: torch.Tensor  # int32 [B]
+    err: torch.Tensor     # int32 [1], OR of the append kernels' error bits
+
+
+def _quantize(w: torch.Tensor, device: torch.device) -> tuple:
+    q, s = quantize_weight(w.to(device=device, dtype=torch.float32))
+    return pack_weight(q), s, int(w.shape[0])
+
+
+def _random_quantized(n: int, k: int, gen: torch.Generator, device: torch.device, std: float) -> tuple:
     w = torch.randn(n, k, generator=gen, device=device, dtype=torch.float32) * std
-    q, s = quantize_weight(w)
+    out = _quantize(w, device)
     del w
-    return pack_weight(q), s, n
+    return out
 
 
 class Int8DecodeModel:
-    """Random-init int8 decoder (weights quantized with the build's format on the device)."""
+    """int8 decoder for the native decode step: random init or weights loaded from HF."""
 
     def __init__(self, shape: DecoderShape, device: torch.device | str = "cuda", seed: int = 0, std: float = 0.02,
-                 layers: int | None = None) -> None:
+                 layers: int | None = None, max_positions: int = 32768, init: bool = True) -> None:
         self.shape = shape
         self.device = torch.device(device)
         self.n_layers = layers if layers is not None else shape.layers
+        self.rope = rope_table(max_positions, shape.head_dim, shape.rope_theta, self.device)
+        self._buffers: dict[int, _Buffers] = {}
+        self.layers: list[_Layer] = []
+        if not init:
+            return
         gen = torch.Generator(device=self.device).manual_seed(seed)
         s = shape
         self.embed = (torch.randn(s.vocab, s.hidden, generator=gen, device=self.device) * std).to(torch.float16)
-        self.layers: list[_Layer] = []
         for _ in range(self.n_layers):
-            qkv = _quantized(s.qkv_out, s.hidden, gen, self.device, std)
-            if s.qkv_bias:
-                qkv = (*qkv, (torch.randn(s.qkv_out, generator=gen, device=self.device) * std).to(torch.float16))
-            else:
-                qkv = (*qkv, None)
+            qkv = _random_quantized(s.qkv_out, s.hidden, gen, self.device, std)
+            bias = (torch.randn(s.qkv_out, generator=gen, device=self.device) * std).to(torch.float16) \
+                if s.qkv_bias else None
             self.layers.append(_Layer(
                 ln_in=torch.ones(s.hidden, dtype=torch.float16, device=self.device),
                 ln_post=torch.ones(s.hidden, dtype=torch.float16, device=self.device),
-                qkv=qkv,
-                o=(*_quantized(s.hidden, s.heads * s.head_dim, gen, self.device, std), None),
-                gate_up=(*_quantized(2 * s.intermediate, s.hidden, gen, self.device, std), None),
-                down=(*_quantized(s.hidden, s.intermediate, gen, self.device, std), None),
+                qkv=(*qkv, bias),
+                o=(*_random_quantized(s.hidden, s.heads * s.head_dim, gen, self.device, std), None),
+                gate_up=(*_random_quantized(2 * s.intermediate, s.hidden, gen, self.device, std), None),
+                down=(*_random_quantized(s.hidden, s.intermediate, gen, self.device, std), None),
             ))
         self.ln_final = torch.ones(s.hidden, dtype=torch.float16, device=self.device)
-        self.lm_head = (*_quantized(s.vocab, s.hidden, gen, self.device, std), None)
-        half = s.head_dim // 2
-        self.inv_freq = 1.0 / (s.rope_theta ** (torch.arange(0, half, device=self.device, dtype=torch.float32) / half))
+        self.lm_head = (*_random_quantized(s.vocab, s.hidden, gen, self.device, std), None)
+
+    @classmethod
+    def from_hf(cls, model, device: torch.device | str = "cuda", max_positions: int = 32768) -> "Int8DecodeModel":
+        """Quantize an HF ``LlamaForCausalLM`` / ``Qwen2ForCausalLM`` (fp32 weights) into this layout.
+
+        q/k/v are stacked into one projection (rows q, then k, then v) and
+        gate/up into one (gate rows first). Per-output-channel quantization is
+        row-wise, so each stacked weight quantizes exactly as its parts would.
+        Norms, biases and the embedding are stored in fp16; lm_head is int8.
+        """
+        cfg = model.config
+        heads = int(cfg.num_attention_heads)
+        head_dim = int(getattr(cfg, "head_dim", None) or cfg.hidden_size // heads)
+        rope = getattr(cfg, "rope_parameters", None) or {}
+        theta = float(rope.get("rope_theta", getattr(cfg, "rope_theta", 10000.0)))
+        attn0 = model.model.layers[0].self_attn
+        shape = DecoderShape(hidden=int(cfg.hidden_size), layers=int(cfg.num_hidden_layers), heads=heads,
+                             kv_heads=int(cfg.num_key_value_heads), head_dim=head_dim,
+                             intermediate=int(cfg.intermediate_size), vocab=int(cfg.vocab_size), rope_theta=theta,
+                             rms_eps=float(cfg.rms_norm_eps), qkv_bias=attn0.q_proj.bias is not None)
+        self = cls(shape, device=device, max_positions=max_positions, init=False)
+        dev = self.device
+
+        def f16(t):
+            return t.detach().to(device=dev, dtype=torch.float16).contiguous()
+
+        with torch.no_grad():
+            self.embed = f16(model.model.embed_tokens.weight)
+            for layer in model.model.layers:
+                at, mlp = layer.self_attn, layer.mlp
+                qkv_w = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], dim=0)
+                bias = None
+                if at.q_proj.bias is not None:
+                    bias = f16(torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias]))
+                self.layers.append(_Layer(
+                    ln_in=f16(layer.input_layernorm.weight),
+                    ln_post=f16(layer.post_attention_layernorm.weight),
+                    qkv=(*_quantize(qkv_w, dev), bias),
+                    o=(*_quantize(at.o_proj.weight, dev), None),
+                    gate_up=(*_quantize(torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], dim=0), dev), None),
+                    down=(*_quantize(mlp.down_proj.weight, dev), None),
+                ))
+            self.ln_final = f16(model.model.norm.weight)
+            self.lm_head = (*_quantize(model.lm_head.weight, dev), None)
+        return self
 
     # --- byte accounting (algorithmic HBM bytes of one step) -------------------
     def linear_bytes(self, batch: int) -> dict[str, int]:
@@ -117,66 +195,75 @@ class Int8DecodeModel:
             "lm_head": lb(s.vocab, s.hidden),
         }
 
-    # --- glue -------------------------------------------------------------------
-    def _rms(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.shape.rms_eps)
-        return w * xf.to(torch.float16)
+    def buffers(self, batch: int) -> _Buffers:
+        buf = self._buffers.get(batch)
+        if buf is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("decode buffers must be allocated before graph capture; run one eager step")
+            s, dev, f16 = self.shape, self.device, torch.float16
 
-    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        # x [B, H, D], pos [B] int -> rotate-half RoPE (HF Llama/Qwen2 convention).
-        freqs = pos.float().unsqueeze(-1) * self.inv_freq.unsqueeze(0)  # [B, D/2]
-        emb = torch.cat((freqs, freqs), dim=-1)
-        cos = emb.cos().to(x.dtype).unsqueeze(1)
-        sin = emb.sin().to(x.dtype).unsqueeze(1)
-        half = x.shape[-1] // 2
-        rot = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
-        return x * cos + rot * sin
+            def e(*shape):
+                return torch.empty(*shape, dtype=f16, device=dev)
+
+            buf = _Buffers(h=e(batch, s.hidden), x=e(batch, s.hidden), qkv=e(batch, s.qkv_out),
+                           q=e(batch, s.heads * s.head_dim), attn=e(batch, s.heads, 1, s.head_dim),
+                           o=e(batch, s.hidden), gu=e(batch, 2 * s.intermediate), act=e(batch, s.intermediate),
+                           mlp=e(batch, s.hidden), logits=e(batch, s.vocab),
+                           attn_lens=torch.zeros(batch, dtype=torch.int32, device=dev),
+                           err=torch.zeros(1, dtype=torch.int32, device=dev))
+            self._buffers[batch] = buf
+        return buf
+
+    def error_flag(self) -> int:
+        """OR of the KV-append error bits since the buffers were created (one host sync)."""
+        flag = 0
+        for buf in self._buffers.values():
+            flag |= int(buf.err.item())
+        return flag
 
     def step(self, tokens: torch.Tensor, pool, block_tables: torch.Tensor, seq_lens: torch.Tensor,
-             timers: dict | None = None) -> torch.Tensor:
-        """Decode one token per row. ``seq_lens`` holds the KV length BEFORE this token and is
-        advanced in place. Returns the greedy next tokens ``[B]`` (int64, on device)."""
+             timers: dict | None = None, return_logits: bool = False):
+        """Decode one token per row. ``seq_lens`` (int32) holds the KV length BEFORE this token
+        (= the token's position) and is advanced in place. Returns the greedy next tokens
+        ``[B]`` (int64, on device), and the fp16 logits ``[B, vocab]`` with ``return_logits``."""
         s = self.shape
         bsz = int(tokens.shape[0])
-        bs = pool.block_size_tokens
-        pos = seq_lens.to(torch.int64)
-        rows = torch.arange(bsz, device=self.device)
-        phys = block_tables.to(torch.int64)[rows, torch.div(pos, bs, rounding_mode="floor")]
-        off = pos % bs
-        attn_lens = (seq_lens + 1).to(torch.int32)
-        h = self.embed.index_select(0, tokens)
-        nq, nkv = s.heads * s.head_dim, s.kv_heads * s.head_dim
+        buf = self.buffers(bsz)
+        if seq_lens.dtype != torch.int32 or block_tables.dtype != torch.int32:
+            raise ValueError("seq_lens and block_tables must be int32 device tensors")
+        torch.add(seq_lens, 1, out=buf.attn_lens)
+        torch.index_select(self.embed, 0, tokens, out=buf.h)
+        eps = s.rms_eps
         for li, layer in enumerate(self.layers):
-            x = self._rms(h, layer.ln_in)
-            qkv = self._lin(x, layer.qkv, timers, "qkv")
-            q = self._rope(qkv[:, :nq].view(bsz, s.heads, s.head_dim), pos)
-            k = self._rope(qkv[:, nq:nq + nkv].view(bsz, s.kv_heads, s.head_dim), pos)
-            v = qkv[:, nq + nkv:].view(bsz, s.kv_heads, s.head_dim)
+            if li == 0:
+                add_rmsnorm(buf.h, layer.ln_in, eps, out=buf.x)
+            else:
+                add_rmsnorm(buf.mlp, layer.ln_in, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
+            self._lin(buf.x, layer.qkv, buf.qkv, timers, "qkv")
             k_layer = pool.k_layer_view(li)
             v_layer = pool.v_layer_view(li)
-            k_layer[phys, :, off, :] = k
-            v_layer[phys, :, off, :] = v
+            qkv_rope_append(buf.qkv, self.rope, seq_lens, buf.q, k_layer, v_layer, block_tables, s.heads,
+                            s.kv_heads, err=buf.err)
             ev = self._tick(timers, "attn")
-            attn = _paged_decode(q.unsqueeze(2), k_layer, v_layer, block_tables, attn_lens, s.head_dim**-0.5,
-                                 s.group)
+            _paged_decode(buf.q.view(bsz, s.heads, 1, s.head_dim), k_layer, v_layer, block_tables, buf.attn_lens,
+                          s.head_dim ** -0.5, s.group, out=buf.attn)
             self._tock(timers, "attn", ev)
-            h = h + self._lin(attn.view(bsz, nq), layer.o, timers, "o")
-            x = self._rms(h, layer.ln_post)
-            gu = self._lin(x, layer.gate_up, timers, "gate_up")
-            a = torch.nn.functional.silu(gu[:, :s.intermediate]) * gu[:, s.intermediate:]
-            h = h + self._lin(a, layer.down, timers, "down")
-        x = self._rms(h, self.ln_final)
-        logits = self._lin(x, self.lm_head, timers, "lm_head")
+            self._lin(buf.attn.view(bsz, -1), layer.o, buf.o, timers, "o")
+            add_rmsnorm(buf.o, layer.ln_post, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
+            self._lin(buf.x, layer.gate_up, buf.gu, timers, "gate_up")
+            silu_mul(buf.gu, out=buf.act)
+            self._lin(buf.act, layer.down, buf.mlp, timers, "down")
+        add_rmsnorm(buf.mlp, self.ln_final, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
+        self._lin(buf.x, self.lm_head, buf.logits, timers, "lm_head")
         seq_lens.add_(1)
-        return logits.argmax(dim=-1)
+        nxt = buf.logits.argmax(dim=-1)
+        return (nxt, buf.logits) if return_logits else nxt
 
-    def _lin(self, x, w, timers, name):
+    def _lin(self, x, w, out, timers, name):
         packed, scale, n, bias = w
         ev = self._tick(timers, name)
-        y = int8_linear(x, packed, scale, bias, n)
+        int8_linear(x, packed, scale, bias, n, out=out)
         self._tock(timers, name, ev)
-        return y
 
     @staticmethod
     def _tick(timers, name):

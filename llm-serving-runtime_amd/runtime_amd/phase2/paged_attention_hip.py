@@ -120,7 +120,8 @@ def workspace_error_flag(device: torch.device | None = None) -> int:
 
 
 def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor,
-            seq_lens: torch.Tensor, scaling: float, num_kv_groups: int) -> torch.Tensor:
+            seq_lens: torch.Tensor, scaling: float, num_kv_groups: int, out: torch.Tensor | None = None
+            ) -> torch.Tensor:
     bsz, hq, q_len, d = query.shape
     if q_len != 1:
         raise ValueError("paged decode expects q_len=1")
@@ -144,7 +145,11 @@ def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, b
     if seq_lens.dtype != torch.int32 or seq_lens.device != query.device or not seq_lens.is_contiguous():
         seq_lens = seq_lens.to(device=query.device, dtype=torch.int32).contiguous()
     max_blocks = int(block_tables.shape[1])
-    out = torch.empty((bsz, hq, 1, d), dtype=query.dtype, device=query.device)
+    if out is None:
+        out = torch.empty((bsz, hq, 1, d), dtype=query.dtype, device=query.device)
+    elif (tuple(out.shape) != (bsz, hq, 1, d) or out.dtype != query.dtype or out.stride(3) != 1
+          or out.device != query.device):
+        raise ValueError("out must be a [B, heads, 1, dim] tensor of the query dtype with unit inner stride")
     if bsz == 0:
         return out
     key = (bsz, hq, hkv, d, max_blocks, bs, _CHUNK_TOKENS)

@@ -124,12 +124,15 @@ class GpuKVBlockPool:
 
     def write_tokens_batch(self, layer_idx: int, block_tables: torch.Tensor, start_positions: torch.Tensor,
                            key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        """Vectorised KV write: tables ``[B, max_blocks]``, starts ``[B]``, states ``[B, Hkv, kv_len, D]``.
+        """KV write: tables ``[B, max_blocks]``, starts ``[B]``, states ``[B, Hkv, kv_len, D]``.
 
-        Same semantics as the reference (``:176-227``), written as one indexed
-        store per call instead of a per-token loop. Outside graph capture the
-        block table bounds are checked on the host as in the reference
-        (``:221-222``).
+        Same semantics as the reference (``:176-227``). On a device pool it is
+        one ``mx_kv_append`` launch (no per-token loop); outside graph capture
+        the table bounds are checked on the host first and raise ``IndexError``
+        as in the reference (``:221-222``), at the cost of one host sync.
+        During capture the kernel skips out-of-range slots instead. A pool on
+        the CPU (used by host-side tests of the cache bookkeeping) takes an
+        indexed torch store.
         """
         if key_states.shape != value_states.shape:
             raise ValueError("key_states and value_states must match shape")
@@ -137,31 +140,40 @@ class GpuKVBlockPool:
         kv_len = int(key_states.shape[-2])
         if block_tables.shape[0] != batch_size or start_positions.shape[0] != batch_size:
             raise ValueError("batch dimension mismatch in write_tokens_batch")
+        if kv_len == 0 or batch_size == 0:
+            return
         self._ensure_pools()
         assert self._k_pool is not None and self._v_pool is not None
         device = self.device
-        capturing = bool(device.type == "cuda" and torch.cuda.is_available() and torch.cuda.is_current_stream_capturing())
+        on_device = device.type == "cuda"
+        capturing = bool(on_device and torch.cuda.is_current_stream_capturing())
         bs = self.block_size_tokens
-        tables = block_tables.to(device=device, dtype=torch.int64)
-        pos = start_positions.to(device=device, dtype=torch.int64).view(-1, 1) + torch.arange(
-            kv_len, device=device, dtype=torch.int64).view(1, -1)  # [B, T]
-        logical = torch.div(pos, bs, rounding_mode="floor")
         if not capturing:
-            if kv_len > 0 and int(logical.max().item()) >= tables.shape[1]:
+            tables = block_tables.to(device=device, dtype=torch.int64)
+            pos = start_positions.to(device=device, dtype=torch.int64).view(-1, 1) + torch.arange(
+                kv_len, device=device, dtype=torch.int64).view(1, -1)  # [B, T]
+            logical = torch.div(pos, bs, rounding_mode="floor")
+            if int(logical.max().item()) >= tables.shape[1] or int(pos.min().item()) < 0:
                 raise IndexError("block table underrun during batched write")
-        physical = torch.gather(tables, 1, logical)  # [B, T]
-        offset = pos % bs
-        if not capturing:
+            physical = torch.gather(tables, 1, logical)  # [B, T]
             if int(physical.min().item()) < 0 or int(physical.max().item()) >= self.shape.num_blocks:
                 raise IndexError("physical block id out of range during batched write")
             self._touch_blocks(physical)
-        # pool[physical, layer, :, offset, :] = states[b, :, t, :]
-        k_src = key_states.to(self.dtype).permute(0, 2, 1, 3).reshape(-1, key_states.shape[1], key_states.shape[3])
-        v_src = value_states.to(self.dtype).permute(0, 2, 1, 3).reshape(-1, value_states.shape[1], value_states.shape[3])
         k_layer = self._k_pool[:, layer_idx]
         v_layer = self._v_pool[:, layer_idx]
-        k_layer[physical.reshape(-1), :, offset.reshape(-1), :] = k_src
-        v_layer[physical.reshape(-1), :, offset.reshape(-1), :] = v_src
+        if on_device:
+            from .decode_glue import kv_append
+
+            kv_append(k_layer, v_layer, block_tables, start_positions, key_states.to(self.dtype),
+                      value_states.to(self.dtype))
+            return
+        offset = (pos % bs).reshape(-1)
+        phys = physical.reshape(-1)
+        # pool[physical, layer, :, offset, :] = states[b, :, t, :]
+        k_layer[phys, :, offset, :] = key_states.to(self.dtype).permute(0, 2, 1, 3).reshape(
+            -1, key_states.shape[1], key_states.shape[3])
+        v_layer[phys, :, offset, :] = value_states.to(self.dtype).permute(0, 2, 1, 3).reshape(
+            -1, value_states.shape[1], value_states.shape[3])
 
     def copy_blocks(self, src_block_ids: list[int], dst_block_ids: list[int]) -> None:
         """Copy full physical blocks (all layers) from src ids to dst ids (``:233-250``)."""

@@ -51,6 +51,13 @@ QWEN2_05B = dict(hidden_size=896, num_hidden_layers=24, num_attention_heads=14, 
                  max_position_embeddings=32768, tie_word_embeddings=False)
 
 
+# Llama-3-8B-shaped decoder (the headline bench shape): 32 layers, hidden 4096,
+# 32 Q / 8 KV heads, head_dim 128, SwiGLU 14336, vocab 128256, theta 5e5, no biases.
+LLAMA3_8B = dict(hidden_size=4096, num_hidden_layers=32, num_attention_heads=32, num_key_value_heads=8,
+                 intermediate_size=14336, vocab_size=128256, rope_theta=500000.0, rms_norm_eps=1e-5,
+                 max_position_embeddings=32768, tie_word_embeddings=False)
+
+
 def random_qwen2(seed: int = 0, **overrides):
     """A random-init ``Qwen2ForCausalLM`` in fp32 on the CPU (eager attention).
 
@@ -60,14 +67,27 @@ def random_qwen2(seed: int = 0, **overrides):
     the biases, which would leave the bias path untested.)
     """
     from transformers import Qwen2Config, Qwen2ForCausalLM
-    from transformers.initialization import no_init_weights
 
     kwargs = dict(QWEN2_05B)
     kwargs.update(overrides)
-    config = Qwen2Config(**kwargs)
+    return _random_model(Qwen2ForCausalLM, Qwen2Config(**kwargs), seed)
+
+
+def random_llama(seed: int = 0, **overrides):
+    """A random-init ``LlamaForCausalLM`` (Llama-3-8B shape unless overridden), as :func:`random_qwen2`."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    kwargs = dict(LLAMA3_8B)
+    kwargs.update(overrides)
+    return _random_model(LlamaForCausalLM, LlamaConfig(**kwargs), seed)
+
+
+def _random_model(model_cls, config, seed: int):
+    from transformers.initialization import no_init_weights
+
     config._attn_implementation = "eager"
     with no_init_weights():
-        model = Qwen2ForCausalLM(config)
+        model = model_cls(config)
     rng = np.random.default_rng(seed)
     with torch.no_grad():
         for name, p in model.named_parameters():
@@ -115,6 +135,14 @@ def teacher_forced_logits(model: nn.Module, prompt: torch.Tensor, generated: tor
     ids = torch.cat([prompt, generated[:-1]]).view(1, -1)
     out = model(input_ids=ids, use_cache=False, logits_to_keep=n)
     return out.logits[0].float()
+
+
+@torch.no_grad()
+def prefill_kv(model: nn.Module, prompt: torch.Tensor) -> tuple[list[tuple[torch.Tensor, torch.Tensor]], torch.Tensor]:
+    """Prompt forward: per layer ``(keys, values)`` ``[Hkv, P, D]`` (after RoPE, fp32) and the last logits ``[V]``."""
+    out = model(input_ids=prompt.reshape(1, -1).to(torch.long).cpu(), use_cache=True, logits_to_keep=1)
+    kv = [(layer.keys[0], layer.values[0]) for layer in out.past_key_values.layers]
+    return kv, out.logits[0, -1].float()
 
 
 @torch.no_grad()

@@ -1,0 +1,236 @@
+"""Glue kernels (KV append, fused RoPE + append, add + RMSNorm, SiLU * up) vs the CPU oracle.
+
+Bars: index/byte work (where a token lands, what is copied) bit-exact, and
+so is the fp16 residual sum (one rounding of an exact fp32 sum). Arithmetic
+outputs stay within the stated atol 1e-2 / rtol 1e-2 and within a few fp16
+ulps of the oracle, which rounds at the same points:
+
+* RoPE (one rounding of an fp32 result; oracle from float64): 1 ulp;
+* RMSNorm and SiLU * up round twice (``n = fp16(h * r)`` then ``fp16(n * w)``;
+  ``s = fp16(silu(g))`` then ``fp16(s * u)``). The reduction order (RMSNorm) or
+  ``exp`` (SiLU) can move the first rounding by 1 ulp of ``n``; scaled by ``w``
+  that shifts the exact product by less than 2 ulps of the output
+  (``|n w| >= |w| 2^e(n)``), so the bar is 2 ulps.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import glue as og
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _ulps(a: torch.Tensor, b: torch.Tensor) -> int:
+    """Largest distance in fp16 units in the last place between two fp16-valued tensors."""
+    def key(t):
+        i = t.to(torch.float16).view(torch.int16).to(torch.int32)
+        return torch.where(i < 0, -(i & 0x7FFF), i)
+    return int((key(a.cpu()) - key(b.cpu())).abs().max())
+
+
+def _close(dev: torch.Tensor, ref: torch.Tensor, max_ulps: int = 1) -> None:
+    torch.testing.assert_close(dev.float().cpu(), ref.float().cpu(), atol=1e-2, rtol=1e-2)
+    assert _ulps(dev, ref) <= max_ulps
+
+
+def _pool(nb, hkv, bs, d, layers=2, seed=0):
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=bs, num_layers=layers, num_kv_heads=hkv, head_dim=d,
+                          dtype=torch.float16, device=DEV)
+    pool._ensure_pools()
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    pool._k_pool.copy_(torch.randn(pool._k_pool.shape, generator=g, device=DEV).half())
+    pool._v_pool.copy_(torch.randn(pool._v_pool.shape, generator=g, device=DEV).half())
+    return pool
+
+
+@pytest.mark.parametrize("T,transposed", [(1, False), (1, True), (7, True), (19, False)])
+def test_kv_append_bit_exact(T, transposed):
+    from runtime_amd.phase2.decode_glue import kv_append
+
+    nb, hkv, bs, d, b = 64, 2, 16, 64, 3
+    pool = _pool(nb, hkv, bs, d)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(T)).tolist()
+    tables = torch.tensor([perm[0:4], perm[4:8], perm[8:12]], dtype=torch.int32)
+    start = torch.tensor([0, 17, 40], dtype=torch.int32)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    if transposed:  # HF's [B, T, Hkv, D] projection viewed as [B, Hkv, T, D]
+        ks = torch.randn(b, T, hkv, d, generator=g, device=DEV).half().transpose(1, 2)
+        vs = torch.randn(b, T, hkv, d, generator=g, device=DEV).half().transpose(1, 2)
+    else:
+        ks = torch.randn(b, hkv, T, d, generator=g, device=DEV).half()
+        vs = torch.randn(b, hkv, T, d, generator=g, device=DEV).half()
+    k_ref = pool.k_layer_view(1).cpu().clone()
+    v_ref = pool.v_layer_view(1).cpu().clone()
+    assert og.append_tokens(k_ref, v_ref, tables, start.tolist(), ks.cpu(), vs.cpu()) == []
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kv_append(pool.k_layer_view(1), pool.v_layer_view(1), tables.to(DEV), start.to(DEV), ks, vs, err=err)
+    assert torch.equal(pool.k_layer_view(1).cpu(), k_ref)
+    assert torch.equal(pool.v_layer_view(1).cpu(), v_ref)
+    assert int(err.item()) == 0
+
+
+def test_kv_append_skips_and_flags_out_of_range_slots():
+    from runtime_amd.phase2.decode_glue import kv_append
+
+    nb, hkv, bs, d = 16, 1, 16, 64
+    pool = _pool(nb, hkv, bs, d)
+    tables = torch.tensor([[3, 4], [5, 99]], dtype=torch.int32)  # row 1: bad physical id for block 1
+    start = torch.tensor([30, 14], dtype=torch.int32)  # row 0: positions 30..33 pass the 2-block table
+    ks = torch.randn(2, hkv, 4, d, device=DEV).half()
+    k_ref = pool.k_layer_view(0).cpu().clone()
+    v_ref = pool.v_layer_view(0).cpu().clone()
+    skipped = og.append_tokens(k_ref, v_ref, tables, start.tolist(), ks.cpu(), ks.cpu())
+    assert len(skipped) == 4
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kv_append(pool.k_layer_view(0), pool.v_layer_view(0), tables.to(DEV), start.to(DEV), ks, ks, err=err)
+    assert torch.equal(pool.k_layer_view(0).cpu(), k_ref) and torch.equal(pool.v_layer_view(0).cpu(), v_ref)
+    assert int(err.item()) == 1
+
+
+def test_pool_write_tokens_batch_uses_kernel_and_keeps_reference_errors():
+    nb, hkv, bs, d = 32, 2, 16, 128
+    pool = _pool(nb, hkv, bs, d)
+    tables = torch.tensor([[7, 2, 9], [1, 0, 4]], dtype=torch.int32, device=DEV)
+    start = torch.tensor([5, 30], dtype=torch.int64, device=DEV)
+    ks = torch.randn(2, hkv, 3, d, device=DEV).half()
+    vs = torch.randn(2, hkv, 3, d, device=DEV).half()
+    k_ref = pool.k_layer_view(0).cpu().clone()
+    v_ref = pool.v_layer_view(0).cpu().clone()
+    og.append_tokens(k_ref, v_ref, tables.cpu(), start.tolist(), ks.cpu(), vs.cpu())
+    pool.write_tokens_batch(0, tables, start, ks, vs)
+    assert torch.equal(pool.k_layer_view(0).cpu(), k_ref) and torch.equal(pool.v_layer_view(0).cpu(), v_ref)
+    with pytest.raises(IndexError):
+        pool.write_tokens_batch(0, tables, torch.tensor([5, 47], device=DEV), ks, vs)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])
+def test_qkv_rope_append(hq, hkv, d):
+    from runtime_amd.phase2.decode_glue import qkv_rope_append, rope_table
+
+    b, nb, bs, theta, max_pos = 9, 80, 16, 5e5, 4096
+    pool = _pool(nb, hkv, bs, d, seed=1)
+    rope = rope_table(max_pos, d, theta, DEV)
+    g = torch.Generator().manual_seed(2)
+    qkv = torch.randn(b, (hq + 2 * hkv) * d, generator=g).half()
+    positions = torch.tensor([0, 1, 15, 16, 100, 511, 512, 2000, max_pos - 1], dtype=torch.int32)
+    tables = torch.randperm(nb, generator=g)[:b * 8].to(torch.int32).view(b, 8)  # 8 distinct blocks a row
+    keep = torch.tensor([int(p) // bs < 8 for p in positions])  # rows whose slot fits the table
+    q_out = torch.empty(b, hq * d, dtype=torch.float16, device=DEV)
+    k_before = pool.k_layer_view(1).cpu().clone()
+    v_before = pool.v_layer_view(1).cpu().clone()
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    qkv_rope_append(qkv.to(DEV), rope, positions.to(DEV), q_out, pool.k_layer_view(1), pool.v_layer_view(1),
+                    tables.to(DEV), hq, hkv, err=err)
+    assert int(err.item()) == (0 if bool(keep.all()) else 1)
+
+    q_ref = og.rope_rotate_half(qkv[:, :hq * d].view(b, hq, d).float(), positions, theta)
+    _close(q_out.view(b, hq, d), q_ref.float())
+    k_rot = og.rope_rotate_half(qkv[:, hq * d:(hq + hkv) * d].view(b, hkv, d).float(), positions, theta)
+    v_new = qkv[:, (hq + hkv) * d:].view(b, hkv, d)
+    k_after = pool.k_layer_view(1).cpu()
+    v_after = pool.v_layer_view(1).cpu()
+    touched = torch.zeros(nb, bs, dtype=torch.bool)
+    for r in range(b):
+        p = int(positions[r])
+        if not keep[r]:
+            continue
+        phys = int(tables[r, p // bs])
+        touched[phys, p % bs] = True
+        _close(k_after[phys, :, p % bs], k_rot[r].float())
+        assert torch.equal(v_after[phys, :, p % bs], v_new[r])
+    # Nothing else in the layer changed.
+    mask = ~touched[:, None, :, None].expand_as(k_after)
+    assert torch.equal(k_after[mask], k_before[mask]) and torch.equal(v_after[mask], v_before[mask])
+
+
+def test_qkv_rope_append_position_outside_table():
+    from runtime_amd.phase2.decode_glue import qkv_rope_append, rope_table
+
+    hq, hkv, d = 4, 2, 64
+    pool = _pool(8, hkv, 16, d)
+    rope = rope_table(32, d, 1e4, DEV)
+    qkv = torch.randn(2, (hq + 2 * hkv) * d, device=DEV).half()
+    q_out = torch.full((2, hq * d), 7.0, dtype=torch.float16, device=DEV)
+    before = pool.k_layer_view(0).cpu().clone()
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    qkv_rope_append(qkv, rope, torch.tensor([32, 3], device=DEV), q_out, pool.k_layer_view(0),
+                    pool.v_layer_view(0), torch.tensor([[1, 2], [3, 4]], dtype=torch.int32, device=DEV), hq, hkv,
+                    err=err)
+    assert int(err.item()) == 2
+    assert float(q_out[0].abs().max()) == 0.0
+    k_after = pool.k_layer_view(0).cpu()
+    assert torch.equal(k_after[1], before[1])  # row 0 wrote nothing
+    assert not torch.equal(k_after[3, :, 3], before[3, :, 3])  # row 1 did
+
+
+def test_rope_table_matches_transformers():
+    from transformers import Qwen2Config
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RotaryEmbedding
+
+    from runtime_amd.phase2.decode_glue import rope_table
+
+    cfg = Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2, rope_theta=1e6)
+    pos = torch.arange(0, 4096, 37)
+    cos, sin = Qwen2RotaryEmbedding(cfg)(torch.zeros(1, dtype=torch.float32), pos.view(1, -1))
+    tab = rope_table(4096, 64, 1e6, DEV).cpu()[pos]
+    torch.testing.assert_close(tab[..., 0], cos[0, :, :32], atol=1e-6, rtol=0)
+    torch.testing.assert_close(tab[..., 1], sin[0, :, :32], atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("m,h", [(1, 4096), (32, 4096), (16, 896), (100, 1024)])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_add_rmsnorm(m, h, with_residual):
+    from runtime_amd.phase2.decode_glue import add_rmsnorm
+
+    g = torch.Generator().manual_seed(m + h)
+    x = (3 * torch.randn(m, h, generator=g)).half()
+    res = torch.randn(m, h, generator=g).half() if with_residual else None
+    w = (1 + 0.2 * torch.randn(h, generator=g)).half()
+    ref_out, ref_h = og.add_rmsnorm(x, w, 1e-5, residual=res)
+    res_out = torch.empty(m, h, dtype=torch.float16, device=DEV) if with_residual else None
+    out = add_rmsnorm(x.to(DEV), w.to(DEV), 1e-5, residual=res.to(DEV) if res is not None else None,
+                      residual_out=res_out)
+    _close(out, ref_out, max_ulps=2)
+    if with_residual:
+        assert torch.equal(res_out.cpu().float(), ref_h)
+
+
+def test_add_rmsnorm_in_place_aliases():
+    from runtime_amd.phase2.decode_glue import add_rmsnorm
+
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(32, 4096, generator=g).half()
+    res = torch.randn(32, 4096, generator=g).half()
+    w = (1 + 0.2 * torch.randn(4096, generator=g)).half()
+    ref_out, ref_h = og.add_rmsnorm(x, w, 1e-6, residual=res)
+    xd, rd = x.to(DEV), res.to(DEV)
+    add_rmsnorm(xd, w.to(DEV), 1e-6, residual=rd, out=xd, residual_out=rd)
+    _close(xd, ref_out, max_ulps=2)
+    assert torch.equal(rd.cpu().float(), ref_h)
+
+
+@pytest.mark.parametrize("m,i", [(1, 14336), (32, 14336), (16, 4864), (3, 8)])
+def test_silu_mul(m, i):
+    from runtime_amd.phase2.decode_glue import silu_mul
+
+    g = torch.Generator().manual_seed(i)
+    gu = (4 * torch.randn(m, 2 * i, generator=g)).half()
+    _close(silu_mul(gu.to(DEV)), og.silu_mul(gu), max_ulps=2)
+
+
+def test_glue_rejects_bad_arguments():
+    from runtime_amd.phase2.decode_glue import add_rmsnorm, silu_mul
+
+    with pytest.raises(ValueError):
+        add_rmsnorm(torch.randn(2, 12, device=DEV).half(), torch.ones(12, device=DEV).half(), 1e-6)  # H % 8
+    with pytest.raises(ValueError):
+        silu_mul(torch.randn(2, 12, device=DEV).half())  # I = 6, not a multiple of 8
+    with pytest.raises(ValueError):
+        add_rmsnorm(torch.randn(2, 8), torch.ones(8), 1e-6)  # CPU tensors

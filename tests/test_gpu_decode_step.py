@@ -1,0 +1,132 @@
+"""The native decode step (``Int8DecodeModel.step``: int8 linears, fused glue, paged
+attention) against the HF model oracle holding the same weights.
+
+The model is an HF ``Qwen2ForCausalLM`` / ``LlamaForCausalLM`` with random
+weights (``oracle.model``), loaded with ``Int8DecodeModel.from_hf`` (q/k/v and
+gate/up stacked, every projection and the lm_head int8). Each row's prompt is
+run by the fp32 oracle; its K/V (after RoPE) are written into the paged pool
+at the row's shuffled blocks and its greedy token starts the native decode.
+After ``STEPS`` native steps the oracle is teacher-forced on the native tokens
+and every step's logits and token are compared, with the same rules as the
+HF-path greedy test: ``max|dL| <= max(LOGIT_ATOL, 1.25 * torch-fp16 error)``
+per row and token mismatches only at near ties (at most 2 % of steps).
+
+Shapes: Qwen2-0.5B dims (biases, head_dim 64, GQA 7) and Llama-3-8B dims
+(hidden 4096, head_dim 128, GQA 4, intermediate 14336), 2 layers each, at the
+bench batch sizes; the Llama case uses a 32768-token vocabulary to keep the
+CPU oracle short (the lm_head kernel is the same int8 linear at any N).
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+
+import pytest
+import torch
+
+from oracle import glue as og
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_ATOL = 1e-2
+YARDSTICK_SLACK = 1.25
+MAX_TIE_FRACTION = 0.02
+BLOCK_SIZE = 16
+STEPS = 32
+
+
+def _run(hf, batch, lo, hi, seed, graph):
+    from runtime_amd.phase2.decode_step import Int8DecodeModel
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    dev = torch.device("cuda:0")
+    cfg = hf.config
+    ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
+    torch16 = copy.deepcopy(ref).to(device=dev, dtype=torch.float16).eval()
+    native = Int8DecodeModel.from_hf(hf, device=dev, max_positions=4096)
+    s = native.shape
+    assert (s.qkv_bias, s.group) == (cfg.model_type == "qwen2", cfg.num_attention_heads // cfg.num_key_value_heads)
+
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g) for n in lens]
+    need = [math.ceil((n + STEPS + 1) / BLOCK_SIZE) for n in lens]
+    nb = sum(need) + 7
+    perm = torch.randperm(nb, generator=g)
+    tables = torch.zeros(batch, max(need), dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = perm[at:at + n].to(torch.int32)
+        at += n
+
+    # Prompt K/V from the oracle into a host copy of the pool, then to the device.
+    pool_k = torch.zeros(nb, s.layers, s.kv_heads, BLOCK_SIZE, s.head_dim, dtype=torch.float16)
+    pool_v = torch.zeros_like(pool_k)
+    first = []
+    for b, prompt in enumerate(prompts):
+        kv, logits = om.prefill_kv(ref, prompt)
+        first.append(int(logits.argmax()))
+        for li, (k, v) in enumerate(kv):
+            assert og.append_tokens(pool_k[:, li], pool_v[:, li], tables[b:b + 1], [0], k.unsqueeze(0),
+                                    v.unsqueeze(0)) == []
+    pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=BLOCK_SIZE, num_layers=s.layers, num_kv_heads=s.kv_heads,
+                          head_dim=s.head_dim, dtype=torch.float16, device=dev)
+    pool._ensure_pools()
+    pool._k_pool.copy_(pool_k)
+    pool._v_pool.copy_(pool_v)
+
+    tables_d = tables.to(dev)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    tokens = torch.tensor(first, dtype=torch.int64, device=dev)
+    out_tokens, out_logits = [], []
+    print(f"[step] {cfg.model_type} layers={s.layers} batch={batch} lens={lo}..{hi} graph={graph}", flush=True)
+    step_graph = None
+    for k in range(STEPS):
+        if graph and k == 1:  # capture after one eager step sized the buffers
+            step_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(step_graph):
+                nxt_g, logits_g = native.step(tokens, pool, tables_d, seq_lens, return_logits=True)
+        if step_graph is not None:
+            step_graph.replay()
+            nxt, logits = nxt_g, logits_g
+        else:
+            nxt, logits = native.step(tokens, pool, tables_d, seq_lens, return_logits=True)
+        out_logits.append(logits.float().cpu())
+        out_tokens.append(nxt.cpu())
+        tokens.copy_(nxt)
+    assert native.error_flag() == 0
+    assert seq_lens.cpu().tolist() == [n + STEPS for n in lens]
+    toks = torch.stack(out_tokens, dim=1)  # [B, STEPS]: predictions of t1..tSTEPS
+    logits = torch.stack(out_logits, dim=1)
+
+    results = []
+    for b in range(batch):
+        gen = torch.cat([torch.tensor([first[b]]), toks[b]])
+        ref_logits = om.teacher_forced_logits(ref, prompts[b], gen)[1:]
+        ids = torch.cat([prompts[b], gen[:-1]]).view(1, -1).to(dev)
+        with torch.no_grad():
+            t16 = torch16(input_ids=ids, use_cache=False, logits_to_keep=STEPS + 1).logits[0, 1:].float().cpu()
+        err = float((logits[b] - ref_logits).abs().max())
+        err16 = float((t16 - ref_logits).abs().max())
+        allowed = max(LOGIT_ATOL, YARDSTICK_SLACK * err16)
+        agree = om.greedy_agreement(ref_logits, toks[b], tie_tol=2 * allowed)
+        results.append((b, err, allowed, agree))
+        print(f"[step] row {b} prompt {lens[b]}: max|dL| native {err:.3e} torch16 {err16:.3e} "
+              f"mismatches {agree['mismatches']}/{agree['steps']}", flush=True)
+    for b, err, allowed, agree in results:
+        assert err <= allowed, f"row {b}: logits off by {err:.3e} (allowed {allowed:.3e})"
+        assert agree["ties_ok"], f"row {b}: mismatch outside the near-tie band {agree}"
+    ties = sum(r[3]["mismatches"] for r in results)
+    assert ties <= MAX_TIE_FRACTION * batch * STEPS
+
+
+def test_native_step_qwen2_shape():
+    _run(om.random_qwen2(seed=1, num_hidden_layers=2), batch=16, lo=64, hi=256, seed=1, graph=False)
+
+
+@pytest.mark.timeout(600)
+def test_native_step_llama3_shape_graph_replay():
+    hf = om.random_llama(seed=2, num_hidden_layers=2, vocab_size=32768)
+    _run(hf, batch=32, lo=48, hi=160, seed=2, graph=True)
