@@ -99,15 +99,21 @@ int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, c
  * out: fp16 [B, Hq, D] with strides (o_sb, o_sh, 1)
  * num_pool_blocks: block ids outside [0, num_pool_blocks) are skipped and
  *      recorded in the workspace error word (see mx_paged_attn_error_offset)
- * chunk_tokens: split-K chunk (multiple of 16, at most 4096); 0 picks one
- *      from B, Hkv and max_blocks (256..2048 tokens, about one workgroup per
- *      CU). Must be the value the workspace was sized for.
- *      Rows longer than one chunk are merged by a second, small kernel on
- *      the same stream. At most 1024 chunks per row (max_blocks*block_size).
+ * chunk_tokens: split granularity. All (sequence, kv-head) tiles of 16 tokens
+ *      form one sequence that is cut into W equal ranges, one per wave, so
+ *      every wave streams the same K/V bytes whatever the mix of lengths.
+ *      chunk_tokens > 0 (a multiple of 16, at most 1024) sets ranges of about
+ *      that many tokens when every row is at the table width
+ *      (max_blocks * block_size); 0 picks 2048 waves (one round of resident
+ *      waves on MI355X), fewer when ranges would be shorter than 4 tiles. A
+ *      range never exceeds 64 tiles (more waves are used instead). Must be
+ *      the value the workspace was sized for. A
+ *      second, small kernel on the same stream merges the ranges of a
+ *      sequence that more than one wave touched.
  * Supported: D in {64, 128}; block_size in {16, 32}; Hq = G * Hkv, G in 1..8.
  * The workspace holds fp32 split partials and the error word; zero it once at
  * allocation so the error word starts clear. Concurrent calls must not share
- * a workspace.
+ * a workspace. out rows must be 16-byte aligned (o_sb, o_sh multiples of 8).
  * ------------------------------------------------------------------------- */
 size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                      int32_t block_size, int32_t chunk_tokens);

@@ -5,14 +5,20 @@
 // split kernel (:245-336), the B=1 direct kernel (:338-412) and the log-sum-exp
 // combine (:414-457), for any batch and any mix of context lengths.
 //
-// Kernel 1 (partial): one workgroup (4 waves) per (token chunk, kv-head,
-// sequence). The G = Hq/Hkv query heads of a kv-head share every K/V byte the
-// workgroup reads, so K/V are fetched once per kv-head (the reference grid
-// (B, Hq) re-reads them G times, :179-181). Chunks are fixed-size runs of
-// tokens, so a long row gets more workgroups than a short one (ragged-aware
-// split-K, where the reference splits only B=1 rows, :82-87, :537-552).
+// Work decomposition. A segment is one (sequence, kv-head) pair; it holds
+// ceil(seq_len / 16) tiles of 16 tokens. The G = Hq/Hkv query heads of a
+// kv-head share every K/V byte of the segment, so K/V are read once per
+// kv-head (the reference grid (B, Hq) re-reads them G times, :179-181). All
+// segments, row-major over (sequence, kv-head), form one sequence of T tiles
+// that is cut into W = min(workers, T) equal contiguous ranges, one per wave
+// ("worker"): worker w owns tiles [floor(w T / W), floor((w + 1) T / W)), at
+// least one. Every wave thus
+// streams the same number of K/V bytes whatever the mix of context lengths, so
+// the chip drains evenly (fixed per-sequence chunks leave a long tail when
+// lengths are ragged, and the reference splits only B=1 rows, :82-87,
+// :537-552).
 //
-// Per 16-token tile a wave:
+// Kernel 1 (split): a wave walks its range; for each segment piece it
 //   * loads K rows as the A operand of v_mfma_f32_16x16x32_f16 (16 tokens x
 //     32 dims per instruction, one 128-bit load per lane), with the G query
 //     heads (zero padded to 16) as the B operand -> scores S[token][head];
@@ -20,18 +26,21 @@
 //     pre-multiplied by scale*log2(e); exp2(x*log2 e) == exp(x));
 //   * shares p[token][head] and the rescale factor through a per-wave LDS
 //     slot and accumulates P.V on the VALU from V rows loaded as contiguous
-//     1 KiB runs (lane: 8 dims of RPL-strided tokens), fp32 accumulation.
-// A wave keeps two tiles in flight (the next tile's K/V loads are issued
-// before the current tile is computed) and reads its block ids for the whole
-// chunk with one vector load up front. Waves merge in LDS. A row covered by
-// one chunk is written directly; otherwise the chunk's fp32 partial
-// (m, l, acc[G][D]) goes to the workspace.
+//     1 KiB runs, fp32 accumulation;
+//   * keeps P tiles of K/V loads in flight and reads the piece's block ids
+//     with one vector load (a range never exceeds 64 tiles).
+// A piece that is a whole segment is written as fp16 output; otherwise its
+// fp32 partial (m, l, acc[G][D]) goes to workspace slot w + s. Pairs (w, s)
+// that overlap form a monotone staircase, so w + s is unique and at most
+// W + B*Hkv - 1 slots exist. The workers holding a segment's first and last
+// tile record themselves in seg_w, so the merge needs no prefix sums.
 //
-// Kernel 2 (combine): one workgroup per (kv-head, sequence) with more than one
-// chunk applies the log-sum-exp merge and writes fp16 output. Splitting the
-// merge into its own launch keeps kernel 1 free of device-scope fences: on
-// gfx950 a release/acquire at agent scope writes back and invalidates the XCD's
-// L2, which serialises thousands of workgroups.
+// Kernel 2 (merge): one workgroup per segment reads its worker span, applies
+// the log-sum-exp merge of the partials and writes fp16 output (zeros for an
+// empty row). Each thread owns output elements and issues all of its loads
+// at once, so a merge costs two dependent memory round trips. Keeping the merge in its own launch keeps kernel
+// 1 free of device-scope fences: on gfx950 a release/acquire at agent scope
+// writes back and invalidates the XCD's L2.
 #include "common.h"
 
 namespace mx {
@@ -47,38 +56,94 @@ struct Params {
     int64_t bt_sb;
     int max_blocks;
     const int32_t* seq_lens;
-    int Hkv;
+    int B, Hkv;
     int num_pool_blocks;
     float scale_log2e;
     _Float16* out;
     int64_t o_sb, o_sh;
-    float* part_ml;   // [B*Hkv*max_chunks][G][2]  (m, l) on the exp2 scale
-    float* part_acc;  // [B*Hkv*max_chunks][G][D]
+    float* part_ml;   // [slots][G][2]  (m, l) on the exp2 scale
+    float* part_acc;  // [slots][G][D]
+    int* seg_w;       // [B*Hkv][2]: workers holding the first and the last tile of a segment
     int* err;         // error word
-    int max_chunks;
-    int chunk_tiles;
+    int workers;
 };
 
 constexpr int kWaves = 4;
-constexpr int kTile = 16;  // tokens per MFMA tile
-constexpr int kDefaultChunkTokens = 256;
-constexpr int kMaxChunkTokens = kWaves * 64 * kTile;  // a wave prefetches at most 64 block ids
-constexpr int kMaxChunks = 1024;                      // combine kernel keeps chunk weights in LDS
+constexpr int kTile = 16;               // tokens per MFMA tile
+constexpr int kMaxRangeTiles = 64;      // a worker's range fits one vector of block ids
+constexpr int kDefaultWorkers = 2048;   // 256 CUs x 8 resident waves on MI355X
+constexpr int kMinDefaultTiles = 4;     // default ranges are at least this long when T allows
+constexpr int kMaxChunkTokens = kMaxRangeTiles * kTile;
 
 __device__ __forceinline__ half8v load_half8(const _Float16* p) {
     return __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(p));
 }
 
-// Number of 16-token chunks of a row, shared by both kernels.
+// Tiles of row b (bounded by the table width) and its effective length.
 template <int BS>
-__device__ __forceinline__ void row_extent(int S, int max_blocks, int chunk_tiles, int& s_eff, int& ntiles,
-                                           int& nchunks) {
+__device__ __forceinline__ int row_tiles(const Params& p, int b, int& s_eff) {
+    const int S = p.seq_lens[b];
     int nblk = S > 0 ? (S + BS - 1) / BS : 0;
-    if (nblk > max_blocks) nblk = max_blocks;
+    if (nblk > p.max_blocks) nblk = p.max_blocks;
     s_eff = S < nblk * BS ? S : nblk * BS;
-    ntiles = (s_eff + kTile - 1) / kTile;
-    nchunks = (ntiles + chunk_tiles - 1) / chunk_tiles;
+    return (s_eff + kTile - 1) / kTile;
 }
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+// Total tiles of all segments: Hkv * sum_b tiles(b).
+template <int BS>
+__device__ __forceinline__ int64_t total_tiles(const Params& p, int lane) {
+    int64_t sum = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        int s_eff, n = 0;
+        if (b0 + lane < p.B) n = row_tiles<BS>(p, b0 + lane, s_eff);
+        sum += wave_sum_i(n);
+    }
+    return sum * p.Hkv;
+}
+
+struct Seg {
+    int b, ntiles;
+    int64_t row_start;  // global index of tile 0 of (b, kv-head 0)
+};
+
+// The row whose tiles contain global tile index x (x < total).
+template <int BS>
+__device__ __forceinline__ Seg locate(const Params& p, int64_t x, int lane) {
+    int64_t base = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        int s_eff, n = 0;
+        const bool valid = b0 + lane < p.B;
+        if (valid) n = row_tiles<BS>(p, b0 + lane, s_eff);
+        const int incl = wave_incl_scan(n, lane);
+        const int64_t chunk_total = (int64_t)__builtin_amdgcn_readlane(incl, 63) * p.Hkv;
+        if (x < base + chunk_total) {
+            const int excl = incl - n;
+            const bool le = valid && base + (int64_t)excl * p.Hkv <= x;
+            const int bl = __builtin_popcountll(__builtin_amdgcn_ballot_w64(le)) - 1;
+            return Seg{b0 + bl, __builtin_amdgcn_readlane(n, bl),
+                       base + (int64_t)__builtin_amdgcn_readlane(excl, bl) * p.Hkv};
+        }
+        base += chunk_total;
+    }
+    return Seg{0, 0, 0};  // unreachable for x < total
+}
+
+__device__ __forceinline__ int64_t range_lo(int64_t w, int64_t T, int W) { return w * T / W; }
 
 template <int KK, int NL>
 struct TileRegs {
@@ -94,7 +159,7 @@ constexpr int pa_depth(int D, int G) {
 }
 
 template <int D, int BS, int G>
-__global__ __launch_bounds__(kWaves * 64) void decode_partial_kernel(Params p) {
+__global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
     constexpr int KK = D / 32;       // MFMA k-steps over the head dim
     constexpr int LPR = D / 8;       // lanes per token row when loading V
     constexpr int RPL = 64 / LPR;    // token rows per V load instruction
@@ -103,283 +168,376 @@ __global__ __launch_bounds__(kWaves * 64) void decode_partial_kernel(Params p) {
     constexpr int P = pa_depth(D, G);
     const float kNegInf = -__builtin_huge_valf();
 
-    const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int worker = blockIdx.x * kWaves + wave;
     const int g = lane >> 4, r = lane & 15;
-    const int h0 = kvh * G;
-
-    int s_eff, ntiles, nchunks;
-    row_extent<BS>(p.seq_lens[b], p.max_blocks, p.chunk_tiles, s_eff, ntiles, nchunks);
-
-    _Float16* out_row = p.out + (int64_t)b * p.o_sb + (int64_t)h0 * p.o_sh;
-    if (nchunks == 0) {  // empty row: defined as a zero output
-        if (chunk == 0) {
-            for (int idx = tid; idx < G * D; idx += kWaves * 64)
-                out_row[(int64_t)(idx / D) * p.o_sh + idx % D] = (_Float16)0.0f;
-        }
-        return;
-    }
-    if (chunk >= nchunks) return;
-    const int t_begin = chunk * p.chunk_tiles;
-    const int t_end = (t_begin + p.chunk_tiles) < ntiles ? (t_begin + p.chunk_tiles) : ntiles;
-    const int t_first = t_begin + wave;
-    const int nj = t_first < t_end ? (t_end - t_first + kWaves - 1) / kWaves : 0;  // tiles of this wave
 
     __shared__ float s_p[kWaves][kTile][17];
     __shared__ float s_alpha[kWaves][16];
-    __shared__ float s_m[kWaves][G];
-    __shared__ float s_l[kWaves][G];
-    __shared__ float s_acc[kWaves][G][D];
 
-    // Block ids of this wave's tiles: lane j holds the id of tile t_first + 4*j;
-    // an id outside the pool becomes -1 (tile skipped, error recorded).
-    const int32_t* bt_row = p.bt + (int64_t)b * p.bt_sb;
-    int my_pb = 0;
-    if (lane < nj) {
-        my_pb = bt_row[(t_first + kWaves * lane) / TPB];
-        if ((unsigned)my_pb >= (unsigned)p.num_pool_blocks) {  // never read outside the pool
-            atomicOr(p.err, 1);
-            my_pb = -1;
-        }
-    }
-
-    // B operand: query head r (zero past G), dims 32*kk + 8*g + [0, 8).
-    half8v qf[KK];
-    if (r < G) {
-        const _Float16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h0 + r) * p.q_sh + 8 * g;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) qf[kk] = load_half8(qp + 32 * kk);
+    // Up to 64 rows: one read of seq_lens per wave, reused to locate every piece.
+    const bool one_pass = p.B <= 64;
+    int n_lane = 0, s_eff_lane = 0, incl_lane = 0;
+    int64_t T;
+    if (one_pass) {
+        if (lane < p.B) n_lane = row_tiles<BS>(p, lane, s_eff_lane);
+        incl_lane = wave_incl_scan(n_lane, lane);
+        T = (int64_t)__builtin_amdgcn_readlane(incl_lane, 63) * p.Hkv;
     } else {
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) qf[kk] = (_Float16)0.0f;
+        T = total_tiles<BS>(p, lane);
     }
+    const int W = T < p.workers ? (int)T : p.workers;  // every worker gets >= 1 tile
+    if (worker >= W) return;
+    const int64_t hi = range_lo(worker + 1, T, W);
+    int64_t x = range_lo(worker, T, W);
 
-    float m_run = kNegInf;  // running max of head r (same in all 4 lane groups)
-    float l_run = 0.0f;     // partial denominator over this lane's tokens
-    float acc[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
-
-    const _Float16* kbase = p.k + (int64_t)kvh * p.kv_shead;
-    const _Float16* vbase = p.v + (int64_t)kvh * p.kv_shead;
     const int vrow = lane / LPR, vcol = (lane % LPR) * 8;
     const int koff = r * D + 8 * g;
     const int voff = vrow * D + vcol;
 
-    // Loads are unconditional: past the wave's last tile the index is clamped
-    // (an L2 hit) and a skipped block reads block 0; only the compute below is
-    // predicated, by wave-uniform flags, so waits count exact stages.
-    auto load_tile = [&](int j, TileRegs<KK, NL>& tr) {
-        const int jc = j < nj ? j : nj - 1;
-        const int pb = __builtin_amdgcn_readlane(my_pb, jc);
-        const int t = t_first + kWaves * jc;
-        const int64_t base = (int64_t)(pb < 0 ? 0 : pb) * p.kv_sblk + (t % TPB) * kTile * D;
-        const _Float16* kt = kbase + base;
-        const _Float16* vt = vbase + base;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_half8(kt + koff + 32 * kk);
-#pragma unroll
-        for (int jj = 0; jj < NL; ++jj) tr.v[jj] = load_half8(vt + voff + jj * RPL * D);
-    };
-
-    auto compute_tile = [&](int j, const TileRegs<KK, NL>& tr) {
-        const int t = t_first + kWaves * j;
-        float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(tr.k[kk], qf[kk], s, 0, 0, 0);
-        // s[i] = score of token t*16 + 4g + i for head r.
-        const int tok0 = t * kTile + 4 * g;
-        float sc[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < s_eff) ? s[i] * p.scale_log2e : kNegInf;
-        const float mx = xor_max_16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        float psum = 0.0f;
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float pi = __builtin_amdgcn_exp2f(sc[i] - m_new);
-            s_p[wave][4 * g + i][r] = pi;
-            psum += pi;
+    while (x < hi) {
+        Seg sg;
+        if (one_pass) {
+            const int excl = incl_lane - n_lane;
+            const bool le = lane < p.B && (int64_t)excl * p.Hkv <= x;
+            const int bl = __builtin_popcountll(__builtin_amdgcn_ballot_w64(le)) - 1;
+            sg = Seg{bl, __builtin_amdgcn_readlane(n_lane, bl), (int64_t)__builtin_amdgcn_readlane(excl, bl) * p.Hkv};
+        } else {
+            sg = locate<BS>(p, x, lane);
         }
-        l_run = l_run * alpha + psum;
-        const bool rescale = __builtin_amdgcn_ballot_w64(m_new != m_run) != 0;
-        m_run = m_new;
-        if (g == 0) s_alpha[wave][r] = alpha;
-        __builtin_amdgcn_wave_barrier();
-        // P.V on the VALU: this lane owns dims vcol..vcol+7 of tokens jj*RPL + vrow.
-        if (rescale) {
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float a = s_alpha[wave][h];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] *= a;
+        const int b = sg.b, nt = sg.ntiles;
+        if (nt <= 0) {  // cannot happen for x < T; stop rather than divide by zero
+            atomicOr(p.err, 4);
+            break;
+        }
+        const int kvh = (int)((x - sg.row_start) / nt);
+        const int t0 = (int)((x - sg.row_start) % nt);
+        const int t1 = (int64_t)(nt - t0) < hi - x ? nt : (int)(t0 + (hi - x));
+        const int nj = t1 - t0;  // <= kMaxRangeTiles because W >= ceil(T_max / 64)
+        if (nj > kMaxRangeTiles) {
+            atomicOr(p.err, 4);
+            break;
+        }
+        x += nj;
+        int s_eff;
+        if (one_pass) s_eff = __builtin_amdgcn_readlane(s_eff_lane, b);
+        else row_tiles<BS>(p, b, s_eff);
+        const int h0 = kvh * G;
+
+        // Block ids of the piece: lane j holds the id of tile t0 + j; an id outside
+        // the pool becomes -1 (tile skipped, error recorded).
+        const int32_t* bt_row = p.bt + (int64_t)b * p.bt_sb;
+        int my_pb = 0;
+        if (lane < nj) {
+            my_pb = bt_row[(t0 + lane) / TPB];
+            if ((unsigned)my_pb >= (unsigned)p.num_pool_blocks) {  // never read outside the pool
+                atomicOr(p.err, 1);
+                my_pb = -1;
             }
         }
-#pragma unroll
-        for (int jj = 0; jj < NL; ++jj) {
-            const int tok = jj * RPL + vrow;
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float pj = s_p[wave][tok][h];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pj, (float)tr.v[jj][e], acc[h][e]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-    };
 
-    if (nj > 0) {
-        TileRegs<KK, NL> st[P];
+        // B operand: query head r (zero past G), dims 32*kk + 8*g + [0, 8).
+        half8v qf[KK];
+        if (r < G) {
+            const _Float16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h0 + r) * p.q_sh + 8 * g;
 #pragma unroll
-        for (int s = 0; s < P; ++s) load_tile(s, st[s]);
-        for (int j0 = 0; j0 < nj; j0 += P) {
+            for (int kk = 0; kk < KK; ++kk) qf[kk] = load_half8(qp + 32 * kk);
+        } else {
 #pragma unroll
-            for (int s = 0; s < P; ++s) {
-                const int j = j0 + s;
-                if (j < nj && __builtin_amdgcn_readlane(my_pb, j) >= 0) compute_tile(j, st[s]);
-                load_tile(j + P, st[s]);
-            }
+            for (int kk = 0; kk < KK; ++kk) qf[kk] = (_Float16)0.0f;
         }
-    }
 
-    // Wave totals: l over the 4 lane groups, acc over the token groups.
-    l_run = xor_sum_16_32(l_run);
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = acc[h][e];
-            if (LPR == 8) v = xor8_sum(v);
-            acc[h][e] = xor_sum_16_32(v);
-        }
-    if (g == 0 && r < G) {
-        s_m[wave][r] = m_run;
-        s_l[wave][r] = l_run;
-    }
-    if (lane < LPR) {
+        float m_run = kNegInf;  // running max of head r (same in all 4 lane groups)
+        float l_run = 0.0f;     // partial denominator over this lane's tokens
+        float acc[G][8];
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s_acc[wave][h][vcol + e] = acc[h][e];
-    }
-    __syncthreads();
+            for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 
-    const int64_t pslot = ((int64_t)b * p.Hkv + kvh) * p.max_chunks + chunk;
-    for (int idx = tid; idx < G * D; idx += kWaves * 64) {
-        const int h = idx / D, d = idx % D;
-        float mw = s_m[0][h];
+        const _Float16* kbase = p.k + (int64_t)kvh * p.kv_shead;
+        const _Float16* vbase = p.v + (int64_t)kvh * p.kv_shead;
+
+        // Loads are unconditional: past the piece's last tile the index is clamped
+        // (an L2 hit) and a skipped block reads block 0; only the compute below is
+        // predicated, by wave-uniform flags, so waits count exact stages.
+        auto load_tile = [&](int j, TileRegs<KK, NL>& tr) {
+            const int jc = j < nj ? j : nj - 1;
+            const int pb = __builtin_amdgcn_readlane(my_pb, jc);
+            const int t = t0 + jc;
+            const int64_t base = (int64_t)(pb < 0 ? 0 : pb) * p.kv_sblk + (t % TPB) * kTile * D;
+            const _Float16* kt = kbase + base;
+            const _Float16* vt = vbase + base;
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) mw = fmaxf(mw, s_m[w][h]);
-        float lw = 0.0f, aw = 0.0f;
+            for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_half8(kt + koff + 32 * kk);
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float f = exp2f(s_m[w][h] - mw);
-            lw += f * s_l[w][h];
-            aw += f * s_acc[w][h][d];
-        }
-        if (nchunks == 1) {
-            out_row[(int64_t)h * p.o_sh + d] = (_Float16)(aw / lw);
-        } else {
-            p.part_acc[(pslot * G + h) * D + d] = aw;
-            if (d == 0) {
-                p.part_ml[(pslot * G + h) * 2 + 0] = mw;
-                p.part_ml[(pslot * G + h) * 2 + 1] = lw;
+            for (int jj = 0; jj < NL; ++jj) tr.v[jj] = load_half8(vt + voff + jj * RPL * D);
+        };
+
+        auto compute_tile = [&](int j, const TileRegs<KK, NL>& tr) {
+            const int t = t0 + j;
+            float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(tr.k[kk], qf[kk], s, 0, 0, 0);
+            // s[i] = score of token t*16 + 4g + i for head r.
+            const int tok0 = t * kTile + 4 * g;
+            float sc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < s_eff) ? s[i] * p.scale_log2e : kNegInf;
+            const float mx = xor_max_16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            float psum = 0.0f;
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pi = __builtin_amdgcn_exp2f(sc[i] - m_new);
+                s_p[wave][4 * g + i][r] = pi;
+                psum += pi;
             }
+            l_run = l_run * alpha + psum;
+            const bool rescale = __builtin_amdgcn_ballot_w64(m_new != m_run) != 0;
+            m_run = m_new;
+            if (g == 0) s_alpha[wave][r] = alpha;
+            __builtin_amdgcn_wave_barrier();
+            // P.V on the VALU: this lane owns dims vcol..vcol+7 of tokens jj*RPL + vrow.
+            if (rescale) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float a = s_alpha[wave][h];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[h][e] *= a;
+                }
+            }
+#pragma unroll
+            for (int jj = 0; jj < NL; ++jj) {
+                const int tok = jj * RPL + vrow;
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float pj = s_p[wave][tok][h];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pj, (float)tr.v[jj][e], acc[h][e]);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        };
+
+        {
+            TileRegs<KK, NL> st[P];
+#pragma unroll
+            for (int s = 0; s < P; ++s) load_tile(s, st[s]);
+            for (int j0 = 0; j0 < nj; j0 += P) {
+#pragma unroll
+                for (int s = 0; s < P; ++s) {
+                    const int j = j0 + s;
+                    if (j < nj && __builtin_amdgcn_readlane(my_pb, j) >= 0) compute_tile(j, st[s]);
+                    load_tile(j + P, st[s]);
+                }
+            }
+        }
+
+        // Wave totals: l over the 4 lane groups, acc over the token-row groups.
+        l_run = xor_sum_16_32(l_run);
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float v = acc[h][e];
+                if (LPR == 8) v = xor8_sum(v);
+                acc[h][e] = xor_sum_16_32(v);
+            }
+        const bool whole = t0 == 0 && t1 == nt;
+        const int64_t seg = (int64_t)b * p.Hkv + kvh;
+        const int64_t slot = worker + seg;
+        if (lane == 0) {
+            if (t0 == 0) p.seg_w[2 * seg] = worker;
+            if (t1 == nt) p.seg_w[2 * seg + 1] = worker;
+        }
+        if (lane < LPR) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float lh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_run), h));
+                if (whole) {
+                    half8v o;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] = (_Float16)(acc[h][e] / lh);
+                    *reinterpret_cast<uint4*>(p.out + (int64_t)b * p.o_sb + (int64_t)(h0 + h) * p.o_sh + vcol) =
+                        __builtin_bit_cast(uint4, o);
+                } else {
+                    float4v* dst = reinterpret_cast<float4v*>(p.part_acc + (slot * G + h) * D + vcol);
+                    dst[0] = float4v{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+                    dst[1] = float4v{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+                }
+            }
+        }
+        if (!whole && g == 0 && r < G) {
+            p.part_ml[(slot * G + r) * 2 + 0] = m_run;
+            p.part_ml[(slot * G + r) * 2 + 1] = l_run;
         }
     }
 }
 
-// Log-sum-exp merge of the chunk partials of one (kv-head, sequence).
+// Log-sum-exp merge of the partials of one (kv-head, sequence); zeros for an empty row.
+// Workers seg_w[s] .. seg_w[s + 1] cut segment s, each with a partial at slot w + s.
 template <int D, int BS, int G>
-__global__ __launch_bounds__(256) void decode_combine_kernel(Params p) {
+__global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     const int kvh = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x;
-    int s_eff, ntiles, nchunks;
-    row_extent<BS>(p.seq_lens[b], p.max_blocks, p.chunk_tiles, s_eff, ntiles, nchunks);
-    if (nchunks <= 1) return;
-    __shared__ float s_w[kMaxChunks][G];
-    __shared__ float s_inv_l[G];
-    const int64_t base = ((int64_t)b * p.Hkv + kvh) * p.max_chunks;
-    if (tid < G) {
-        const int h = tid;
-        float mg = -__builtin_huge_valf();
-        for (int c = 0; c < nchunks; ++c) mg = fmaxf(mg, p.part_ml[((base + c) * G + h) * 2]);
-        float lg = 0.0f;
-        for (int c = 0; c < nchunks; ++c) {
-            const float f = exp2f(p.part_ml[((base + c) * G + h) * 2] - mg);
-            s_w[c][h] = f;
-            lg += f * p.part_ml[((base + c) * G + h) * 2 + 1];
-        }
-        s_inv_l[h] = 1.0f / lg;
-    }
-    __syncthreads();
+    const int64_t s = (int64_t)b * p.Hkv + kvh;
+    int s_eff;
+    const int nt = row_tiles<BS>(p, b, s_eff);
+    const int w0 = p.seg_w[2 * s], w1 = p.seg_w[2 * s + 1];
     _Float16* out_row = p.out + (int64_t)b * p.o_sb + (int64_t)(kvh * G) * p.o_sh;
-    for (int idx = tid; idx < G * D; idx += 256) {
+    if (nt == 0) {
+        for (int idx = tid; idx < G * D; idx += 256) out_row[(int64_t)(idx / D) * p.o_sh + idx % D] = (_Float16)0.0f;
+        return;
+    }
+    if (w0 == w1) return;  // one worker held the whole segment and wrote the output
+    // One online pass over the pieces, U at a time, for all EPT output elements
+    // of this thread together: every load of a batch is issued before the first
+    // is used (indices clamped, values masked), so a batch costs one memory
+    // round trip and a segment cut by at most U workers needs one batch.
+    constexpr int U = 16;
+    constexpr int EPT = (G * D + 255) / 256;
+    const int np = w1 - w0 + 1;
+    const float kNegInf = -__builtin_huge_valf();
+    float mg[EPT], l[EPT], a[EPT];
+    const float* mlp[EPT];
+    const float* accp[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int idx = tid + e * 256 < G * D ? tid + e * 256 : G * D - 1;
         const int h = idx / D, d = idx % D;
-        float a = 0.0f;
-        for (int c = 0; c < nchunks; ++c) a += s_w[c][h] * p.part_acc[((base + c) * G + h) * D + d];
-        out_row[(int64_t)h * p.o_sh + d] = (_Float16)(a * s_inv_l[h]);
+        mlp[e] = p.part_ml + (((int64_t)w0 + s) * G + h) * 2;
+        accp[e] = p.part_acc + (((int64_t)w0 + s) * G + h) * D + d;
+        mg[e] = kNegInf;
+        l[e] = 0.0f;
+        a[e] = 0.0f;
+    }
+    for (int i0 = 0; i0 < np; i0 += U) {
+        float mv[EPT][U], lv[EPT][U], av[EPT][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + u < np ? i0 + u : np - 1;
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                mv[e][u] = mlp[e][i * G * 2];
+                lv[e][u] = mlp[e][i * G * 2 + 1];
+                av[e][u] = accp[e][i * G * D];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            float mc = kNegInf;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (i0 + u < np) mc = fmaxf(mc, mv[e][u]);
+            const float mn = fmaxf(mg[e], mc);
+            if (mn == kNegInf) continue;  // only skipped tiles so far
+            const float r = exp2f(mg[e] - mn);
+            l[e] *= r;
+            a[e] *= r;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (i0 + u < np) {
+                    const float f = exp2f(mv[e][u] - mn);
+                    l[e] += f * lv[e][u];
+                    a[e] += f * av[e][u];
+                }
+            }
+            mg[e] = mn;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int idx = tid + e * 256;
+        if (idx < G * D)
+            out_row[(int64_t)(idx / D) * p.o_sh + idx % D] = (_Float16)(l[e] > 0.0f ? a[e] / l[e] : 0.0f);
     }
 }
 
 struct Layout {
-    size_t err, ml, acc, total;
-    int max_chunks, chunk_tokens;
+    size_t err, segw, ml, acc, total;
+    int workers;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Default chunk: the largest of 2048/1024/512/256 tokens that still gives about
-// one workgroup per CU when rows are, on average, half the table width.
-// Larger chunks amortise each workgroup's start-up and the merge; smaller ones
-// keep a few long rows spread over the chip. Host-only: no seq_lens read.
-static int resolve_chunk_tokens(int chunk_tokens, int B, int Hkv, int max_blocks, int block_size) {
-    if (chunk_tokens > 0) return chunk_tokens;
-    const int64_t half_row = ((int64_t)max_blocks * block_size + 1) / 2;
-    for (int ct = 2048; ct > kDefaultChunkTokens; ct /= 2) {
-        if ((int64_t)B * Hkv * ceil_div(half_row, ct) >= 256) return ct;
+// Number of workers. T_max (every row at the table width) bounds the real tile
+// count, so W >= ceil(T_max / 64) keeps each range within one vector of block
+// ids. chunk_tokens > 0 asks for ranges of about that many tokens at T_max;
+// 0 picks kDefaultWorkers (one round of resident waves on the chip), fewer
+// when that would make ranges shorter than kMinDefaultTiles tiles.
+static int resolve_workers(int chunk_tokens, int B, int Hkv, int max_blocks, int block_size) {
+    const int64_t row_tiles_max = ceil_div((int64_t)max_blocks * block_size, kTile);
+    const int64_t t_max = (int64_t)B * Hkv * row_tiles_max;
+    const int64_t floor_w = ceil_div(t_max, kMaxRangeTiles);
+    int64_t w;
+    if (chunk_tokens > 0) {
+        w = ceil_div(t_max, chunk_tokens / kTile);
+    } else {
+        w = ceil_div(t_max, kMinDefaultTiles);
+        if (w > kDefaultWorkers) w = kDefaultWorkers;
     }
-    return kDefaultChunkTokens;
+    if (w < floor_w) w = floor_w;
+    if (w < 1) w = 1;
+    return (int)(w > (1 << 30) ? (1 << 30) : w);
 }
 
 static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_size, int chunk_tokens) {
     Layout L{};
-    L.chunk_tokens = resolve_chunk_tokens(chunk_tokens, B, Hkv, max_blocks, block_size);
-    const int64_t max_tokens = (int64_t)max_blocks * block_size;
-    L.max_chunks = (int)(max_tokens > 0 ? ceil_div(max_tokens, L.chunk_tokens) : 1);
+    L.workers = resolve_workers(chunk_tokens, B, Hkv, max_blocks, block_size);
     const int G = Hkv > 0 ? Hq / Hkv : 0;
-    const size_t units = (size_t)B * Hkv;
+    const size_t slots = (size_t)L.workers + (size_t)B * Hkv;
     L.err = 0;
-    L.ml = 256;
-    L.acc = L.ml + align256(units * L.max_chunks * G * 2 * sizeof(float));
-    L.total = L.acc + align256(units * L.max_chunks * G * D * sizeof(float));
+    L.segw = 256;
+    L.ml = L.segw + align256((size_t)B * Hkv * 2 * sizeof(int));
+    L.acc = L.ml + align256(slots * G * 2 * sizeof(float));
+    L.total = L.acc + align256(slots * G * D * sizeof(float));
     return L;
 }
 
+// Waves of this kernel instance that fit on the current device at once
+// (occupancy x CUs), cached per device; 0 if the runtime cannot say.
 template <int D, int BS, int G>
-static void launch(const Params& prm, int B, hipStream_t st) {
-    hipLaunchKernelGGL((decode_partial_kernel<D, BS, G>), dim3(prm.max_chunks, prm.Hkv, B), dim3(kWaves * 64), 0, st,
-                       prm);
-    if (prm.max_chunks > 1)
-        hipLaunchKernelGGL((decode_combine_kernel<D, BS, G>), dim3(prm.Hkv, B), dim3(256), 0, st, prm);
+static int resident_waves() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cache[dev] == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_kernel<D, BS, G>, kWaves * 64, 0) !=
+                hipSuccess)
+            return 0;
+        cache[dev] = cus * per_cu * kWaves;
+    }
+    return cache[dev];
+}
+
+template <int D, int BS, int G>
+static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
+    // More workers than resident waves would leave a second, partial round; use
+    // one round unless ranges would then exceed kMaxRangeTiles.
+    const int cap = resident_waves<D, BS, G>();
+    if (cap > 0 && prm.workers > cap) prm.workers = (int)(floor_workers > cap ? floor_workers : cap);
+    const int blocks = (int)ceil_div(prm.workers, kWaves);
+    hipLaunchKernelGGL((decode_split_kernel<D, BS, G>), dim3(blocks), dim3(kWaves * 64), 0, st, prm);
+    hipLaunchKernelGGL((decode_merge_kernel<D, BS, G>), dim3(prm.Hkv, B), dim3(256), 0, st, prm);
 }
 
 template <int D, int BS>
-static bool dispatch_g(int G, const Params& prm, int B, hipStream_t st) {
+static bool dispatch_g(int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
     switch (G) {
-        case 1: launch<D, BS, 1>(prm, B, st); return true;
-        case 2: launch<D, BS, 2>(prm, B, st); return true;
-        case 3: launch<D, BS, 3>(prm, B, st); return true;
-        case 4: launch<D, BS, 4>(prm, B, st); return true;
-        case 5: launch<D, BS, 5>(prm, B, st); return true;
-        case 6: launch<D, BS, 6>(prm, B, st); return true;
-        case 7: launch<D, BS, 7>(prm, B, st); return true;
-        case 8: launch<D, BS, 8>(prm, B, st); return true;
+        case 1: launch<D, BS, 1>(prm, B, st, fw); return true;
+        case 2: launch<D, BS, 2>(prm, B, st, fw); return true;
+        case 3: launch<D, BS, 3>(prm, B, st, fw); return true;
+        case 4: launch<D, BS, 4>(prm, B, st, fw); return true;
+        case 5: launch<D, BS, 5>(prm, B, st, fw); return true;
+        case 6: launch<D, BS, 6>(prm, B, st, fw); return true;
+        case 7: launch<D, BS, 7>(prm, B, st, fw); return true;
+        case 8: launch<D, BS, 8>(prm, B, st, fw); return true;
         default: return false;
     }
 }
@@ -421,17 +579,15 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     if (max_blocks < 1 || num_pool_blocks < 1)
         return fail(MX_ERR_INVALID, "mx_paged_attn_decode: max_blocks and num_pool_blocks must be >= 1");
     if (B > 65535 || Hkv > 65535) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: B or Hkv too large");
-    const int ct = pa::resolve_chunk_tokens(chunk_tokens, B, Hkv, max_blocks, block_size);
-    if (ct % pa::kTile != 0 || ct > pa::kMaxChunkTokens)
-        return fail(MX_ERR_INVALID, "mx_paged_attn_decode: chunk_tokens must be a multiple of 16 and <= %d",
+    if (chunk_tokens < 0 || chunk_tokens % pa::kTile != 0 || chunk_tokens > pa::kMaxChunkTokens)
+        return fail(MX_ERR_INVALID, "mx_paged_attn_decode: chunk_tokens must be 0 or a multiple of 16 <= %d",
                     pa::kMaxChunkTokens);
+    if ((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, pa::kTile) > ((int64_t)1 << 31))
+        return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: more than 2^31 tiles");
     if (!aligned(q, 16) || q_sb % 8 || q_sh % 8 || !aligned(k, 16) || !aligned(v, 16) || kv_sblk % 8 ||
-        kv_shead % 8 || !aligned(out, 2))
-        return fail(MX_ERR_ALIGNMENT, "mx_paged_attn_decode: q/K/V rows must be 16-byte aligned");
-    const pa::Layout L = pa::layout(B, Hq, Hkv, D, max_blocks, block_size, ct);
-    if (L.max_chunks > pa::kMaxChunks)
-        return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: max_blocks*block_size/chunk_tokens exceeds %d chunks",
-                    pa::kMaxChunks);
+        kv_shead % 8 || !aligned(out, 16) || o_sb % 8 || o_sh % 8)
+        return fail(MX_ERR_ALIGNMENT, "mx_paged_attn_decode: q/K/V/out rows must be 16-byte aligned");
+    const pa::Layout L = pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens);
     if (!workspace || workspace_bytes < L.total)
         return fail(MX_ERR_WORKSPACE, "mx_paged_attn_decode: workspace needs %zu bytes, got %zu", L.total,
                     workspace_bytes);
@@ -450,6 +606,7 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     prm.bt_sb = bt_sb;
     prm.max_blocks = max_blocks;
     prm.seq_lens = seq_lens;
+    prm.B = B;
     prm.Hkv = Hkv;
     prm.num_pool_blocks = num_pool_blocks;
     prm.scale_log2e = scale * 1.4426950408889634f;
@@ -459,14 +616,17 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     prm.err = reinterpret_cast<int*>(ws + L.err);
     prm.part_ml = reinterpret_cast<float*>(ws + L.ml);
     prm.part_acc = reinterpret_cast<float*>(ws + L.acc);
-    prm.max_chunks = L.max_chunks;
-    prm.chunk_tiles = ct / pa::kTile;
+    prm.seg_w = reinterpret_cast<int*>(ws + L.segw);
+    prm.workers = L.workers;
     hipStream_t st = as_stream(stream);
     bool ok = false;
-    if (D == 128 && block_size == 16) ok = pa::dispatch_g<128, 16>(G, prm, B, st);
-    else if (D == 128 && block_size == 32) ok = pa::dispatch_g<128, 32>(G, prm, B, st);
-    else if (D == 64 && block_size == 16) ok = pa::dispatch_g<64, 16>(G, prm, B, st);
-    else ok = pa::dispatch_g<64, 32>(G, prm, B, st);
+    // Fewest workers that keep every range within one vector of block ids.
+    const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, pa::kTile),
+                                pa::kMaxRangeTiles);
+    if (D == 128 && block_size == 16) ok = pa::dispatch_g<128, 16>(G, prm, B, st, fw);
+    else if (D == 128 && block_size == 32) ok = pa::dispatch_g<128, 32>(G, prm, B, st, fw);
+    else if (D == 64 && block_size == 16) ok = pa::dispatch_g<64, 16>(G, prm, B, st, fw);
+    else ok = pa::dispatch_g<64, 32>(G, prm, B, st, fw);
     if (!ok) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: unsupported configuration");
     return check_launch("mx_paged_attn_decode");
 }

@@ -1,22 +1,30 @@
 """Block-paged KV storage read by the HIP paged-attention decode kernel.
 
-Keeps the reference's ``GpuKVBlockPool`` API (``runtime/phase2/paged_kv_kernel.py:24-315``)
-and its storage layout, which the kernel reads in place:
+Keeps the reference's ``GpuKVBlockPool`` API (``runtime/phase2/paged_kv_kernel.py:24-315``):
+``k_layer_view(l)`` / ``v_layer_view(l)`` are ``[num_blocks, Hkv, bs, D]`` per
+layer with every (block, kv-head) one contiguous ``bs*D`` run (4 KiB at bs=16,
+D=128, fp16), and token ``pos`` of a row is stored in block
+``table[pos // bs]`` at offset ``pos % bs`` (``:163-174``, ``:217-227``).
 
-* K and V are ``[num_blocks, num_layers, num_kv_heads, block_size, head_dim]``
-  (``:101-107``); ``k_layer_view(l)`` is ``pool[:, l]`` ->
-  ``[num_blocks, Hkv, bs, D]`` with strides ``(L*Hkv*bs*D, bs*D, D, 1)``
-  (``:124-134``), so every (block, layer, kv-head) is one contiguous
-  ``bs*D`` run (4 KiB at bs=16, D=128, fp16);
-* token ``pos`` of a row is stored in block ``table[pos // bs]`` at offset
-  ``pos % bs`` (``:163-174``, ``:217-227``).
+MI355X-first differences:
 
-MI355X-first difference: the reference grows its slabs lazily 8 blocks at a time
-and copies the whole slab on every growth (``:86-115``). Here the first use
-allocates all ``num_blocks`` at once (288 GB of HBM per GPU makes that the
-cheap choice), so tensor addresses never change after ``_ensure_pools`` and a
-captured HIP graph stays valid. Block usage accounting
-(``allocated_block_count`` / ``peak_allocated_block_count``) is unchanged.
+* Layer-major storage. The reference stores ``[num_blocks, num_layers, Hkv,
+  bs, D]`` (``:101-107``), so one layer's blocks are spread over the whole
+  pool, one ``Hkv*bs*D`` run every ``num_layers`` runs. Here the tensors are
+  ``[num_layers, num_blocks, Hkv, bs, D]`` and a layer view is one contiguous
+  region (``num_blocks * 32 KiB`` for Llama-3-8B's 8 KV heads): the decode
+  kernel's random block reads for a layer then stay inside a region the GPU's
+  address-translation caches cover, instead of landing on a different 2 MiB
+  page almost every time across a 17 GB pool. The views keep the reference's
+  shape and per-block contents; only ``stride(0)`` differs
+  (``Hkv*bs*D`` instead of ``num_layers*Hkv*bs*D``), and every consumer takes
+  strides from the view.
+* The reference grows its slabs lazily 8 blocks at a time and copies the
+  whole slab on every growth (``:86-115``). Here the first use allocates all
+  ``num_blocks`` at once (288 GB of HBM per GPU makes that the cheap choice),
+  so tensor addresses never change after ``_ensure_pools`` and a captured HIP
+  graph stays valid. Block usage accounting (``allocated_block_count`` /
+  ``peak_allocated_block_count``) is unchanged.
 """
 
 from __future__ import annotations
@@ -47,7 +55,6 @@ class GpuKVBlockPool:
                                num_kv_heads=num_kv_heads, head_dim=head_dim)
         self.dtype = dtype
         self.device = torch.device(device)
-        self._block_shape = (num_layers, num_kv_heads, block_size_tokens, head_dim)
         self._k_pool: torch.Tensor | None = None
         self._v_pool: torch.Tensor | None = None
         self._used_blocks: set[int] = set()
@@ -78,7 +85,7 @@ class GpuKVBlockPool:
         if self._k_pool is not None:
             return
         s = self.shape
-        shape = (s.num_blocks, s.num_layers, s.num_kv_heads, s.block_size_tokens, s.head_dim)
+        shape = (s.num_layers, s.num_blocks, s.num_kv_heads, s.block_size_tokens, s.head_dim)
         self._k_pool = torch.zeros(shape, dtype=self.dtype, device=self.device)
         self._v_pool = torch.zeros(shape, dtype=self.dtype, device=self.device)
 
@@ -96,13 +103,13 @@ class GpuKVBlockPool:
         """Per-layer K blocks: ``[num_blocks, num_kv_heads, block_size, head_dim]``."""
         self._ensure_pools()
         assert self._k_pool is not None
-        return self._k_pool[:, layer_idx]
+        return self._k_pool[layer_idx]
 
     def v_layer_view(self, layer_idx: int) -> torch.Tensor:
         """Per-layer V blocks: ``[num_blocks, num_kv_heads, block_size, head_dim]``."""
         self._ensure_pools()
         assert self._v_pool is not None
-        return self._v_pool[:, layer_idx]
+        return self._v_pool[layer_idx]
 
     def write_tokens(self, layer_idx: int, block_ids: list[int], start_pos: int, key_states: torch.Tensor,
                      value_states: torch.Tensor) -> None:
@@ -159,8 +166,8 @@ class GpuKVBlockPool:
             if int(physical.min().item()) < 0 or int(physical.max().item()) >= self.shape.num_blocks:
                 raise IndexError("physical block id out of range during batched write")
             self._touch_blocks(physical)
-        k_layer = self._k_pool[:, layer_idx]
-        v_layer = self._v_pool[:, layer_idx]
+        k_layer = self._k_pool[layer_idx]
+        v_layer = self._v_pool[layer_idx]
         if on_device:
             from .decode_glue import kv_append
 
@@ -191,8 +198,8 @@ class GpuKVBlockPool:
             return
         src = torch.tensor([s for s, _ in pairs], device=self.device, dtype=torch.long)
         dst = torch.tensor([d for _, d in pairs], device=self.device, dtype=torch.long)
-        self._k_pool[dst] = self._k_pool[src]
-        self._v_pool[dst] = self._v_pool[src]
+        self._k_pool[:, dst] = self._k_pool[:, src]
+        self._v_pool[:, dst] = self._v_pool[:, src]
 
     def gather_layer(self, layer_idx: int, block_ids: list[int], seq_len: int) -> tuple[torch.Tensor, torch.Tensor]:
         """Gather one row as ``[1, Hkv, seq_len, D]`` (prefill / parity, ``:252-283``)."""
@@ -209,8 +216,8 @@ class GpuKVBlockPool:
             self._touch_block(b)
         ids = torch.tensor(ids_list, device=self.device, dtype=torch.long)
         s = self.shape
-        k = self._k_pool[ids, layer_idx].permute(1, 0, 2, 3).reshape(s.num_kv_heads, n_logical * bs, s.head_dim)
-        v = self._v_pool[ids, layer_idx].permute(1, 0, 2, 3).reshape(s.num_kv_heads, n_logical * bs, s.head_dim)
+        k = self._k_pool[layer_idx, ids].permute(1, 0, 2, 3).reshape(s.num_kv_heads, n_logical * bs, s.head_dim)
+        v = self._v_pool[layer_idx, ids].permute(1, 0, 2, 3).reshape(s.num_kv_heads, n_logical * bs, s.head_dim)
         return k[:, :seq_len].unsqueeze(0), v[:, :seq_len].unsqueeze(0)
 
     def gather_layer_batch(self, layer_idx: int, block_tables: torch.Tensor, seq_lens: torch.Tensor

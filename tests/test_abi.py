@@ -36,13 +36,16 @@ def test_paged_attn_workspace_layout_is_host_computable():
     small = lib.mx_paged_attn_workspace_bytes(4, 8, 2, 64, 8, 16, 0)
     big = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 256)
     assert 0 < small < big
-    assert big >= 32 * 8 * (4096 // 256) * 4 * 128 * 4  # fp32 partial accumulators, 16 chunks per row
+    # One fp32 partial (G x (D + 2)) per worker + segment slot: 65536 tiles at the table
+    # width in ranges of 16 tiles -> 4096 workers, + 256 segments.
+    assert big >= (4096 + 256) * 4 * 128 * 4
     assert lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 512) < big
-    # Default chunk: 2048 tokens for B*Hkv = 256 rows of up to 4096 tokens, 256 for a single short row.
+    # Default split: 2048 workers for config 2's table (ranges of 32 tiles = 512 tokens at full
+    # width); a single short row gets ranges of 4 tiles (64 tokens).
     assert lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 0) == \
-        lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 2048)
+        lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 512)
     assert lib.mx_paged_attn_workspace_bytes(1, 8, 2, 64, 8, 16, 0) == \
-        lib.mx_paged_attn_workspace_bytes(1, 8, 2, 64, 8, 16, 256)
+        lib.mx_paged_attn_workspace_bytes(1, 8, 2, 64, 8, 16, 64)
     assert lib.mx_paged_attn_error_offset(4, 8, 2, 64, 8, 16, 0) % 256 == 0
     # Split-K partials only for a long K with few n-blocks: 4 splits x 32 rows x 4096 fp32 for the
     # 4096x14336 down projection at M=32; none for K=4096, where n-blocks fill the chip, or the GEMV.
@@ -87,6 +90,7 @@ def test_invalid_arguments_return_status_codes():
     _status(call(D=96), _hip.MX_ERR_UNSUPPORTED)
     _status(call(bs=8), _hip.MX_ERR_UNSUPPORTED)
     _status(call(ct=40), _hip.MX_ERR_INVALID)
+    _status(call(ct=2048), _hip.MX_ERR_INVALID)  # split granularity is at most 64 tiles
     _status(call(), _hip.MX_ERR_WORKSPACE)
     _status(call(q_sh=60), _hip.MX_ERR_ALIGNMENT)
     with pytest.raises(ValueError):

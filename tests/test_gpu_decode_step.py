@@ -74,8 +74,9 @@ def _run(hf, batch, lo, hi, seed, graph):
     pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=BLOCK_SIZE, num_layers=s.layers, num_kv_heads=s.kv_heads,
                           head_dim=s.head_dim, dtype=torch.float16, device=dev)
     pool._ensure_pools()
-    pool._k_pool.copy_(pool_k)
-    pool._v_pool.copy_(pool_v)
+    for li in range(s.layers):
+        pool.k_layer_view(li).copy_(pool_k[:, li])
+        pool.v_layer_view(li).copy_(pool_v[:, li])
 
     tables_d = tables.to(dev)
     seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)

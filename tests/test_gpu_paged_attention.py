@@ -4,7 +4,7 @@ Bar: fp16 outputs within atol 1e-2 and rtol 1e-2 of the fp32 per-row oracle
 (oracle/paged_attention.py: decode_rows_fp32), on the reference's own test
 shapes (tests/test_paged_attention_kernel_parity.py:103-198 of the reference),
 the full config-2 shape, and the edge cases (ragged, zero-length, clamped,
-GQA 1..8, D 64/128, block size 16/32, split chunk sizes).
+GQA 1..8, D 64/128, block size 16/32, split granularities).
 """
 
 from __future__ import annotations
@@ -196,7 +196,7 @@ def test_split_chunk_size_invariance():
     grp, scale = 4, 128**-0.5
     want = oracle_out(q, k, v, tables, lens, scale, grp)
     outs = []
-    for ct in (16, 64, 256, 1024, 4096):
+    for ct in (16, 64, 256, 1024, 0):
         out, err = _abi_decode(q, k, v, tables, lens, scale, grp, ct)
         assert err == 0
         _check(out, want, f"chunk_tokens={ct}")

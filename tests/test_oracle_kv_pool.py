@@ -48,17 +48,19 @@ def test_product_pool_matches_oracle_layout():
         pool.write_tokens_batch(layer, tables, starts, k, v)
         for b in range(2):
             kv_pool.write_tokens(ok, ov, layer, tables[b].tolist(), int(starts[b]), k[b:b + 1], v[b:b + 1])
-    assert torch.equal(pool._k_pool, ok) and torch.equal(pool._v_pool, ov)
-    assert torch.equal(pool.k_layer_view(1), ok[:, 1])
-    assert pool.k_layer_view(1).stride() == (layers * hkv * bs * d, bs * d, d, 1)
+    for layer in range(layers):  # same per-layer contents; layer-major storage
+        assert torch.equal(pool.k_layer_view(layer), ok[:, layer])
+        assert torch.equal(pool.v_layer_view(layer), ov[:, layer])
+    assert pool.k_layer_view(1).stride() == (hkv * bs * d, bs * d, d, 1)
+    assert pool.k_layer_view(1).is_contiguous()
     keys, vals = pool.gather_layer(2, tables[1].tolist(), 11)
     ok_k, ok_v = kv_pool.gather_layer(ok, ov, 2, tables[1].tolist(), 11)
     assert torch.equal(keys, ok_k) and torch.equal(vals, ok_v)
     # decode-style single-token append
     k1 = torch.randn(2, hkv, 1, d, generator=g)
     pool.write_tokens_batch(0, tables, torch.tensor([11, 15]), k1, k1)
-    assert torch.equal(pool._k_pool[int(tables[0, 2]), 0, :, 3], k1[0, :, 0])
-    assert torch.equal(pool._k_pool[int(tables[1, 3]), 0, :, 3], k1[1, :, 0])
+    assert torch.equal(pool.k_layer_view(0)[int(tables[0, 2]), :, 3], k1[0, :, 0])
+    assert torch.equal(pool.k_layer_view(0)[int(tables[1, 3]), :, 3], k1[1, :, 0])
 
 
 def test_pool_errors_and_accounting():
