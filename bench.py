@@ -142,7 +142,7 @@ def family_launches(model, pool, tables, seq_lens, bsz, dev) -> dict:
     """Per kernel family: (callable issuing that family's launches of one decode step, launches per call)."""
     import torch
 
-    from runtime_amd.phase2.int8_linear import int8_linear
+    from runtime_amd.phase2.int8_linear import int8_linear, int8_linear_partials
     from runtime_amd.phase2.paged_attention_hip import _decode
 
     s = model.shape
@@ -154,13 +154,21 @@ def family_launches(model, pool, tables, seq_lens, bsz, dev) -> dict:
     lens = (seq_lens + 1).to(torch.int32)
     out = {}
 
+    splits = model.buffers(bsz).splits
+
     def lin(name, x):
+        # The call the decode step makes: split-K partials (summed by the consuming glue
+        # kernel) when the shape splits, else the fused kernel writing fp16.
         outs = [torch.empty(bsz, getattr(layer, name)[2], device=dev, dtype=torch.float16) for layer in model.layers]
+        part = model.buffers(bsz).part
 
         def run():
             for layer, y in zip(model.layers, outs):
                 packed, scale, n, bias = getattr(layer, name)
-                int8_linear(x, packed, scale, bias, n, out=y)
+                if splits[name] > 1:
+                    int8_linear_partials(x, packed, scale, n, part)
+                else:
+                    int8_linear(x, packed, scale, bias, n, out=y)
         return run
 
     nl = len(model.layers)

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 2
+#define MX_ABI_VERSION 3
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -76,6 +76,22 @@ size_t mx_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                     const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t N, int64_t y_stride,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Number of K splits the MFMA path uses for this shape (1 <= M <= 64): 1 means
+ * mx_w8a16_linear writes y directly; above 1, mx_w8a16_linear_partials can
+ * hand the split partials to a consumer that sums them itself (the decode
+ * glue kernels below), saving mx_w8a16_linear's separate reduce launch. */
+int mx_w8a16_splits(int64_t M, int64_t N, int64_t K);
+
+/* The split-K part of mx_w8a16_linear without the reduction:
+ * partials[s][m][n] = scale[n] * sum over the k of split s of x[m, k] q[n, k]
+ * (fp32, no bias), for s < mx_w8a16_splits(M, N, K) > 1; partials is fp32
+ * [splits][M][N], contiguous. Summing the splits, adding the bias and rounding
+ * to fp16 gives mx_w8a16_linear's y. Shapes with one split are rejected
+ * (MX_ERR_UNSUPPORTED). No reference counterpart: the reference runs its
+ * linear as one HF module call (worker_server.py:194-205). */
+int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
+                             const uint16_t* scale, int64_t N, float* partials, size_t partials_bytes, void* stream);
 
 /* ----------------------------------------------------------------------------
  * Paged-attention decode.
@@ -172,6 +188,16 @@ int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32_t B, int32
                        const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, int32_t block_size,
                        int32_t num_pool_blocks, int32_t* err, void* stream);
 
+/* mx_qkv_rope_append with the QKV projection given as split-K partials
+ * (fp32 [splits][B][(Hq + 2*Hkv) * D], from mx_w8a16_linear_partials): each
+ * element is fp16(sum over splits + bias), the value mx_w8a16_linear would
+ * have written, then rotated and appended as above. bias may be NULL. */
+int mx_qkv_rope_append_splits(const float* partials, int32_t splits, const uint16_t* bias, int32_t B, int32_t Hq,
+                              int32_t Hkv, int32_t D, const float* rope, int32_t max_pos, const int32_t* positions,
+                              uint16_t* q_out, int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk,
+                              int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
+                              int32_t block_size, int32_t num_pool_blocks, int32_t* err, void* stream);
+
 /* h = residual ? fp16(x + residual) : x;  residual_out (if not NULL) = h;
  * out = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * weight), per row of H
  * (H % 8 == 0, H <= 16384). The decoder layer's residual add and the
@@ -181,6 +207,14 @@ int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32_t B, int32
 int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride,
                    const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out, int64_t out_stride,
                    uint16_t* residual_out, int64_t ro_stride, void* stream);
+
+/* mx_add_rmsnorm with x given as the split-K partials of the linear that
+ * produced it (fp32 [splits][M][H] from mx_w8a16_linear_partials): x =
+ * fp16(sum over splits + bias) as mx_w8a16_linear would have written it; the
+ * rest is mx_add_rmsnorm. bias may be NULL. */
+int mx_add_rmsnorm_splits(const float* partials, int32_t splits, const uint16_t* bias, const uint16_t* residual,
+                          int64_t r_stride, const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out,
+                          int64_t out_stride, uint16_t* residual_out, int64_t ro_stride, void* stream);
 
 /* out[m, i] = fp16(fp16(silu(gate_up[m, i])) * gate_up[m, I + i]) for i < I
  * (I % 8 == 0): the SwiGLU product between the fused gate||up projection and

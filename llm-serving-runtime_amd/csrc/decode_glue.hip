@@ -19,6 +19,43 @@ __device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<u
 __device__ __forceinline__ half8v as_h8(uint4 v) { return __builtin_bit_cast(half8v, v); }
 __device__ __forceinline__ uint4 as_u4(half8v v) { return __builtin_bit_cast(uint4, v); }
 
+// Linear output element(s) from split-K partials: fp16(bias[col] + sum_s part[s*split_stride + off]),
+// the value mx_w8a16_linear would have written (its reduce adds the bias, then the splits in order).
+// KS > 0 is the split count known at compile time: every load is issued before the first add, so
+// the partials cost one memory round trip; KS == 0 reads `splits` in a loop.
+template <int KS, int E>
+__device__ __forceinline__ void sum_splits(const float* part, int splits, int64_t split_stride, int64_t off,
+                                           const uint16_t* bias, int col, _Float16 (&out)[E]) {
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = bias ? (float)reinterpret_cast<const _Float16*>(bias)[col + e] : 0.0f;
+    if (KS > 0) {
+        float4v v[KS > 0 ? KS : 1][E / 4];
+#pragma unroll
+        for (int sp = 0; sp < KS; ++sp)
+#pragma unroll
+            for (int e = 0; e < E; e += 4) v[sp][e / 4] = *reinterpret_cast<const float4v*>(part + sp * split_stride + off + e);
+#pragma unroll
+        for (int sp = 0; sp < KS; ++sp)
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[e] += v[sp][e / 4][e % 4];
+    } else {
+        for (int sp = 0; sp < splits; ++sp) {
+            const float* q = part + sp * split_stride + off;
+#pragma unroll
+            for (int e = 0; e < E; e += 4) {
+                const float4v v = *reinterpret_cast<const float4v*>(q + e);
+                acc[e] += v[0];
+                acc[e + 1] += v[1];
+                acc[e + 2] += v[2];
+                acc[e + 3] += v[3];
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) out[e] = (_Float16)acc[e];
+}
+
 // Where token `pos` of row `b` lives in the pool, or -1 when its logical block is past the
 // table or its physical id is outside the pool (the token is then skipped and flagged).
 __device__ __forceinline__ int64_t slot_offset(const int32_t* bt, int64_t bt_sb, int max_blocks, int b, int pos,
@@ -71,8 +108,12 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendParams p, int
 }
 
 struct RopeAppendParams {
-    const uint16_t* qkv;
+    const uint16_t* qkv;      // fp16 rows, or NULL with part != NULL
     int64_t qkv_stride;
+    const float* part;        // split-K partials [splits][B][(Hq + 2 Hkv) * D]
+    int splits;
+    int64_t split_stride;
+    const uint16_t* bias;     // added to the partial sums (NULL: none)
     int Hq, Hkv, D;
     const float2* rope;  // [max_pos][D/2] (cos, sin)
     int max_pos;
@@ -91,7 +132,10 @@ struct RopeAppendParams {
 // Rotate-half RoPE (pairs i and i + D/2 share frequency i) on the q and k heads of one
 // fused-QKV output row, then q -> q_out and k, v -> the pool slot of position `pos`.
 // One thread per 4 pairs of a q/k head (two 8-byte loads) or per 8 elements of a v head.
+// KS < 0: fp16 QKV rows; KS >= 0: split partials (see sum_splits).
+template <int KS>
 __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendParams p, int64_t total) {
+    constexpr bool SPLIT = KS >= 0;
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= total) return;
     const int per_head = p.D >> 3;
@@ -99,7 +143,8 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendPar
     const int c = (int)(i % per_head);
     const int hs = (int)((i / per_head) % heads);
     const int b = (int)(i / ((int64_t)per_head * heads));
-    const uint16_t* row = p.qkv + (int64_t)b * p.qkv_stride + (int64_t)hs * p.D;
+    const uint16_t* row = SPLIT ? nullptr : p.qkv + (int64_t)b * p.qkv_stride + (int64_t)hs * p.D;
+    const int64_t poff = SPLIT ? ((int64_t)b * (p.Hq + 2 * p.Hkv) + hs) * p.D : 0;  // element offset in a split
     const int pos = p.positions[b];
     if (hs < p.Hq + p.Hkv) {
         const int half = p.D >> 1;
@@ -107,8 +152,21 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendPar
         const bool pos_ok = pos >= 0 && pos < p.max_pos;
         half4v o1 = {0, 0, 0, 0}, o2 = {0, 0, 0, 0};
         if (pos_ok) {
-            const half4v x1 = __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(row + j));
-            const half4v x2 = __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(row + half + j));
+            half4v x1, x2;
+            if (SPLIT) {
+                _Float16 v1[4], v2[4];
+                sum_splits<(KS > 0 ? KS : 0), 4>(p.part, p.splits, p.split_stride, poff + j, p.bias, hs * p.D + j, v1);
+                sum_splits<(KS > 0 ? KS : 0), 4>(p.part, p.splits, p.split_stride, poff + half + j, p.bias,
+                                                 hs * p.D + half + j, v2);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x1[e] = v1[e];
+                    x2[e] = v2[e];
+                }
+            } else {
+                x1 = __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(row + j));
+                x2 = __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(row + half + j));
+            }
             const float2* cs = p.rope + (int64_t)pos * half + j;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -141,7 +199,16 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendPar
     const int64_t dst = slot_offset(p.bt, p.bt_sb, p.max_blocks, b, pos, p.bs, p.num_pool_blocks, p.sblk, p.shead,
                                     hs - p.Hq - p.Hkv, p.D);
     if (dst < 0) return;  // flagged by the k thread of the same chunk
-    st16(p.v_pool + dst + c * 8, ld16(row + c * 8));
+    if (SPLIT) {
+        _Float16 v[8];
+        sum_splits<(KS > 0 ? KS : 0), 8>(p.part, p.splits, p.split_stride, poff + c * 8, p.bias, hs * p.D + c * 8, v);
+        half8v o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = v[e];
+        st16(p.v_pool + dst + c * 8, as_u4(o));
+    } else {
+        st16(p.v_pool + dst + c * 8, ld16(row + c * 8));
+    }
 }
 
 constexpr int kNormMaxChunks = 8;  // H <= kThreads * 8 * kNormMaxChunks = 16384
@@ -158,48 +225,76 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return s;
 }
 
+struct NormParams {
+    const uint16_t* x;     // fp16 rows, or NULL with part != NULL
+    int64_t xs;
+    const float* part;     // split-K partials [splits][M][H] of the producing linear
+    int splits;
+    int64_t split_stride;
+    const uint16_t* bias;  // added to the partial sums (NULL: none)
+    const uint16_t* res;
+    int64_t rs;
+    const uint16_t* w;
+    int H;
+    float eps;
+    uint16_t* out;
+    int64_t os;
+    uint16_t* res_out;
+    int64_t ros;
+};
+
 // h = x (+ residual, rounded to fp16); residual_out = h; out = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * w).
 // The two roundings of the output follow HF's RMSNorm (normalise in fp32, cast, scale in fp16).
-// out may alias x and residual_out may alias residual (each thread reads its chunks before
-// it writes them); out must not alias residual_out.
-__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(const uint16_t* x, int64_t xs, const uint16_t* res,
-                                                               int64_t rs, const uint16_t* w, int H, float eps,
-                                                               uint16_t* out, int64_t os, uint16_t* res_out,
-                                                               int64_t ros) {
+// With SPLIT, x is first formed from the producing linear's split partials and rounded to fp16,
+// as that linear's own output would have been. out may alias x and residual_out may alias
+// residual (each thread reads its chunks before it writes them); out must not alias residual_out.
+// KS < 0: fp16 x rows; KS >= 0: split partials (see sum_splits).
+template <int KS>
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(NormParams p) {
+    constexpr bool SPLIT = KS >= 0;
     __shared__ float red[kThreads / 64];
     const int m = blockIdx.x;
-    const int chunks = H >> 3;
+    const int chunks = p.H >> 3;
     half8v h[kNormMaxChunks];
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kNormMaxChunks; ++u) {
         const int c = threadIdx.x + u * kThreads;
         if (c < chunks) {
-            half8v v = as_h8(ld16(x + (int64_t)m * xs + c * 8));
-            if (res) {
-                const half8v r = as_h8(ld16(res + (int64_t)m * rs + c * 8));
+            half8v v;
+            if (SPLIT) {
+                _Float16 t[8];
+                sum_splits<(KS > 0 ? KS : 0), 8>(p.part, p.splits, p.split_stride, (int64_t)m * p.H + c * 8, p.bias,
+                                                 c * 8, t);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = t[e];
+            } else {
+                v = as_h8(ld16(p.x + (int64_t)m * p.xs + c * 8));
+            }
+            if (p.res) {
+                const half8v r = as_h8(ld16(p.res + (int64_t)m * p.rs + c * 8));
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] + (float)r[e]);
             }
-            if (res_out) st16(res_out + (int64_t)m * ros + c * 8, as_u4(v));
+            if (p.res_out) st16(p.res_out + (int64_t)m * p.ros + c * 8, as_u4(v));
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
             h[u] = v;
         }
     }
-    const float scale = rsqrtf(block_sum(ss, red) / (float)H + eps);
+    const float scale = rsqrtf(block_sum(ss, red) / (float)p.H + p.eps);
 #pragma unroll
     for (int u = 0; u < kNormMaxChunks; ++u) {
         const int c = threadIdx.x + u * kThreads;
         if (c < chunks) {
-            const half8v g = as_h8(ld16(w + c * 8));
+            const half8v g = as_h8(ld16(p.w + c * 8));
             half8v o;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const _Float16 n = (_Float16)((float)h[u][e] * scale);
                 o[e] = (_Float16)((float)n * (float)g[e]);
             }
-            st16(out + (int64_t)m * os + c * 8, as_u4(o));
+            st16(p.out + (int64_t)m * p.os + c * 8, as_u4(o));
         }
     }
 }
@@ -256,6 +351,31 @@ extern "C" int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_
     return check_launch("mx_kv_append");
 }
 
+static int rope_append_common(const char* what, glue::RopeAppendParams& p, int32_t B, void* stream) {
+    if (B < 0) return fail(MX_ERR_INVALID, "%s: B must be >= 0", what);
+    if (B == 0) return MX_OK;
+    if (!p.rope || !p.positions || !p.q_out || !p.k_pool || !p.v_pool || !p.bt)
+        return fail(MX_ERR_NULL, "%s: null pointer", what);
+    if (p.Hq <= 0 || p.Hkv <= 0 || p.D <= 0 || p.D % 8 || p.max_pos <= 0 || p.bs <= 0 || p.max_blocks <= 0 ||
+        p.num_pool_blocks <= 0)
+        return fail(MX_ERR_INVALID, "%s: need positive sizes and D %% 8 == 0 (Hq=%d Hkv=%d D=%d)", what, p.Hq, p.Hkv,
+                    p.D);
+    if (p.q_stride % 8 || p.sblk % 8 || p.shead % 8 || !glue::a16(p.q_out) || !glue::a16(p.k_pool) ||
+        !glue::a16(p.v_pool) || !aligned(p.rope, 8))
+        return fail(MX_ERR_ALIGNMENT, "%s: rows need 16-byte alignment", what);
+    if (p.q_stride < (int64_t)p.Hq * p.D) return fail(MX_ERR_INVALID, "%s: q row stride shorter than the row", what);
+    const int64_t total = (int64_t)B * (p.Hq + 2 * p.Hkv) * (p.D / 8);
+    const dim3 grid((unsigned)ceil_div(total, glue::kThreads)), block(glue::kThreads);
+    hipStream_t st = as_stream(stream);
+    if (!p.part) hipLaunchKernelGGL(glue::qkv_rope_append_kernel<-1>, grid, block, 0, st, p, total);
+    else if (p.splits == 2) hipLaunchKernelGGL(glue::qkv_rope_append_kernel<2>, grid, block, 0, st, p, total);
+    else if (p.splits == 4) hipLaunchKernelGGL(glue::qkv_rope_append_kernel<4>, grid, block, 0, st, p, total);
+    else if (p.splits == 8) hipLaunchKernelGGL(glue::qkv_rope_append_kernel<8>, grid, block, 0, st, p, total);
+    else if (p.splits == 16) hipLaunchKernelGGL(glue::qkv_rope_append_kernel<16>, grid, block, 0, st, p, total);
+    else hipLaunchKernelGGL(glue::qkv_rope_append_kernel<0>, grid, block, 0, st, p, total);
+    return check_launch(what);
+}
+
 extern "C" int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32_t B, int32_t Hq, int32_t Hkv,
                                   int32_t D, const float* rope, int32_t max_pos, const int32_t* positions,
                                   uint16_t* q_out, int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool,
@@ -263,45 +383,82 @@ extern "C" int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32
                                   int32_t max_blocks, int32_t block_size, int32_t num_pool_blocks, int32_t* err,
                                   void* stream) {
     clear_error();
-    if (B < 0) return fail(MX_ERR_INVALID, "mx_qkv_rope_append: B must be >= 0");
-    if (B == 0) return MX_OK;
-    if (!qkv || !rope || !positions || !q_out || !k_pool || !v_pool || !block_tables)
-        return fail(MX_ERR_NULL, "mx_qkv_rope_append: null pointer");
-    if (Hq <= 0 || Hkv <= 0 || D <= 0 || D % 8 || max_pos <= 0 || block_size <= 0 || max_blocks <= 0 ||
-        num_pool_blocks <= 0)
-        return fail(MX_ERR_INVALID, "mx_qkv_rope_append: need positive sizes and D %% 8 == 0 (Hq=%d Hkv=%d D=%d)",
-                    Hq, Hkv, D);
-    if (qkv_stride % 8 || q_stride % 8 || kv_sblk % 8 || kv_shead % 8 || !glue::a16(qkv) || !glue::a16(q_out) ||
-        !glue::a16(k_pool) || !glue::a16(v_pool) || !aligned(rope, 8))
+    if (B > 0 && !qkv) return fail(MX_ERR_NULL, "mx_qkv_rope_append: null pointer");
+    if (B > 0 && (qkv_stride % 8 || !glue::a16(qkv)))
         return fail(MX_ERR_ALIGNMENT, "mx_qkv_rope_append: rows need 16-byte alignment");
-    if (qkv_stride < (int64_t)(Hq + 2 * Hkv) * D || q_stride < (int64_t)Hq * D)
+    if (B > 0 && qkv_stride < (int64_t)(Hq + 2 * Hkv) * D)
         return fail(MX_ERR_INVALID, "mx_qkv_rope_append: row strides shorter than the rows");
-    glue::RopeAppendParams p{qkv, qkv_stride, Hq, Hkv, D, reinterpret_cast<const float2*>(rope), max_pos, positions,
-                             q_out, q_stride, k_pool, v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks,
-                             block_size, num_pool_blocks, err};
-    const int64_t total = (int64_t)B * (Hq + 2 * Hkv) * (D / 8);
-    hipLaunchKernelGGL(glue::qkv_rope_append_kernel, dim3((unsigned)ceil_div(total, glue::kThreads)),
-                       dim3(glue::kThreads), 0, as_stream(stream), p, total);
-    return check_launch("mx_qkv_rope_append");
+    glue::RopeAppendParams p{qkv, qkv_stride, nullptr, 0, 0, nullptr, Hq, Hkv, D,
+                             reinterpret_cast<const float2*>(rope), max_pos, positions, q_out, q_stride, k_pool,
+                             v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, block_size, num_pool_blocks,
+                             err};
+    return rope_append_common("mx_qkv_rope_append", p, B, stream);
+}
+
+extern "C" int mx_qkv_rope_append_splits(const float* partials, int32_t splits, const uint16_t* bias, int32_t B,
+                                         int32_t Hq, int32_t Hkv, int32_t D, const float* rope, int32_t max_pos,
+                                         const int32_t* positions, uint16_t* q_out, int64_t q_stride,
+                                         uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
+                                         const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
+                                         int32_t block_size, int32_t num_pool_blocks, int32_t* err, void* stream) {
+    clear_error();
+    if (B > 0 && !partials) return fail(MX_ERR_NULL, "mx_qkv_rope_append_splits: null pointer");
+    if (splits < 1) return fail(MX_ERR_INVALID, "mx_qkv_rope_append_splits: splits must be >= 1");
+    if (B > 0 && (!glue::a16(partials) || (bias && !aligned(bias, 8))))
+        return fail(MX_ERR_ALIGNMENT, "mx_qkv_rope_append_splits: partials need 16-byte alignment");
+    const int64_t width = (int64_t)(Hq + 2 * Hkv) * D;
+    glue::RopeAppendParams p{nullptr, width, partials, splits, (int64_t)B * width, bias, Hq, Hkv, D,
+                             reinterpret_cast<const float2*>(rope), max_pos, positions, q_out, q_stride, k_pool,
+                             v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, block_size, num_pool_blocks,
+                             err};
+    return rope_append_common("mx_qkv_rope_append_splits", p, B, stream);
+}
+
+static int add_rmsnorm_common(const char* what, glue::NormParams& p, int32_t M, void* stream) {
+    if (M < 0) return fail(MX_ERR_INVALID, "%s: M must be >= 0", what);
+    if (M == 0) return MX_OK;
+    if (!p.w || !p.out) return fail(MX_ERR_NULL, "%s: null pointer", what);
+    if (p.H <= 0 || p.H % 8 || p.H > glue::kThreads * 8 * glue::kNormMaxChunks)
+        return fail(MX_ERR_INVALID, "%s: need H %% 8 == 0 and H <= %d (H=%d)", what,
+                    glue::kThreads * 8 * glue::kNormMaxChunks, p.H);
+    if (p.os % 8 || (p.res && p.rs % 8) || (p.res_out && p.ros % 8) || !glue::a16(p.w) || !glue::a16(p.out) ||
+        (p.res && !glue::a16(p.res)) || (p.res_out && !glue::a16(p.res_out)))
+        return fail(MX_ERR_ALIGNMENT, "%s: rows need 16-byte alignment", what);
+    const dim3 grid(M), block(glue::kThreads);
+    hipStream_t st = as_stream(stream);
+    if (!p.part) hipLaunchKernelGGL(glue::add_rmsnorm_kernel<-1>, grid, block, 0, st, p);
+    else if (p.splits == 2) hipLaunchKernelGGL(glue::add_rmsnorm_kernel<2>, grid, block, 0, st, p);
+    else if (p.splits == 4) hipLaunchKernelGGL(glue::add_rmsnorm_kernel<4>, grid, block, 0, st, p);
+    else if (p.splits == 8) hipLaunchKernelGGL(glue::add_rmsnorm_kernel<8>, grid, block, 0, st, p);
+    else if (p.splits == 16) hipLaunchKernelGGL(glue::add_rmsnorm_kernel<16>, grid, block, 0, st, p);
+    else hipLaunchKernelGGL(glue::add_rmsnorm_kernel<0>, grid, block, 0, st, p);
+    return check_launch(what);
 }
 
 extern "C" int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride,
                               const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out,
                               int64_t out_stride, uint16_t* residual_out, int64_t ro_stride, void* stream) {
     clear_error();
-    if (M < 0) return fail(MX_ERR_INVALID, "mx_add_rmsnorm: M must be >= 0");
-    if (M == 0) return MX_OK;
-    if (!x || !weight || !out) return fail(MX_ERR_NULL, "mx_add_rmsnorm: null pointer");
-    if (H <= 0 || H % 8 || H > glue::kThreads * 8 * glue::kNormMaxChunks)
-        return fail(MX_ERR_INVALID, "mx_add_rmsnorm: need H %% 8 == 0 and H <= %d (H=%d)",
-                    glue::kThreads * 8 * glue::kNormMaxChunks, H);
-    if (x_stride % 8 || out_stride % 8 || (residual && r_stride % 8) || (residual_out && ro_stride % 8) ||
-        !glue::a16(x) || !glue::a16(weight) || !glue::a16(out) || (residual && !glue::a16(residual)) ||
-        (residual_out && !glue::a16(residual_out)))
+    if (M > 0 && !x) return fail(MX_ERR_NULL, "mx_add_rmsnorm: null pointer");
+    if (M > 0 && (x_stride % 8 || !glue::a16(x)))
         return fail(MX_ERR_ALIGNMENT, "mx_add_rmsnorm: rows need 16-byte alignment");
-    hipLaunchKernelGGL(glue::add_rmsnorm_kernel, dim3(M), dim3(glue::kThreads), 0, as_stream(stream), x, x_stride,
-                       residual, r_stride, weight, H, eps, out, out_stride, residual_out, ro_stride);
-    return check_launch("mx_add_rmsnorm");
+    glue::NormParams p{x, x_stride, nullptr, 0, 0, nullptr, residual, r_stride, weight, H, eps, out, out_stride,
+                       residual_out, ro_stride};
+    return add_rmsnorm_common("mx_add_rmsnorm", p, M, stream);
+}
+
+extern "C" int mx_add_rmsnorm_splits(const float* partials, int32_t splits, const uint16_t* bias,
+                                     const uint16_t* residual, int64_t r_stride, const uint16_t* weight, int32_t M,
+                                     int32_t H, float eps, uint16_t* out, int64_t out_stride,
+                                     uint16_t* residual_out, int64_t ro_stride, void* stream) {
+    clear_error();
+    if (M > 0 && !partials) return fail(MX_ERR_NULL, "mx_add_rmsnorm_splits: null pointer");
+    if (splits < 1) return fail(MX_ERR_INVALID, "mx_add_rmsnorm_splits: splits must be >= 1");
+    if (M > 0 && (!glue::a16(partials) || (bias && !glue::a16(bias))))
+        return fail(MX_ERR_ALIGNMENT, "mx_add_rmsnorm_splits: partials need 16-byte alignment");
+    glue::NormParams p{nullptr, H, partials, splits, (int64_t)M * H, bias, residual, r_stride, weight, H, eps, out,
+                       out_stride, residual_out, ro_stride};
+    return add_rmsnorm_common("mx_add_rmsnorm_splits", p, M, stream);
 }
 
 extern "C" int mx_silu_mul(const uint16_t* gate_up, int64_t gu_stride, int32_t M, int32_t I, uint16_t* out,

@@ -246,48 +246,68 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 // the instruction applies is consistent. C element i of lane l is row
 // 4*(l/16) + i, column l%16.
 //
-// Each x fragment a wave loads (from L2: every workgroup reads all of x) is
-// reused for NPW weight tiles; at M=32 the x bytes a wave loads per weight byte
-// are 4/NPW, and that L2->L1 traffic, not the weight stream, limits the kernel
-// at NPW=1. With NPW=4 a small-N matrix has too few n-blocks to fill the chip,
-// so K is split over gridDim.y workgroups: each writes its scaled fp32 partial
-// to the workspace and reduce_kernel adds the splits and the bias.
+// Work split: the WAVES waves of a workgroup own different n-tiles (wave w:
+// tiles (blockIdx.x*WAVES + w)*NPW + [0, NPW)) and walk the same k-tiles of the
+// workgroup's K split (blockIdx.y of gridDim.y) in step. Every k-tile of x
+// ([16*MT rows x 64] fp16) is fetched once per workgroup with coalesced
+// 16-byte loads, written to a padded LDS double buffer, and read back as MFMA
+// fragments by all waves after one barrier. Loading the fragments straight
+// from global memory instead (each 16-byte lane load touching 16 x rows)
+// made the x reads, not the weight stream, the limit: at M=32 every wave
+// pulled 4 bytes of x per byte of weights through L1.
+//
+// A wave owns whole output tiles, so there is no cross-wave reduction. With one
+// split, the epilogue writes fp16 y (scale, bias); otherwise it writes the
+// scaled fp32 partial of its split, which the caller or reduce_kernel adds.
 // ---------------------------------------------------------------------------
 template <int MT, int NPW, int WAVES, int P>
 __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
                                                                const uint16_t* __restrict__ bias,
-                                                               uint16_t* __restrict__ y, int64_t ys, int KT, int N,
+                                                               uint16_t* __restrict__ y, int64_t ys, int KT, int NT,
                                                                float* __restrict__ partial) {
-    const int nt0 = blockIdx.x * NPW;
+    constexpr int ROWS = MT * 16;
+    constexpr int RS = kTileK + 8;  // LDS row stride (halfs): 144 bytes, rows start 4 banks apart
+    constexpr int XCH = ROWS * 8;   // 16-byte chunks of one x k-tile
+    constexpr int XC = (XCH + WAVES * 64 - 1) / (WAVES * 64);
+    __shared__ __attribute__((aligned(16))) _Float16 xl[2][ROWS * RS];
+
     const int ks = blockIdx.y, KS = gridDim.y;
     const int kt_lo = (int)((int64_t)ks * KT / KS);
-    const int KTL = (int)((int64_t)(ks + 1) * KT / KS) - kt_lo;  // k-tiles of this split
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    const int nj = (int)((int64_t)(ks + 1) * KT / KS) - kt_lo;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
     const int g = lane >> 4, r = lane & 15;
-    const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt0 * KT * 64;
-    const _Float16* xbase = reinterpret_cast<const _Float16*>(x);
-    const int nj = wave < KTL ? (KTL - wave + WAVES - 1) / WAVES : 0;
-    const int rot = kt_rotation(blockIdx.x, KTL);
-    int xoff[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = (mt * 16 + r) < M ? (mt * 16 + r) : (M - 1);
-        xoff[mt] = (int)(m * xs) + g * 16;
-    }
+    const int nt_w = (blockIdx.x * WAVES + wave) * NPW;
+    const bool valid = nt_w < NT;                 // NT % NPW == 0: a wave is all in or all out
+    const int nt_c = valid ? nt_w : NT - NPW;     // out-of-range waves load (and drop) the last tiles
+    const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt_c * KT * 64;
 
-    auto load = [&](int j, Stage<NPW, 2 * MT>& st) {
-        const int kt = kt_lo + rotate_kt(wave + (j < nj ? j : nj - 1) * WAVES, rot, KTL);
+    // x chunks of this thread: chunk c = tid + u*WAVES*64 (wrapped when the tile has
+    // fewer chunks than threads; the duplicate writes store identical bytes).
+    int xsrc[XC], xdst[XC];
+#pragma unroll
+    for (int u = 0; u < XC; ++u) {
+        const int c = (tid + u * WAVES * 64) % XCH;
+        const int row = c / 8, col = (c % 8) * 8;
+        const int rc = row < M ? row : M - 1;
+        xsrc[u] = (int)(rc * xs) + col;
+        xdst[u] = row * RS + col;
+    }
+    const _Float16* xbase = reinterpret_cast<const _Float16*>(x);
+
+    struct St {
+        uint4 w[NPW];
+        uint4 x[XC];
+    };
+    auto load = [&](int j, St& st) {
+        const int kt = kt_lo + (j < nj ? j : nj - 1);
 #pragma unroll
         for (int p = 0; p < NPW; ++p) st.w[p] = (wbase + ((int64_t)p * KT + kt) * 64)[lane];
-        const _Float16* xk = xbase + kt * kTileK;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            st.x[2 * mt] = load_half8(xk + xoff[mt]);
-            st.x[2 * mt + 1] = load_half8(xk + xoff[mt] + 8);
-        }
+        for (int u = 0; u < XC; ++u) st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
     };
 
     float4v acc[NPW][MT];
@@ -295,64 +315,55 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
     for (int p = 0; p < NPW; ++p)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[p][mt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-    auto compute = [&](const Stage<NPW, 2 * MT>& st) {
+
+    // Buffer parity alternates per k-tile. Buffer b is rewritten two k-tiles after
+    // it was read; every wave finished that read before the barrier in between.
+    int step = 0;
+    auto compute = [&](const St& st) {
+        _Float16* buf = xl[step & 1];
+#pragma unroll
+        for (int u = 0; u < XC; ++u) *reinterpret_cast<uint4*>(buf + xdst[u]) = st.x[u];
+        __syncthreads();
+        half8v a[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const _Float16* src = buf + (mt * 16 + r) * RS + 16 * g;
+            a[mt][0] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(src));
+            a[mt][1] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(src + 8));
+        }
 #pragma unroll
         for (int p = 0; p < NPW; ++p) {
             const half8v b0 = dequant8(st.w[p].x, st.w[p].y);
             const half8v b1 = dequant8(st.w[p].z, st.w[p].w);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[2 * mt], b0, acc[p][mt], 0, 0, 0);
-                acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[2 * mt + 1], b1, acc[p][mt], 0, 0, 0);
+                acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][0], b0, acc[p][mt], 0, 0, 0);
+                acc[p][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][1], b1, acc[p][mt], 0, 0, 0);
             }
         }
+        ++step;
     };
     if (nj > 0) {
-        Stage<NPW, 2 * MT> st[P];
+        St st[P];
         PIPELINE_BODY(P, nj, st, load, compute(st[s]))
     }
-
-    // Cross-wave sum in LDS, in two halves to bound the buffer: the upper half
-    // of the waves stores, the lower half adds its own tile and stores back.
-    constexpr int HW = WAVES / 2;
-    __shared__ float red[HW][NPW][MT][16][kTileN];
-    if (wave >= HW) {
+    if (!valid) return;
+    const int N = NT * kTileN;
 #pragma unroll
-        for (int p = 0; p < NPW; ++p)
+    for (int p = 0; p < NPW; ++p) {
+        const int64_t n = (int64_t)(nt_w + p) * kTileN + r;
+        const float sc = h2f(scale, n);
+        const float bi = (KS == 1 && bias) ? h2f(bias, n) : 0.0f;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) red[wave - HW][p][mt][4 * g + i][r] = acc[p][mt][i];
-    }
-    __syncthreads();
-    if (wave < HW) {
-#pragma unroll
-        for (int p = 0; p < NPW; ++p)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) red[wave][p][mt][4 * g + i][r] += acc[p][mt][i];
-    }
-    __syncthreads();
-    constexpr int kOut = NPW * MT * 16 * kTileN;
-    for (int idx = threadIdx.x; idx < kOut; idx += WAVES * 64) {
-        const int p = idx / (MT * 256);
-        const int rem = idx % (MT * 256);
-        const int mt = rem / 256;
-        const int mm = (rem % 256) / kTileN;
-        const int rr = rem % kTileN;
-        const int m = mt * 16 + mm;
-        if (m >= M) continue;
-        float s = 0.0f;
-#pragma unroll
-        for (int wv = 0; wv < HW; ++wv) s += red[wv][p][mt][mm][rr];
-        const int64_t n = (int64_t)(nt0 + p) * kTileN + rr;
-        const float v = s * h2f(scale, n);
-        if (KS == 1) {
-            y[(int64_t)m * ys + n] = f2h_bits(bias ? v + h2f(bias, n) : v);
-        } else {
-            partial[((int64_t)ks * M + m) * N + n] = v;
-        }
+            for (int i = 0; i < 4; ++i) {
+                const int m = mt * 16 + 4 * g + i;
+                if (m >= M) continue;
+                const float v = acc[p][mt][i] * sc;
+                if (KS == 1) y[(int64_t)m * ys + n] = f2h_bits(v + bi);
+                else partial[((int64_t)ks * M + m) * N + n] = v;
+            }
     }
 }
 
@@ -371,52 +382,46 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
 // Largest M handled by the VALU GEMV; above it the MFMA kernel runs.
 constexpr int kValuMaxM = 4;
 constexpr int kGemvWaves = 8;
-constexpr int kMfmaWaves = 8;
-constexpr int kMinBlocks = 160;     // fewest workgroups a wider n-block may leave (measured: qkv at M=32)
-constexpr int kTargetBlocks = 256;  // about one workgroup per CU, for split-K
-constexpr int kMaxSplits = 8;
+constexpr int kMfmaWaves = 4;
+constexpr int kWideGrid = 256;    // at least this many n-groups: no K split
+constexpr int kSplitGrid = 512;   // otherwise split K until the grid reaches this many workgroups
+constexpr int kMaxSplits = 16;
+constexpr int kMinSplitTiles = 4; // k-tiles per split
 
 // Pipeline depth from the VGPRs one stage costs (4 per 1 KiB weight tile, 8
-// per x row fragment of 32 bytes) after the accumulators, within the 256 VGPRs
-// a 512-thread workgroup allows per wave.
+// per x row fragment of 32 bytes) after the accumulators.
 constexpr int clamp_depth(int d) { return d < 2 ? 2 : (d > 8 ? 8 : d); }
 constexpr int gemv_depth(int M) { return clamp_depth(160 / (4 + 8 * M)); }
-constexpr int mfma_depth(int MT, int NPW) { return clamp_depth((176 - 4 * NPW * MT) / (4 * NPW + 8 * MT)); }
+constexpr int mfma_depth(int MT) { return MT <= 2 ? 8 : 6; }
 
 // Launch plan for one chunk of at most 64 rows.
 struct Plan {
     bool valu;
-    int MT, NPW, KS;
+    int MT, KS;
 };
 
-// Output tiles per wave: 4 at M 17..32 (x fragment reused 4x), 2 otherwise,
-// shrunk while that leaves fewer than kMinBlocks workgroups. A long K
-// (>= 8192) keeps the preferred width and splits K over workgroups instead;
-// for K = 4096 the extra reduce launch costs more than the split saves.
+// K splits for the MFMA kernel: none when the n-groups alone fill the chip,
+// else the smallest power of two that gives kSplitGrid workgroups (measured at
+// M=32 on Llama-3-8B shapes: qkv and o take 8 splits, down 8, gate_up none).
+static int splits_for(int NT, int KT) {
+    const int groups = (NT + kMfmaWaves - 1) / kMfmaWaves;
+    if (groups >= kWideGrid) return 1;
+    int ks = 1;
+    while (ks < kMaxSplits && groups * ks < kSplitGrid && KT / (2 * ks) >= kMinSplitTiles) ks *= 2;
+    return ks;
+}
+
 static Plan plan_for(int M, int NT, int KT) {
     Plan pl{};
     pl.KS = 1;
     if (M <= kValuMaxM) {
         pl.valu = true;
         pl.MT = M;
-        pl.NPW = 1;
         return pl;
     }
     pl.valu = false;
     pl.MT = (M + 15) / 16;
-    const int want = pl.MT == 2 ? 4 : 2;
-    int npw = want;
-    while (npw > 1 && (NT % npw || NT / npw < kMinBlocks)) npw /= 2;
-    pl.NPW = npw;
-    if (npw < want && NT % want == 0 && KT >= 128) {
-        const int blocks = NT / want;
-        int ks = (kTargetBlocks + blocks - 1) / blocks;
-        while (ks > 1 && (ks > kMaxSplits || KT / ks < 32)) --ks;
-        if (ks > 1) {
-            pl.NPW = want;
-            pl.KS = ks;
-        }
-    }
+    pl.KS = splits_for(NT, KT);
     return pl;
 }
 
@@ -432,28 +437,32 @@ static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const u
                        xs, w, s, b, y, ys, KT);
 }
 
-template <int MT, int NPW>
+// The MFMA kernel alone: KS == 1 writes fp16 y, KS > 1 writes the scaled fp32
+// partials [KS][M][N] to `partial` (no bias).
+template <int MT>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
-    const int N = NT * kTileN;
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, kMfmaWaves, mfma_depth(MT, NPW)>), dim3(NT / NPW, KS),
-                       dim3(kMfmaWaves * 64), 0, st, x, xs, M, w, s, b, y, ys, KT, N, partial);
-    if (KS > 1) {
-        const int64_t total = (int64_t)M * N;
-        hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, partial, KS, M, N, b,
-                           y, ys);
+    const int groups = (NT + kMfmaWaves - 1) / kMfmaWaves;
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, 1, kMfmaWaves, mfma_depth(MT)>), dim3(groups, KS),
+                       dim3(kMfmaWaves * 64), 0, st, x, xs, M, w, s, b, y, ys, KT, NT, partial);
+}
+
+static void launch_mfma_mt(int MT, const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
+                           const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial,
+                           hipStream_t st) {
+    switch (MT) {
+        case 1: launch_mfma<1>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 2: launch_mfma<2>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 3: launch_mfma<3>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        default: launch_mfma<4>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
     }
 }
 
-template <int MT>
-static void launch_mfma_npw(const Plan& pl, const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
-                            const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, float* partial,
-                            hipStream_t st) {
-    switch (pl.NPW) {
-        case 4: launch_mfma<MT, 4>(x, xs, M, w, s, b, y, ys, NT, KT, pl.KS, partial, st); break;
-        case 2: launch_mfma<MT, 2>(x, xs, M, w, s, b, y, ys, NT, KT, pl.KS, partial, st); break;
-        default: launch_mfma<MT, 1>(x, xs, M, w, s, b, y, ys, NT, KT, pl.KS, partial, st); break;
-    }
+static void launch_reduce(const float* partial, int KS, int M, int N, const uint16_t* b, uint16_t* y, int64_t ys,
+                          hipStream_t st) {
+    const int64_t total = (int64_t)M * N;
+    hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, partial, KS, M, N, b, y,
+                       ys);
 }
 
 }  // namespace w8a16
@@ -527,15 +536,44 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
                 default: w8a16::launch_gemv<4>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
             }
         } else {
-            switch (pl.MT) {
-                case 1: w8a16::launch_mfma_npw<1>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
-                case 2: w8a16::launch_mfma_npw<2>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
-                case 3: w8a16::launch_mfma_npw<3>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
-                default: w8a16::launch_mfma_npw<4>(pl, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, partial, st); break;
-            }
+            w8a16::launch_mfma_mt(pl.MT, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, pl.KS, partial,
+                                  st);
+            if (pl.KS > 1) w8a16::launch_reduce(partial, pl.KS, mc, (int)N, bias, yc, y_stride, st);
         }
         const int rc = check_launch("mx_w8a16_linear");
         if (rc != MX_OK) return rc;
     }
     return MX_OK;
+}
+
+extern "C" int mx_w8a16_splits(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || M > 64 || N <= 0 || K <= 0 || N % w8a16::kTileN || K % w8a16::kTileK) return 1;
+    return w8a16::plan_for((int)M, (int)(N / w8a16::kTileN), (int)(K / w8a16::kTileK)).KS;
+}
+
+extern "C" int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride,
+                                        const uint8_t* packed, const uint16_t* scale, int64_t N, float* partials,
+                                        size_t partials_bytes, void* stream) {
+    if (!x || !packed || !scale || !partials) return fail(MX_ERR_NULL, "mx_w8a16_linear_partials: null pointer");
+    if (M <= 0 || M > 64 || N <= 0 || K <= 0)
+        return fail(MX_ERR_INVALID, "mx_w8a16_linear_partials: need 1 <= M <= 64 and positive N, K");
+    if (N % w8a16::kTileN || K % w8a16::kTileK)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear_partials: need N %% 16 == 0 and K %% 64 == 0");
+    if (x_stride < K) return fail(MX_ERR_INVALID, "mx_w8a16_linear_partials: x row stride must cover K");
+    if (!aligned(x, 16) || (x_stride % 8) != 0 || !aligned(packed, 16) || !aligned(partials, 16))
+        return fail(MX_ERR_ALIGNMENT, "mx_w8a16_linear_partials: x rows, weights and partials must be 16-byte aligned");
+    if (N / w8a16::kTileN > 0x7fffffff || K * 64 > 0x7fffffff)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear_partials: matrix too large");
+    const int NT = (int)(N / w8a16::kTileN);
+    const int KT = (int)(K / w8a16::kTileK);
+    const w8a16::Plan pl = w8a16::plan_for((int)M, NT, KT);
+    if (pl.valu || pl.KS == 1)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear_partials: shape is not split (mx_w8a16_splits == 1); "
+                                        "use mx_w8a16_linear");
+    if (partials_bytes < (size_t)pl.KS * M * N * sizeof(float))
+        return fail(MX_ERR_WORKSPACE, "mx_w8a16_linear_partials: partials need %zu bytes, got %zu",
+                    (size_t)pl.KS * M * N * sizeof(float), partials_bytes);
+    w8a16::launch_mfma_mt(pl.MT, x, x_stride, (int)M, packed, scale, nullptr, nullptr, 0, NT, KT, pl.KS, partials,
+                          as_stream(stream));
+    return check_launch("mx_w8a16_linear_partials");
 }

@@ -8,6 +8,9 @@
   ``apply_rotary_pos_emb`` + ``BlockPagedBatchLayer.update`` write,
   ``runtime/phase2/paged_kv_cache.py:121-157``);
 * :func:`add_rmsnorm` — residual add fused with RMSNorm;
+* :func:`qkv_rope_append_splits` / :func:`add_rmsnorm_splits` — the same, reading
+  the producing linear's split-K partials (``int8_linear_partials``) and
+  forming its fp16 output on the fly;
 * :func:`silu_mul` — SwiGLU's ``silu(gate) * up``;
 * :func:`rope_table` — the fp32 ``(cos, sin)`` table the fused RoPE reads,
   computed like transformers' default rotary embedding
@@ -111,6 +114,52 @@ def qkv_rope_append(qkv: torch.Tensor, rope: torch.Tensor, positions: torch.Tens
         k_layer.stride(1), tables.data_ptr(), tables.stride(0), int(tables.shape[1]), bs, nb,
         err.data_ptr() if err is not None else None, _hip.stream_handle(dev)), "mx_qkv_rope_append")
     return q_out
+
+
+def qkv_rope_append_splits(partials: torch.Tensor, splits: int, bias: torch.Tensor | None, rope: torch.Tensor,
+                           positions: torch.Tensor, q_out: torch.Tensor, k_layer: torch.Tensor,
+                           v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,
+                           err: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`qkv_rope_append` with the QKV projection as fp32 split partials ``[splits, B, width]``."""
+    _hip.require_device_tensor(partials, "partials")
+    dev = partials.device
+    nb, hkv, bs, d = k_layer.shape
+    width = (num_heads + 2 * num_kv_heads) * d
+    b = int(q_out.shape[0])
+    if hkv != num_kv_heads or partials.dtype != torch.float32 or partials.numel() < splits * b * width:
+        raise ValueError("partials must be fp32 [splits, B, (Hq + 2 Hkv) * D]")
+    if rope.dtype != torch.float32 or rope.dim() != 3 or rope.shape[1:] != (d // 2, 2) or not rope.is_contiguous():
+        raise ValueError("rope must be a contiguous fp32 [max_pos, D/2, 2] table")
+    tables = _i32(block_tables, dev)
+    pos = _i32(positions.reshape(-1), dev)
+    q2 = q_out.reshape(b, -1)
+    lib = _hip.load()
+    _hip.check(lib.mx_qkv_rope_append_splits(
+        partials.data_ptr(), splits, bias.data_ptr() if bias is not None else None, b, num_heads, num_kv_heads, d,
+        rope.data_ptr(), int(rope.shape[0]), pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(),
+        v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), tables.data_ptr(), tables.stride(0),
+        int(tables.shape[1]), bs, nb, err.data_ptr() if err is not None else None, _hip.stream_handle(dev)),
+        "mx_qkv_rope_append_splits")
+    return q_out
+
+
+def add_rmsnorm_splits(partials: torch.Tensor, splits: int, bias: torch.Tensor | None, weight: torch.Tensor,
+                       eps: float, out: torch.Tensor, residual: torch.Tensor | None = None,
+                       residual_out: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`add_rmsnorm` with x as the producing linear's fp32 split partials ``[splits, M, H]``."""
+    _hip.require_device_tensor(partials, "partials")
+    m, h = (int(v) for v in out.shape)
+    if partials.dtype != torch.float32 or partials.numel() < splits * m * h:
+        raise ValueError("partials must be fp32 [splits, M, H]")
+    r2 = _rows16(residual.reshape(m, h)) if residual is not None else None
+    ro2 = residual_out.view(m, h) if residual_out is not None else None
+    lib = _hip.load()
+    _hip.check(lib.mx_add_rmsnorm_splits(
+        partials.data_ptr(), splits, bias.data_ptr() if bias is not None else None,
+        r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0, weight.data_ptr(), m, h,
+        float(eps), out.data_ptr(), out.stride(0), ro2.data_ptr() if ro2 is not None else None,
+        ro2.stride(0) if ro2 is not None else 0, _hip.stream_handle(partials.device)), "mx_add_rmsnorm_splits")
+    return out
 
 
 def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,

@@ -19,6 +19,12 @@ current stream:
     h += m Wdown^T                         mx_w8a16_linear (+ the next add_rmsnorm)
     logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, torch argmax
 
+A projection whose shape splits K (``mx_w8a16_splits`` > 1: qkv, o and down at
+batch 32) writes fp32 split partials instead (``mx_w8a16_linear_partials``)
+and the kernel that consumes it (``mx_qkv_rope_append_splits`` /
+``mx_add_rmsnorm_splits``) sums them, adds the bias and rounds to fp16 at the
+point the linear would have, so no reduce launch sits between the two.
+
 Activations live in per-batch-size buffers allocated on the first step, so a
 whole step can be captured in one HIP graph and replayed. Architecture is
 Llama / Qwen2 style (pre-norm, rotate-half RoPE, GQA, SwiGLU, untied int8
@@ -33,8 +39,9 @@ from dataclasses import dataclass
 
 import torch
 
-from .decode_glue import add_rmsnorm, qkv_rope_append, rope_table, silu_mul
-from .int8_linear import int8_linear, pack_weight, quantize_weight
+from .decode_glue import (add_rmsnorm, add_rmsnorm_splits, qkv_rope_append, qkv_rope_append_splits, rope_table,
+                          silu_mul)
+from .int8_linear import int8_linear, int8_linear_partials, linear_splits, pack_weight, quantize_weight
 from .paged_attention_hip import _decode as _paged_decode
 
 
@@ -88,6 +95,8 @@ class _Buffers:
     act: torch.Tensor     # [B, intermediate]
     mlp: torch.Tensor     # [B, hidden]
     logits: torch.Tensor  # [B, vocab]
+    part: torch.Tensor    # fp32 split partials of the current split projection
+    splits: dict          # projection name -> K splits at this batch size
     attn_lens: torch.Tensor  # int32 [B]
     err: torch.Tensor     # int32 [1], OR of the append kernels' error bits
 
@@ -205,10 +214,16 @@ class Int8DecodeModel:
             def e(*shape):
                 return torch.empty(*shape, dtype=f16, device=dev)
 
+            shapes = {"qkv": (s.qkv_out, s.hidden), "o": (s.hidden, s.heads * s.head_dim),
+                      "gate_up": (2 * s.intermediate, s.hidden), "down": (s.hidden, s.intermediate),
+                      "lm_head": (s.vocab, s.hidden)}
+            splits = {k: linear_splits(batch, n, kk) for k, (n, kk) in shapes.items()}
+            part_elems = max([splits[k] * batch * shapes[k][0] for k in shapes if splits[k] > 1] + [4])
             buf = _Buffers(h=e(batch, s.hidden), x=e(batch, s.hidden), qkv=e(batch, s.qkv_out),
                            q=e(batch, s.heads * s.head_dim), attn=e(batch, s.heads, 1, s.head_dim),
                            o=e(batch, s.hidden), gu=e(batch, 2 * s.intermediate), act=e(batch, s.intermediate),
                            mlp=e(batch, s.hidden), logits=e(batch, s.vocab),
+                           part=torch.empty(part_elems, dtype=torch.float32, device=dev), splits=splits,
                            attn_lens=torch.zeros(batch, dtype=torch.int32, device=dev),
                            err=torch.zeros(1, dtype=torch.int32, device=dev))
             self._buffers[batch] = buf
@@ -234,30 +249,59 @@ class Int8DecodeModel:
         torch.add(seq_lens, 1, out=buf.attn_lens)
         torch.index_select(self.embed, 0, tokens, out=buf.h)
         eps = s.rms_eps
+        sp = buf.splits
         for li, layer in enumerate(self.layers):
             if li == 0:
                 add_rmsnorm(buf.h, layer.ln_in, eps, out=buf.x)
             else:
-                add_rmsnorm(buf.mlp, layer.ln_in, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
-            self._lin(buf.x, layer.qkv, buf.qkv, timers, "qkv")
+                self._norm_after_down(buf, layer.ln_in)
             k_layer = pool.k_layer_view(li)
             v_layer = pool.v_layer_view(li)
-            qkv_rope_append(buf.qkv, self.rope, seq_lens, buf.q, k_layer, v_layer, block_tables, s.heads,
-                            s.kv_heads, err=buf.err)
+            if sp["qkv"] > 1:
+                self._partials(buf.x, layer.qkv, buf.part, timers, "qkv")
+                qkv_rope_append_splits(buf.part, sp["qkv"], layer.qkv[3], self.rope, seq_lens, buf.q, k_layer,
+                                       v_layer, block_tables, s.heads, s.kv_heads, err=buf.err)
+            else:
+                self._lin(buf.x, layer.qkv, buf.qkv, timers, "qkv")
+                qkv_rope_append(buf.qkv, self.rope, seq_lens, buf.q, k_layer, v_layer, block_tables, s.heads,
+                                s.kv_heads, err=buf.err)
             ev = self._tick(timers, "attn")
             _paged_decode(buf.q.view(bsz, s.heads, 1, s.head_dim), k_layer, v_layer, block_tables, buf.attn_lens,
                           s.head_dim ** -0.5, s.group, out=buf.attn)
             self._tock(timers, "attn", ev)
-            self._lin(buf.attn.view(bsz, -1), layer.o, buf.o, timers, "o")
-            add_rmsnorm(buf.o, layer.ln_post, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
+            if sp["o"] > 1:
+                self._partials(buf.attn.view(bsz, -1), layer.o, buf.part, timers, "o")
+                add_rmsnorm_splits(buf.part, sp["o"], layer.o[3], layer.ln_post, eps, buf.x, residual=buf.h,
+                                   residual_out=buf.h)
+            else:
+                self._lin(buf.attn.view(bsz, -1), layer.o, buf.o, timers, "o")
+                add_rmsnorm(buf.o, layer.ln_post, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
             self._lin(buf.x, layer.gate_up, buf.gu, timers, "gate_up")
             silu_mul(buf.gu, out=buf.act)
-            self._lin(buf.act, layer.down, buf.mlp, timers, "down")
-        add_rmsnorm(buf.mlp, self.ln_final, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
+            if sp["down"] > 1:
+                self._partials(buf.act, layer.down, buf.part, timers, "down")
+            else:
+                self._lin(buf.act, layer.down, buf.mlp, timers, "down")
+        self._norm_after_down(buf, self.ln_final)
         self._lin(buf.x, self.lm_head, buf.logits, timers, "lm_head")
         seq_lens.add_(1)
         nxt = buf.logits.argmax(dim=-1)
         return (nxt, buf.logits) if return_logits else nxt
+
+    def _norm_after_down(self, buf: _Buffers, weight: torch.Tensor) -> None:
+        """x = RMSNorm(h + down output) * weight; h updated in place."""
+        eps = self.shape.rms_eps
+        if buf.splits["down"] > 1:
+            add_rmsnorm_splits(buf.part, buf.splits["down"], None, weight, eps, buf.x, residual=buf.h,
+                               residual_out=buf.h)
+        else:
+            add_rmsnorm(buf.mlp, weight, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
+
+    def _partials(self, x, w, part, timers, name):
+        packed, scale, n, _ = w
+        ev = self._tick(timers, name)
+        int8_linear_partials(x, packed, scale, n, part)
+        self._tock(timers, name, ev)
 
     def _lin(self, x, w, out, timers, name):
         packed, scale, n, bias = w

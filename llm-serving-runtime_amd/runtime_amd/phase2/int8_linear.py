@@ -118,6 +118,36 @@ def int8_linear(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias
     return y.view(*lead, n)
 
 
+def linear_splits(m: int, n: int, k: int) -> int:
+    """K splits the MFMA kernel uses for ``[m, k] x [k, n]`` (1: :func:`int8_linear` writes y directly)."""
+    return int(_hip.load().mx_w8a16_splits(m, n, k))
+
+
+def int8_linear_partials(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, out_features: int,
+                         partials: torch.Tensor) -> int:
+    """Split-K partials of ``x @ (q*s)^T`` into fp32 ``partials`` (``[splits, M, N]`` contiguous, or larger).
+
+    Returns the split count. Summing the splits, adding the bias and rounding
+    to fp16 gives :func:`int8_linear`'s output; the decode glue kernels do that
+    in their input stage (``mx_*_splits``), so no reduce launch is needed.
+    """
+    _hip.require_device_tensor(x, "x")
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise ValueError("int8_linear_partials expects fp16 x [M, K]")
+    m, k = (int(v) for v in x.shape)
+    n = int(out_features)
+    if x.stride(-1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    if partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous fp32 tensor")
+    lib = _hip.load()
+    splits = int(lib.mx_w8a16_splits(m, n, k))
+    _hip.check(lib.mx_w8a16_linear_partials(x.data_ptr(), m, k, x.stride(0), packed.data_ptr(), scale.data_ptr(), n,
+                                            partials.data_ptr(), partials.numel() * 4, _hip.stream_handle(x.device)),
+               "mx_w8a16_linear_partials")
+    return splits
+
+
 class Int8Linear(nn.Module):
     """Drop-in for ``nn.Linear`` on the decode path with int8 weights and fp16 scales."""
 

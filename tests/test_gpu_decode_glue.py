@@ -234,3 +234,57 @@ def test_glue_rejects_bad_arguments():
         silu_mul(torch.randn(2, 12, device=DEV).half())  # I = 6, not a multiple of 8
     with pytest.raises(ValueError):
         add_rmsnorm(torch.randn(2, 8), torch.ones(8), 1e-6)  # CPU tensors
+
+
+def test_split_consumers_equal_fp16_consumers():
+    """mx_qkv_rope_append_splits / mx_add_rmsnorm_splits on a projection's split partials give
+    bit-for-bit what the fp16 kernels give on mx_w8a16_linear's output of the same projection."""
+    from runtime_amd.phase2.decode_glue import (add_rmsnorm, add_rmsnorm_splits, qkv_rope_append,
+                                                qkv_rope_append_splits, rope_table)
+    from runtime_amd.phase2.int8_linear import (int8_linear, int8_linear_partials, linear_splits, pack_weight,
+                                                quantize_weight)
+
+    b, hq, hkv, d, hidden = 32, 32, 8, 128, 4096
+    g = torch.Generator(device=DEV).manual_seed(77)
+    x = torch.randn(b, hidden, generator=g, device=DEV).half()
+
+    # qkv projection with bias -> RoPE + append
+    n_qkv = (hq + 2 * hkv) * d
+    q8, s8 = quantize_weight(torch.randn(n_qkv, hidden, generator=g, device=DEV) * 0.02)
+    pk = pack_weight(q8)
+    bias = (torch.randn(n_qkv, generator=g, device=DEV) * 0.1).half()
+    splits = linear_splits(b, n_qkv, hidden)
+    assert splits > 1
+    part = torch.empty(splits * b * n_qkv, dtype=torch.float32, device=DEV)
+    int8_linear_partials(x, pk, s8, n_qkv, part)
+    qkv = int8_linear(x, pk, s8, bias, n_qkv)
+    rope = rope_table(4096, d, 5e5, DEV)
+    pos = torch.randint(0, 1000, (b,), generator=torch.Generator().manual_seed(1), dtype=torch.int32).to(DEV)
+    tables = torch.arange(b * 64, dtype=torch.int32, device=DEV).view(b, 64)
+    outs = []
+    for use_splits in (False, True):
+        pool = _pool(b * 64, hkv, 16, d, layers=1, seed=3)
+        q_out = torch.empty(b, hq * d, dtype=torch.float16, device=DEV)
+        if use_splits:
+            qkv_rope_append_splits(part, splits, bias, rope, pos, q_out, pool.k_layer_view(0), pool.v_layer_view(0),
+                                   tables, hq, hkv)
+        else:
+            qkv_rope_append(qkv, rope, pos, q_out, pool.k_layer_view(0), pool.v_layer_view(0), tables, hq, hkv)
+        outs.append((q_out.clone(), pool.k_layer_view(0).clone(), pool.v_layer_view(0).clone()))
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+
+    # o projection (no bias) -> residual add + RMSNorm
+    o8, os8 = quantize_weight(torch.randn(hidden, hidden, generator=g, device=DEV) * 0.02)
+    po = pack_weight(o8)
+    so = linear_splits(b, hidden, hidden)
+    part_o = torch.empty(so * b * hidden, dtype=torch.float32, device=DEV)
+    int8_linear_partials(x, po, os8, hidden, part_o)
+    y = int8_linear(x, po, os8, None, hidden)
+    res = torch.randn(b, hidden, generator=g, device=DEV).half()
+    w = (1 + 0.1 * torch.randn(hidden, generator=g, device=DEV)).half()
+    ra, rb = res.clone(), res.clone()
+    out_a = add_rmsnorm(y, w, 1e-5, residual=ra, residual_out=ra)
+    out_b = torch.empty_like(out_a)
+    add_rmsnorm_splits(part_o, so, None, w, 1e-5, out_b, residual=rb, residual_out=rb)
+    assert torch.equal(out_a, out_b) and torch.equal(ra, rb)

@@ -169,3 +169,39 @@ def test_quantize_model_swaps_linears():
     assert y.shape == (3, 64) and y.dtype == torch.float16
     q, s = int8_quant.quantize_per_channel(w)
     np.testing.assert_allclose(y.float().cpu().numpy(), int8_quant.linear_ref_fp32(x, q, s, b), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 4096), (4096, 14336)])
+def test_split_partials_sum_to_linear_output(n, k):
+    """qkv, o and down at M=32 split K: the partials, summed bias-first in split order and
+    rounded, are exactly mx_w8a16_linear's output (its reduce adds in that order)."""
+    from runtime_amd.phase2.int8_linear import (int8_linear, int8_linear_partials, linear_splits, pack_weight,
+                                                quantize_weight)
+
+    g = torch.Generator(device="cuda").manual_seed(n + k)
+    w = torch.randn(n, k, generator=g, device="cuda") * 0.02
+    q, s = quantize_weight(w)
+    packed = pack_weight(q)
+    x = torch.randn(32, k, generator=g, device="cuda").half()
+    bias = (torch.randn(n, generator=g, device="cuda") * 0.1).half()
+    splits = linear_splits(32, n, k)
+    assert splits == 8
+    part = torch.full((splits * 32 * n,), float("nan"), dtype=torch.float32, device="cuda")
+    assert int8_linear_partials(x, packed, s, n, part) == splits
+    acc = bias.float().unsqueeze(0).expand(32, n).clone()
+    for sp in part.view(splits, 32, n):
+        acc = acc + sp
+    y = int8_linear(x, packed, s, bias, n)
+    assert torch.equal(acc.half(), y)
+    want = int8_quant.linear_ref(x.cpu().numpy(), q.cpu().numpy(), s.cpu().numpy(), bias.cpu().numpy())
+    np.testing.assert_allclose(y.cpu().float().numpy(), want.astype(np.float32), atol=1e-2, rtol=1e-2)
+
+
+def test_partials_reject_unsplit_shapes():
+    from runtime_amd.phase2.int8_linear import int8_linear_partials, linear_splits, pack_weight, quantize_weight
+
+    q, s = quantize_weight(torch.randn(28672, 64, device="cuda"))
+    assert linear_splits(32, 28672, 64) == 1
+    with pytest.raises(ValueError):
+        int8_linear_partials(torch.zeros(32, 64, device="cuda").half(), pack_weight(q), s, 28672,
+                             torch.empty(1 << 20, device="cuda"))
