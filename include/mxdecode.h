@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 3
+#define MX_ABI_VERSION 5
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -92,6 +92,34 @@ int mx_w8a16_splits(int64_t M, int64_t N, int64_t K);
  * linear as one HF module call (worker_server.py:194-205). */
 int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                              const uint16_t* scale, int64_t N, float* partials, size_t partials_bytes, void* stream);
+
+/* mx_w8a16_linear / mx_w8a16_linear_partials with the SwiGLU product as x:
+ * x[m, k] = fp16(fp16(silu(gate_up[m, k])) * gate_up[m, K + k]) for k < K,
+ * formed while the kernel stages x (gate_up: fp16 [M, 2K], row stride
+ * gu_stride >= 2K). The MLP's down projection of a gate||up projection
+ * (transformers' down_proj(act_fn(gate_proj(x)) * up_proj(x)), reached from
+ * worker_server.py:771-775) without materialising the product. Requires
+ * 4 < M <= 64 (the MFMA path); smaller batches use mx_silu_mul and
+ * mx_w8a16_linear. */
+int mx_w8a16_linear_swiglu(const uint16_t* gate_up, int64_t M, int64_t K, int64_t gu_stride, const uint8_t* packed,
+                           const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t N, int64_t y_stride,
+                           void* workspace, size_t workspace_bytes, void* stream);
+int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t M, int64_t K, int64_t gu_stride,
+                                    const uint8_t* packed, const uint16_t* scale, int64_t N, float* partials,
+                                    size_t partials_bytes, void* stream);
+
+/* gate||up projection with the SwiGLU product in its epilogue:
+ * y[m, c] = fp16(fp16(silu(g)) * u), g = fp16(x W_gate[c]^T (+ b)), u likewise
+ * with W_up[c], for c < I; y is fp16 [M, I] (row stride y_stride). The packed
+ * weight is the [2I, K] matrix whose rows alternate in groups of 8: rows
+ * 16t + [0, 8) = gate rows 8t + [0, 8), rows 16t + [8, 16) = up rows
+ * 8t + [0, 8) (scale and bias reordered the same way), quantized and packed
+ * as usual. Replaces transformers' act_fn(gate_proj(x)) * up_proj(x) (reached
+ * from worker_server.py:771-775) with one launch and half the output bytes.
+ * Requires 4 < M <= 64 and mx_w8a16_splits(M, 2I, K) == 1. */
+int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
+                           const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I, int64_t y_stride,
+                           void* stream);
 
 /* ----------------------------------------------------------------------------
  * Paged-attention decode.

@@ -72,6 +72,22 @@ __device__ __forceinline__ float xor_max_16_32(float v) {
     row_swap32(c, d);
     return fmaxf(c, d);
 }
+// Keeps v in an fp32 register, so a following fp16 conversion rounds the fp32 value
+// instead of being folded with the arithmetic that produced v into one mixed-precision
+// FMA (a single rounding). Kernels whose outputs must agree bit for bit round the same way.
+__device__ __forceinline__ float pin_f32(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// silu(g) = g / (1 + e^-g) with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32,
+// about 1 ulp each): the SwiGLU product is rounded to fp16 right after, and the IEEE
+// divide this library otherwise compiles to is several times longer. The result is pinned
+// (pin_f32): callers round it to fp16 from fp32, as torch's fp16 SiLU does.
+__device__ __forceinline__ float silu_f32(float g) {
+    return pin_f32(g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f)));
+}
+
 // v + v[l^8] inside each 16-lane row (DPP row_ror:8).
 __device__ __forceinline__ float xor8_sum(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));

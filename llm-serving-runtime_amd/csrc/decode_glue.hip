@@ -312,8 +312,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, 
     half8v o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float gf = (float)g[e];
-        const _Float16 s = (_Float16)(gf / (1.0f + expf(-gf)));
+        const _Float16 s = (_Float16)silu_f32((float)g[e]);
         o[e] = (_Float16)((float)s * (float)u[e]);
     }
     st16(out + m * os + c * 8, as_u4(o));

@@ -260,7 +260,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 // split, the epilogue writes fp16 y (scale, bias); otherwise it writes the
 // scaled fp32 partial of its split, which the caller or reduce_kernel adds.
 // ---------------------------------------------------------------------------
-template <int MT, int NPW, int WAVES, int P>
+// SW: x is the SwiGLU product of a gate||up row, silu(gate[k]) * up[k], formed while
+// staging each x k-tile: `x` points at gate_up rows [M, 2K] (gate in columns [0, K),
+// up in [K, 2K), row stride xs), rounded as the unfused path rounds it
+// (fp16(fp16(silu(g)) * u), mx_silu_mul).
+//
+// GU: gate||up output with the SwiGLU product taken in the epilogue. The weight rows
+// are interleaved in groups of 8 (rows 16t + [0, 8) are gate channels 8t + [0, 8),
+// rows 16t + [8, 16) the matching up channels; see mx_w8a16_gateup_interleave), so
+// the lanes holding gate channel c and up channel c differ by 8 and one lane swap
+// pairs them. y is [M, N/2] and receives fp16(fp16(silu(g)) * u), g and u rounded to
+// fp16 first as the unfused gate/up projections are. Needs one K split.
+template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false>
 __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
@@ -301,13 +312,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
     struct St {
         uint4 w[NPW];
         uint4 x[XC];
+        uint4 up[SW ? XC : 1];
     };
+    const int up_off = KT * kTileK;  // SW: the up half of a gate_up row
     auto load = [&](int j, St& st) {
         const int kt = kt_lo + (j < nj ? j : nj - 1);
 #pragma unroll
         for (int p = 0; p < NPW; ++p) st.w[p] = (wbase + ((int64_t)p * KT + kt) * 64)[lane];
 #pragma unroll
-        for (int u = 0; u < XC; ++u) st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
+        for (int u = 0; u < XC; ++u) {
+            st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
+            if (SW) st.up[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + up_off + kt * kTileK);
+        }
     };
 
     float4v acc[NPW][MT];
@@ -322,7 +338,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
     auto compute = [&](const St& st) {
         _Float16* buf = xl[step & 1];
 #pragma unroll
-        for (int u = 0; u < XC; ++u) *reinterpret_cast<uint4*>(buf + xdst[u]) = st.x[u];
+        for (int u = 0; u < XC; ++u) {
+            if (SW) {
+                const half8v gt = __builtin_bit_cast(half8v, st.x[u]);
+                const half8v up = __builtin_bit_cast(half8v, st.up[u]);
+                half8v a;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 sg = (_Float16)silu_f32((float)gt[e]);
+                    a[e] = (_Float16)((float)sg * (float)up[e]);
+                }
+                *reinterpret_cast<uint4*>(buf + xdst[u]) = __builtin_bit_cast(uint4, a);
+            } else {
+                *reinterpret_cast<uint4*>(buf + xdst[u]) = st.x[u];
+            }
+        }
         __syncthreads();
         half8v a[MT][2];
 #pragma unroll
@@ -347,8 +377,28 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
         St st[P];
         PIPELINE_BODY(P, nj, st, load, compute(st[s]))
     }
-    if (!valid) return;
     const int N = NT * kTileN;
+    if (GU) {
+        // Every lane takes part in the swap; out-of-range waves just do not store.
+        const int c = nt_c * (kTileN / 2) + (r & 7);  // SwiGLU channel of this lane pair
+        const int64_t n = (int64_t)nt_c * kTileN + r;
+        const float sc = h2f(scale, n);
+        const float bi = bias ? h2f(bias, n) : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = (float)(_Float16)pin_f32(acc[0][mt][i] * sc + bi);  // this lane's projection
+                const float other = __shfl_xor(v, 8);
+                const int m = mt * 16 + 4 * g + i;
+                if (valid && r < 8 && m < M) {
+                    const _Float16 sg = (_Float16)silu_f32(v);
+                    y[(int64_t)m * ys + c] = f2h_bits((float)sg * other);
+                }
+            }
+        return;
+    }
+    if (!valid) return;
 #pragma unroll
     for (int p = 0; p < NPW; ++p) {
         const int64_t n = (int64_t)(nt_w + p) * kTileN + r;
@@ -360,9 +410,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
             for (int i = 0; i < 4; ++i) {
                 const int m = mt * 16 + 4 * g + i;
                 if (m >= M) continue;
-                const float v = acc[p][mt][i] * sc;
-                if (KS == 1) y[(int64_t)m * ys + n] = f2h_bits(v + bi);
-                else partial[((int64_t)ks * M + m) * N + n] = v;
+                if (KS == 1) y[(int64_t)m * ys + n] = f2h_bits(pin_f32(acc[p][mt][i] * sc + bi));
+                else partial[((int64_t)ks * M + m) * N + n] = acc[p][mt][i] * sc;
             }
     }
 }
@@ -439,22 +488,23 @@ static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const u
 
 // The MFMA kernel alone: KS == 1 writes fp16 y, KS > 1 writes the scaled fp32
 // partials [KS][M][N] to `partial` (no bias).
-template <int MT>
+template <int MT, bool SW, bool GU = false>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
     const int groups = (NT + kMfmaWaves - 1) / kMfmaWaves;
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, 1, kMfmaWaves, mfma_depth(MT)>), dim3(groups, KS),
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, 1, kMfmaWaves, mfma_depth(MT), SW, GU>), dim3(groups, KS),
                        dim3(kMfmaWaves * 64), 0, st, x, xs, M, w, s, b, y, ys, KT, NT, partial);
 }
 
+template <bool SW = false>
 static void launch_mfma_mt(int MT, const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial,
                            hipStream_t st) {
     switch (MT) {
-        case 1: launch_mfma<1>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        case 2: launch_mfma<2>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        case 3: launch_mfma<3>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        default: launch_mfma<4>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 1: launch_mfma<1, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 2: launch_mfma<2, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 3: launch_mfma<3, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        default: launch_mfma<4, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
     }
 }
 
@@ -576,4 +626,89 @@ extern "C" int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K,
     w8a16::launch_mfma_mt(pl.MT, x, x_stride, (int)M, packed, scale, nullptr, nullptr, 0, NT, KT, pl.KS, partials,
                           as_stream(stream));
     return check_launch("mx_w8a16_linear_partials");
+}
+
+// SwiGLU-input variants: x = silu(gate_up[:, :K]) * gate_up[:, K:2K], formed in the x
+// staging of the MFMA kernel (M >= 5).
+static int swiglu_checks(const char* what, const uint16_t* gu, int64_t M, int64_t K, int64_t gu_stride,
+                         const uint8_t* packed, const uint16_t* scale, int64_t N) {
+    if (!gu || !packed || !scale) return fail(MX_ERR_NULL, "%s: null pointer", what);
+    if (M <= w8a16::kValuMaxM || M > 64 || N <= 0 || K <= 0)
+        return fail(MX_ERR_UNSUPPORTED, "%s: needs %d < M <= 64 and positive N, K (M=%lld)", what, w8a16::kValuMaxM,
+                    (long long)M);
+    if (N % w8a16::kTileN || K % w8a16::kTileK)
+        return fail(MX_ERR_UNSUPPORTED, "%s: need N %% 16 == 0 and K %% 64 == 0", what);
+    if (gu_stride < 2 * K) return fail(MX_ERR_INVALID, "%s: gate_up row stride must cover 2K", what);
+    if (!aligned(gu, 16) || (gu_stride % 8) != 0 || !aligned(packed, 16))
+        return fail(MX_ERR_ALIGNMENT, "%s: gate_up rows and weights must be 16-byte aligned", what);
+    if (N / w8a16::kTileN > 0x7fffffff || K * 64 > 0x7fffffff) return fail(MX_ERR_UNSUPPORTED, "%s: too large", what);
+    return MX_OK;
+}
+
+extern "C" int mx_w8a16_linear_swiglu(const uint16_t* gate_up, int64_t M, int64_t K, int64_t gu_stride,
+                                      const uint8_t* packed, const uint16_t* scale, const uint16_t* bias, uint16_t* y,
+                                      int64_t N, int64_t y_stride, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+    int rc = swiglu_checks("mx_w8a16_linear_swiglu", gate_up, M, K, gu_stride, packed, scale, N);
+    if (rc != MX_OK) return rc;
+    if (!y) return fail(MX_ERR_NULL, "mx_w8a16_linear_swiglu: null output");
+    if (y_stride < N) return fail(MX_ERR_INVALID, "mx_w8a16_linear_swiglu: y row stride must cover N");
+    if (workspace && !aligned(workspace, 16))
+        return fail(MX_ERR_ALIGNMENT, "mx_w8a16_linear_swiglu: workspace must be 16-byte aligned");
+    const int NT = (int)(N / w8a16::kTileN), KT = (int)(K / w8a16::kTileK);
+    w8a16::Plan pl = w8a16::plan_for((int)M, NT, KT);
+    if (pl.KS > 1 && (!workspace || workspace_bytes < w8a16::workspace_for((int)M, NT, KT))) pl.KS = 1;
+    float* partial = static_cast<float*>(workspace);
+    hipStream_t st = as_stream(stream);
+    w8a16::launch_mfma_mt<true>(pl.MT, gate_up, gu_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, pl.KS,
+                                partial, st);
+    if (pl.KS > 1) w8a16::launch_reduce(partial, pl.KS, (int)M, (int)N, bias, y, y_stride, st);
+    return check_launch("mx_w8a16_linear_swiglu");
+}
+
+extern "C" int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t M, int64_t K, int64_t gu_stride,
+                                               const uint8_t* packed, const uint16_t* scale, int64_t N,
+                                               float* partials, size_t partials_bytes, void* stream) {
+    int rc = swiglu_checks("mx_w8a16_linear_partials_swiglu", gate_up, M, K, gu_stride, packed, scale, N);
+    if (rc != MX_OK) return rc;
+    if (!partials) return fail(MX_ERR_NULL, "mx_w8a16_linear_partials_swiglu: null partials");
+    if (!aligned(partials, 16)) return fail(MX_ERR_ALIGNMENT, "mx_w8a16_linear_partials_swiglu: partials alignment");
+    const int NT = (int)(N / w8a16::kTileN), KT = (int)(K / w8a16::kTileK);
+    const w8a16::Plan pl = w8a16::plan_for((int)M, NT, KT);
+    if (pl.KS == 1) return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear_partials_swiglu: shape is not split");
+    if (partials_bytes < (size_t)pl.KS * M * N * sizeof(float))
+        return fail(MX_ERR_WORKSPACE, "mx_w8a16_linear_partials_swiglu: partials need %zu bytes",
+                    (size_t)pl.KS * M * N * sizeof(float));
+    w8a16::launch_mfma_mt<true>(pl.MT, gate_up, gu_stride, (int)M, packed, scale, nullptr, nullptr, 0, NT, KT, pl.KS,
+                                partials, as_stream(stream));
+    return check_launch("mx_w8a16_linear_partials_swiglu");
+}
+
+extern "C" int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
+                                      const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I,
+                                      int64_t y_stride, void* stream) {
+    if (!x || !packed || !scale || !y) return fail(MX_ERR_NULL, "mx_w8a16_gateup_swiglu: null pointer");
+    if (M <= w8a16::kValuMaxM || M > 64 || I <= 0 || K <= 0)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: needs %d < M <= 64 (M=%lld)", w8a16::kValuMaxM,
+                    (long long)M);
+    if (I % 8 || K % w8a16::kTileK)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: need I %% 8 == 0 and K %% 64 == 0");
+    if (x_stride < K || y_stride < I) return fail(MX_ERR_INVALID, "mx_w8a16_gateup_swiglu: row strides too short");
+    if (!aligned(x, 16) || (x_stride % 8) != 0 || !aligned(packed, 16))
+        return fail(MX_ERR_ALIGNMENT, "mx_w8a16_gateup_swiglu: x rows and weights must be 16-byte aligned");
+    const int NT = (int)(2 * I / w8a16::kTileN), KT = (int)(K / w8a16::kTileK);
+    if ((int64_t)NT * w8a16::kTileN != 2 * I || K * 64 > 0x7fffffff)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: bad shape");
+    const w8a16::Plan pl = w8a16::plan_for((int)M, NT, KT);
+    if (pl.KS != 1)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: shape splits K (mx_w8a16_splits(M, 2I, K) = %d)",
+                    pl.KS);
+    hipStream_t st = as_stream(stream);
+    switch (pl.MT) {
+        case 1: w8a16::launch_mfma<1, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
+        case 2: w8a16::launch_mfma<2, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
+        case 3: w8a16::launch_mfma<3, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
+        default: w8a16::launch_mfma<4, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
+    }
+    return check_launch("mx_w8a16_gateup_swiglu");
 }

@@ -15,8 +15,9 @@ current stream:
     q, K/V slot <- RoPE(qkv), v            mx_qkv_rope_append
     a = paged_attention(q, pool)           mx_paged_attn_decode
     h += a Wo^T;  x = RMSNorm(h)           mx_w8a16_linear, mx_add_rmsnorm
-    gu = x Wgu^T;  m = silu(g) * u         mx_w8a16_linear, mx_silu_mul
-    h += m Wdown^T                         mx_w8a16_linear (+ the next add_rmsnorm)
+    a = silu(x Wg^T) * (x Wu^T)            mx_w8a16_gateup_swiglu (gate and up rows
+                                           interleaved by 8, product in the epilogue)
+    h += a Wdown^T                         mx_w8a16_linear (+ the next add_rmsnorm)
     logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, torch argmax
 
 A projection whose shape splits K (``mx_w8a16_splits`` > 1: qkv, o and down at
@@ -29,7 +30,11 @@ Activations live in per-batch-size buffers allocated on the first step, so a
 whole step can be captured in one HIP graph and replayed. Architecture is
 Llama / Qwen2 style (pre-norm, rotate-half RoPE, GQA, SwiGLU, untied int8
 lm_head); :meth:`Int8DecodeModel.from_hf` loads the weights of an HF
-``LlamaForCausalLM`` / ``Qwen2ForCausalLM``.
+``LlamaForCausalLM`` / ``Qwen2ForCausalLM``. The gate||up weight is stored
+with gate and up rows interleaved in groups of 8 (``gateup_interleave``);
+where the fused epilogue does not apply (batch <= 4, or a batch whose
+gate||up GEMM splits K) the projection runs plain, its output is put back in
+[gate | up] order and ``mx_silu_mul`` forms the product.
 """
 
 from __future__ import annotations
@@ -41,7 +46,8 @@ import torch
 
 from .decode_glue import (add_rmsnorm, add_rmsnorm_splits, qkv_rope_append, qkv_rope_append_splits, rope_table,
                           silu_mul)
-from .int8_linear import int8_linear, int8_linear_partials, linear_splits, pack_weight, quantize_weight
+from .int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu, int8_linear,
+                          int8_linear_partials, linear_splits, pack_weight, quantize_weight)
 from .paged_attention_hip import _decode as _paged_decode
 
 
@@ -149,8 +155,9 @@ class Int8DecodeModel:
         """Quantize an HF ``LlamaForCausalLM`` / ``Qwen2ForCausalLM`` (fp32 weights) into this layout.
 
         q/k/v are stacked into one projection (rows q, then k, then v) and
-        gate/up into one (gate rows first). Per-output-channel quantization is
-        row-wise, so each stacked weight quantizes exactly as its parts would.
+        gate/up into one with rows interleaved by 8 (``gateup_interleave``).
+        Per-output-channel quantization is row-wise, so each stacked weight
+        quantizes exactly as its parts would.
         Norms, biases and the embedding are stored in fp16; lm_head is int8.
         """
         cfg = model.config
@@ -182,7 +189,7 @@ class Int8DecodeModel:
                     ln_post=f16(layer.post_attention_layernorm.weight),
                     qkv=(*_quantize(qkv_w, dev), bias),
                     o=(*_quantize(at.o_proj.weight, dev), None),
-                    gate_up=(*_quantize(torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], dim=0), dev), None),
+                    gate_up=(*_quantize(gateup_interleave(mlp.gate_proj.weight, mlp.up_proj.weight), dev), None),
                     down=(*_quantize(mlp.down_proj.weight, dev), None),
                 ))
             self.ln_final = f16(model.model.norm.weight)
@@ -193,13 +200,13 @@ class Int8DecodeModel:
     def linear_bytes(self, batch: int) -> dict[str, int]:
         s = self.shape
 
-        def lb(n, k, bias=False):
-            return n * k + 2 * n + 2 * batch * k + 2 * batch * n + (2 * n if bias else 0)
+        def lb(n, k, bias=False, out=None):
+            return n * k + 2 * n + 2 * batch * k + 2 * batch * (n if out is None else out) + (2 * n if bias else 0)
 
         return {
             "qkv": lb(s.qkv_out, s.hidden, s.qkv_bias),
             "o": lb(s.hidden, s.heads * s.head_dim),
-            "gate_up": lb(2 * s.intermediate, s.hidden),
+            "gate_up": lb(2 * s.intermediate, s.hidden, out=s.intermediate),  # writes silu(g) * u only
             "down": lb(s.hidden, s.intermediate),
             "lm_head": lb(s.vocab, s.hidden),
         }
@@ -276,8 +283,7 @@ class Int8DecodeModel:
             else:
                 self._lin(buf.attn.view(bsz, -1), layer.o, buf.o, timers, "o")
                 add_rmsnorm(buf.o, layer.ln_post, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
-            self._lin(buf.x, layer.gate_up, buf.gu, timers, "gate_up")
-            silu_mul(buf.gu, out=buf.act)
+            self._gate_up(buf, layer.gate_up, bsz, timers)
             if sp["down"] > 1:
                 self._partials(buf.act, layer.down, buf.part, timers, "down")
             else:
@@ -296,6 +302,17 @@ class Int8DecodeModel:
                                residual_out=buf.h)
         else:
             add_rmsnorm(buf.mlp, weight, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
+
+    def _gate_up(self, buf: _Buffers, w, bsz: int, timers) -> None:
+        """act = silu(gate) * up from the interleaved gate||up weight."""
+        packed, scale, n, bias = w
+        ev = self._tick(timers, "gate_up")
+        if bsz > 4 and buf.splits["gate_up"] == 1:
+            int8_gateup_swiglu(buf.x, packed, scale, bias, n // 2, out=buf.act)
+        else:
+            int8_linear(buf.x, packed, scale, bias, n, out=buf.gu)
+            silu_mul(gateup_deinterleave(buf.gu).contiguous(), out=buf.act)
+        self._tock(timers, "gate_up", ev)
 
     def _partials(self, x, w, part, timers, name):
         packed, scale, n, _ = w

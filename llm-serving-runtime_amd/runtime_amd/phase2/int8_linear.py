@@ -148,6 +148,84 @@ def int8_linear_partials(x: torch.Tensor, packed: torch.Tensor, scale: torch.Ten
     return splits
 
 
+def _gate_up_rows(gate_up: torch.Tensor) -> torch.Tensor:
+    _hip.require_device_tensor(gate_up, "gate_up")
+    if gate_up.dtype != torch.float16 or gate_up.dim() != 2 or gate_up.shape[1] % 2:
+        raise ValueError("gate_up must be fp16 [M, 2K]")
+    if gate_up.stride(-1) != 1 or gate_up.stride(0) % 8 or gate_up.data_ptr() % 16:
+        gate_up = gate_up.contiguous()
+    return gate_up
+
+
+def int8_linear_swiglu(gate_up: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+                       out_features: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``y = (silu(g) * u) @ (q*s)^T + b`` for ``gate_up = [g | u]`` fp16 ``[M, 2K]``, 4 < M <= 64.
+
+    The product is formed inside the GEMM's x staging (same rounding as
+    ``mx_silu_mul``), so it is never written out.
+    """
+    gu = _gate_up_rows(gate_up)
+    m, k = int(gu.shape[0]), int(gu.shape[1]) // 2
+    n = int(out_features)
+    y = torch.empty((m, n), dtype=torch.float16, device=gu.device) if out is None else out.view(m, n)
+    lib = _hip.load()
+    ws_ptr, ws_bytes = _workspace(gu.device, int(lib.mx_w8a16_workspace_bytes(m, n, k)))
+    _hip.check(lib.mx_w8a16_linear_swiglu(gu.data_ptr(), m, k, gu.stride(0), packed.data_ptr(), scale.data_ptr(),
+                                          bias.data_ptr() if bias is not None else None, y.data_ptr(), n, y.stride(0),
+                                          ws_ptr, ws_bytes, _hip.stream_handle(gu.device)), "mx_w8a16_linear_swiglu")
+    return y
+
+
+def int8_linear_partials_swiglu(gate_up: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, out_features: int,
+                                partials: torch.Tensor) -> int:
+    """:func:`int8_linear_partials` with the SwiGLU product of ``gate_up`` as x; returns the split count."""
+    gu = _gate_up_rows(gate_up)
+    m, k = int(gu.shape[0]), int(gu.shape[1]) // 2
+    n = int(out_features)
+    if partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous fp32 tensor")
+    lib = _hip.load()
+    splits = int(lib.mx_w8a16_splits(m, n, k))
+    _hip.check(lib.mx_w8a16_linear_partials_swiglu(gu.data_ptr(), m, k, gu.stride(0), packed.data_ptr(),
+                                                   scale.data_ptr(), n, partials.data_ptr(), partials.numel() * 4,
+                                                   _hip.stream_handle(gu.device)), "mx_w8a16_linear_partials_swiglu")
+    return splits
+
+
+def gateup_interleave(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """Stack gate and up rows (``[I, ...]`` each) in alternating groups of 8, the row order
+    ``mx_w8a16_gateup_swiglu`` expects: rows 16t + [0, 8) = gate 8t + [0, 8), rows
+    16t + [8, 16) = up 8t + [0, 8). Works for weights ``[I, K]`` and for scales/biases ``[I]``."""
+    if gate.shape != up.shape or gate.shape[0] % 8:
+        raise ValueError("gate and up must have the same shape with a multiple of 8 rows")
+    i = gate.shape[0]
+    rest = tuple(gate.shape[1:])
+    return torch.stack((gate.reshape(i // 8, 8, *rest), up.reshape(i // 8, 8, *rest)), dim=1).reshape(2 * i, *rest)
+
+
+def gateup_deinterleave(y: torch.Tensor) -> torch.Tensor:
+    """Inverse of :func:`gateup_interleave` on the last dimension: ``[..., 2I]`` -> ``[gate | up]``."""
+    lead, n = y.shape[:-1], y.shape[-1]
+    return y.reshape(*lead, n // 16, 2, 8).transpose(-3, -2).reshape(*lead, n)
+
+
+def int8_gateup_swiglu(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+                       inter: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(x W_gate^T) * (x W_up^T)`` from an interleaved gate||up weight, as fp16 ``[M, inter]``."""
+    _hip.require_device_tensor(x, "x")
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise ValueError("int8_gateup_swiglu expects fp16 x [M, K]")
+    if x.stride(-1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    m, k = int(x.shape[0]), int(x.shape[1])
+    y = torch.empty((m, inter), dtype=torch.float16, device=x.device) if out is None else out.view(m, inter)
+    _hip.check(_hip.load().mx_w8a16_gateup_swiglu(
+        x.data_ptr(), m, k, x.stride(0), packed.data_ptr(), scale.data_ptr(),
+        bias.data_ptr() if bias is not None else None, y.data_ptr(), inter, y.stride(0),
+        _hip.stream_handle(x.device)), "mx_w8a16_gateup_swiglu")
+    return y
+
+
 class Int8Linear(nn.Module):
     """Drop-in for ``nn.Linear`` on the decode path with int8 weights and fp16 scales."""
 

@@ -205,3 +205,56 @@ def test_partials_reject_unsplit_shapes():
     with pytest.raises(ValueError):
         int8_linear_partials(torch.zeros(32, 64, device="cuda").half(), pack_weight(q), s, 28672,
                              torch.empty(1 << 20, device="cuda"))
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 4096, 14336), (32, 4096, 1024), (5, 256, 128), (64, 896, 4864)])
+def test_swiglu_linear_equals_silu_mul_then_linear(m, n, k):
+    """The SwiGLU product formed in the GEMM's x staging rounds exactly as mx_silu_mul does,
+    so the fused call equals silu_mul followed by the plain linear, bit for bit, and the
+    partials variant sums to it."""
+    from runtime_amd.phase2.decode_glue import silu_mul
+    from runtime_amd.phase2.int8_linear import (int8_linear_partials_swiglu, int8_linear_swiglu, linear_splits,
+                                                pack_weight, quantize_weight)
+
+    g = torch.Generator(device="cuda").manual_seed(m * 7 + n + k)
+    q, s = quantize_weight(torch.randn(n, k, generator=g, device="cuda") * 0.02)
+    packed = pack_weight(q)
+    gu = (2 * torch.randn(m, 2 * k, generator=g, device="cuda")).half()
+    bias = (torch.randn(n, generator=g, device="cuda") * 0.1).half()
+    want = int8_linear(silu_mul(gu), packed, s, bias, n)
+    got = int8_linear_swiglu(gu, packed, s, bias, n)
+    assert torch.equal(got, want)
+    splits = linear_splits(m, n, k)
+    if splits > 1:
+        part = torch.empty(splits * m * n, dtype=torch.float32, device="cuda")
+        int8_linear_partials_swiglu(gu, packed, s, n, part)
+        acc = bias.float().unsqueeze(0).expand(m, n).clone()
+        for sp in part.view(splits, m, n):
+            acc = acc + sp
+        assert torch.equal(acc.half(), want)
+    with pytest.raises(ValueError):
+        int8_linear_swiglu(gu[:4], packed, s, bias, n)  # M <= 4 takes the GEMV path, not fused
+
+
+@pytest.mark.parametrize("m,inter,k", [(32, 14336, 4096), (7, 4864, 896), (64, 1024, 256)])
+def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
+    """gate||up with interleaved rows and the SwiGLU product in the epilogue equals the plain
+    [gate | up] projection followed by mx_silu_mul, bit for bit."""
+    from runtime_amd.phase2.decode_glue import silu_mul
+    from runtime_amd.phase2.int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu,
+                                                linear_splits)
+
+    g = torch.Generator(device="cuda").manual_seed(m + inter + k)
+    wg = torch.randn(inter, k, generator=g, device="cuda") * 0.02
+    wu = torch.randn(inter, k, generator=g, device="cuda") * 0.02
+    x = torch.randn(m, k, generator=g, device="cuda").half()
+    plain_q, plain_s = quantize_weight(torch.cat([wg, wu]))
+    inter_w = gateup_interleave(wg, wu)
+    assert torch.equal(gateup_deinterleave(inter_w.t()).t(), torch.cat([wg, wu]))
+    iq, iscale = quantize_weight(inter_w)
+    assert torch.equal(gateup_interleave(plain_s[:inter], plain_s[inter:]), iscale)  # row-wise quantization
+    want = silu_mul(int8_linear(x, pack_weight(plain_q), plain_s, None, 2 * inter))
+    if linear_splits(m, 2 * inter, k) != 1:
+        pytest.skip("gate||up splits K at this shape; the epilogue fusion does not apply")
+    got = int8_gateup_swiglu(x, pack_weight(iq), iscale, None, inter)
+    assert torch.equal(got, want)
