@@ -264,8 +264,7 @@ def main() -> int:
     setup_s = time.perf_counter() - t_setup
 
     def step():
-        nxt = model.step(tokens, pool, tables_d, seq_lens)
-        tokens.copy_(nxt)
+        model.step(tokens, pool, tables_d, seq_lens, out=tokens)
 
     for _ in range(args.warmup):
         step()

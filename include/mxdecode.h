@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 5
+#define MX_ABI_VERSION 6
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -209,12 +209,14 @@ int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_t new_sb, i
  * position positions[b] (as mx_kv_append). Replaces HF's
  * apply_rotary_pos_emb (transformers, reached from worker_server.py:771-775)
  * followed by BlockPagedBatchLayer.update's write (paged_kv_cache.py:121-157).
- * A position outside the table writes q = 0 and no K/V. */
+ * A position outside the table writes q = 0 and no K/V. lens_out (optional,
+ * int32 [B]) receives positions[b] + 1, the KV length the attention call of
+ * this token reads (seq_lens in paged_attention_triton.py:43-50). */
 int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
                        const float* rope, int32_t max_pos, const int32_t* positions, uint16_t* q_out,
                        int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
                        const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, int32_t block_size,
-                       int32_t num_pool_blocks, int32_t* err, void* stream);
+                       int32_t num_pool_blocks, int32_t* err, int32_t* lens_out, void* stream);
 
 /* mx_qkv_rope_append with the QKV projection given as split-K partials
  * (fp32 [splits][B][(Hq + 2*Hkv) * D], from mx_w8a16_linear_partials): each
@@ -224,17 +226,22 @@ int mx_qkv_rope_append_splits(const float* partials, int32_t splits, const uint1
                               int32_t Hkv, int32_t D, const float* rope, int32_t max_pos, const int32_t* positions,
                               uint16_t* q_out, int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk,
                               int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
-                              int32_t block_size, int32_t num_pool_blocks, int32_t* err, void* stream);
+                              int32_t block_size, int32_t num_pool_blocks, int32_t* err, int32_t* lens_out,
+                              void* stream);
 
 /* h = residual ? fp16(x + residual) : x;  residual_out (if not NULL) = h;
  * out = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * weight), per row of H
  * (H % 8 == 0, H <= 16384). The decoder layer's residual add and the
  * following RMSNorm (transformers' Qwen2/Llama RMSNorm, reached from
- * worker_server.py:771-775) in one pass. out may alias x and residual_out may
- * alias residual; out must not alias residual_out. */
-int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride,
-                   const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out, int64_t out_stride,
-                   uint16_t* residual_out, int64_t ro_stride, void* stream);
+ * worker_server.py:771-775) in one pass. x_rows (optional, int64 [M]) gathers
+ * row m of x from row x_rows[m] (the embedding lookup of a step's tokens); x
+ * then holds x_count rows and an index outside [0, x_count) reads a zero row.
+ * out may alias x and residual_out may alias residual; out must not alias
+ * residual_out. */
+int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const int64_t* x_rows, int64_t x_count,
+                   const uint16_t* residual, int64_t r_stride, const uint16_t* weight, int32_t M, int32_t H,
+                   float eps, uint16_t* out, int64_t out_stride, uint16_t* residual_out, int64_t ro_stride,
+                   void* stream);
 
 /* mx_add_rmsnorm with x given as the split-K partials of the linear that
  * produced it (fp32 [splits][M][H] from mx_w8a16_linear_partials): x =
@@ -243,6 +250,14 @@ int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual
 int mx_add_rmsnorm_splits(const float* partials, int32_t splits, const uint16_t* bias, const uint16_t* residual,
                           int64_t r_stride, const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out,
                           int64_t out_stride, uint16_t* residual_out, int64_t ro_stride, void* stream);
+
+/* out[m] = index of the largest of logits[m, 0..N) (fp16, row stride
+ * `stride`), the first on ties, NaN above any number: the greedy argmax of the
+ * decode step (worker_server.py:786, torch argmax over the last logits).
+ * seq_lens (optional, int32 [M]) is incremented by one per row, advancing the
+ * KV lengths past the token just decoded. */
+int mx_argmax_rows(const uint16_t* logits, int64_t stride, int32_t M, int32_t N, int64_t* out, int32_t* seq_lens,
+                   void* stream);
 
 /* out[m, i] = fp16(fp16(silu(gate_up[m, i])) * gate_up[m, I + i]) for i < I
  * (I % 8 == 0): the SwiGLU product between the fused gate||up projection and

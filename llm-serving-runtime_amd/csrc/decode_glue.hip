@@ -127,6 +127,7 @@ struct RopeAppendParams {
     int64_t bt_sb;
     int max_blocks, bs, num_pool_blocks;
     int32_t* err;
+    int32_t* lens_out;  // optional: lens_out[b] = positions[b] + 1 (the attention length)
 };
 
 // Rotate-half RoPE (pairs i and i + D/2 share frequency i) on the q and k heads of one
@@ -146,6 +147,7 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendPar
     const uint16_t* row = SPLIT ? nullptr : p.qkv + (int64_t)b * p.qkv_stride + (int64_t)hs * p.D;
     const int64_t poff = SPLIT ? ((int64_t)b * (p.Hq + 2 * p.Hkv) + hs) * p.D : 0;  // element offset in a split
     const int pos = p.positions[b];
+    if (p.lens_out && hs == 0 && c == 0) p.lens_out[b] = pos + 1;
     if (hs < p.Hq + p.Hkv) {
         const int half = p.D >> 1;
         const int j = c * 4;
@@ -228,6 +230,8 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 struct NormParams {
     const uint16_t* x;     // fp16 rows, or NULL with part != NULL
     int64_t xs;
+    const int64_t* rows;   // optional gather: row m of x is x + rows[m] * xs (an embedding lookup)
+    int64_t xcount;        // rows of x a gather may read; an index outside [0, xcount) reads a zero row
     const float* part;     // split-K partials [splits][M][H] of the producing linear
     int splits;
     int64_t split_stride;
@@ -269,7 +273,10 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(NormParams p) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = t[e];
             } else {
-                v = as_h8(ld16(p.x + (int64_t)m * p.xs + c * 8));
+                const int64_t xr = p.rows ? p.rows[m] : m;
+                const bool in = (uint64_t)xr < (uint64_t)p.xcount;
+                v = as_h8(ld16(p.x + (in ? xr : 0) * p.xs + c * 8));
+                if (!in) v = half8v{};
             }
             if (p.res) {
                 const half8v r = as_h8(ld16(p.res + (int64_t)m * p.rs + c * 8));
@@ -316,6 +323,65 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, 
         o[e] = (_Float16)((float)s * (float)u[e]);
     }
     st16(out + m * os + c * 8, as_u4(o));
+}
+
+// Greedy token of each row: index of the largest logit, the first one on ties; NaN counts as
+// larger than any number (torch.argmax's convention). One workgroup of 1024 threads per row.
+constexpr int kArgThreads = 1024;
+
+__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
+    const bool na = a != a, nb = b != b;
+    if (na != nb) return na;
+    if (na || a == b) return ia < ib;
+    return a > b;
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t ls, int N,
+                                                             int64_t* __restrict__ out, int32_t* seq_lens) {
+    __shared__ float s_v[kArgThreads / 64];
+    __shared__ int s_i[kArgThreads / 64];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const _Float16* row = reinterpret_cast<const _Float16*>(logits) + (int64_t)m * ls;
+    float best = -__builtin_huge_valf();
+    int bi = 0x7fffffff;
+    const int chunks = N >> 3;
+    for (int c = tid; c < chunks; c += kArgThreads) {
+        const half8v v = as_h8(*reinterpret_cast<const uint4*>(row + c * 8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (arg_better((float)v[e], c * 8 + e, best, bi)) {
+                best = (float)v[e];
+                bi = c * 8 + e;
+            }
+    }
+    for (int n = chunks * 8 + tid; n < N; n += kArgThreads)
+        if (arg_better((float)row[n], n, best, bi)) {
+            best = (float)row[n];
+            bi = n;
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(bi, o);
+        if (arg_better(ov, oi, best, bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        s_v[tid >> 6] = best;
+        s_i[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kArgThreads / 64; ++w)
+            if (arg_better(s_v[w], s_i[w], best, bi)) {
+                best = s_v[w];
+                bi = s_i[w];
+            }
+        out[m] = bi;
+        if (seq_lens) seq_lens[m] += 1;
+    }
 }
 
 inline bool a16(const void* p) { return aligned(p, 16); }
@@ -380,7 +446,7 @@ extern "C" int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32
                                   uint16_t* q_out, int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool,
                                   int64_t kv_sblk, int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb,
                                   int32_t max_blocks, int32_t block_size, int32_t num_pool_blocks, int32_t* err,
-                                  void* stream) {
+                                  int32_t* lens_out, void* stream) {
     clear_error();
     if (B > 0 && !qkv) return fail(MX_ERR_NULL, "mx_qkv_rope_append: null pointer");
     if (B > 0 && (qkv_stride % 8 || !glue::a16(qkv)))
@@ -390,7 +456,7 @@ extern "C" int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32
     glue::RopeAppendParams p{qkv, qkv_stride, nullptr, 0, 0, nullptr, Hq, Hkv, D,
                              reinterpret_cast<const float2*>(rope), max_pos, positions, q_out, q_stride, k_pool,
                              v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, block_size, num_pool_blocks,
-                             err};
+                             err, lens_out};
     return rope_append_common("mx_qkv_rope_append", p, B, stream);
 }
 
@@ -399,7 +465,8 @@ extern "C" int mx_qkv_rope_append_splits(const float* partials, int32_t splits, 
                                          const int32_t* positions, uint16_t* q_out, int64_t q_stride,
                                          uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
                                          const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
-                                         int32_t block_size, int32_t num_pool_blocks, int32_t* err, void* stream) {
+                                         int32_t block_size, int32_t num_pool_blocks, int32_t* err,
+                                         int32_t* lens_out, void* stream) {
     clear_error();
     if (B > 0 && !partials) return fail(MX_ERR_NULL, "mx_qkv_rope_append_splits: null pointer");
     if (splits < 1) return fail(MX_ERR_INVALID, "mx_qkv_rope_append_splits: splits must be >= 1");
@@ -409,7 +476,7 @@ extern "C" int mx_qkv_rope_append_splits(const float* partials, int32_t splits, 
     glue::RopeAppendParams p{nullptr, width, partials, splits, (int64_t)B * width, bias, Hq, Hkv, D,
                              reinterpret_cast<const float2*>(rope), max_pos, positions, q_out, q_stride, k_pool,
                              v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, block_size, num_pool_blocks,
-                             err};
+                             err, lens_out};
     return rope_append_common("mx_qkv_rope_append_splits", p, B, stream);
 }
 
@@ -434,15 +501,17 @@ static int add_rmsnorm_common(const char* what, glue::NormParams& p, int32_t M, 
     return check_launch(what);
 }
 
-extern "C" int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride,
-                              const uint16_t* weight, int32_t M, int32_t H, float eps, uint16_t* out,
-                              int64_t out_stride, uint16_t* residual_out, int64_t ro_stride, void* stream) {
+extern "C" int mx_add_rmsnorm(const uint16_t* x, int64_t x_stride, const int64_t* x_rows, int64_t x_count,
+                              const uint16_t* residual, int64_t r_stride, const uint16_t* weight, int32_t M, int32_t H, float eps,
+                              uint16_t* out, int64_t out_stride, uint16_t* residual_out, int64_t ro_stride,
+                              void* stream) {
     clear_error();
     if (M > 0 && !x) return fail(MX_ERR_NULL, "mx_add_rmsnorm: null pointer");
     if (M > 0 && (x_stride % 8 || !glue::a16(x)))
         return fail(MX_ERR_ALIGNMENT, "mx_add_rmsnorm: rows need 16-byte alignment");
-    glue::NormParams p{x, x_stride, nullptr, 0, 0, nullptr, residual, r_stride, weight, H, eps, out, out_stride,
-                       residual_out, ro_stride};
+    if (x_rows && x_count < 1) return fail(MX_ERR_INVALID, "mx_add_rmsnorm: a gather needs x_count >= 1");
+    glue::NormParams p{x, x_stride, x_rows, x_rows ? x_count : (int64_t)M, nullptr, 0, 0, nullptr, residual,
+                       r_stride, weight, H, eps, out, out_stride, residual_out, ro_stride};
     return add_rmsnorm_common("mx_add_rmsnorm", p, M, stream);
 }
 
@@ -455,8 +524,8 @@ extern "C" int mx_add_rmsnorm_splits(const float* partials, int32_t splits, cons
     if (splits < 1) return fail(MX_ERR_INVALID, "mx_add_rmsnorm_splits: splits must be >= 1");
     if (M > 0 && (!glue::a16(partials) || (bias && !glue::a16(bias))))
         return fail(MX_ERR_ALIGNMENT, "mx_add_rmsnorm_splits: partials need 16-byte alignment");
-    glue::NormParams p{nullptr, H, partials, splits, (int64_t)M * H, bias, residual, r_stride, weight, H, eps, out,
-                       out_stride, residual_out, ro_stride};
+    glue::NormParams p{nullptr, H, nullptr, 0, partials, splits, (int64_t)M * H, bias, residual, r_stride, weight, H,
+                       eps, out, out_stride, residual_out, ro_stride};
     return add_rmsnorm_common("mx_add_rmsnorm_splits", p, M, stream);
 }
 
@@ -474,4 +543,17 @@ extern "C" int mx_silu_mul(const uint16_t* gate_up, int64_t gu_stride, int32_t M
     hipLaunchKernelGGL(glue::silu_mul_kernel, dim3((unsigned)ceil_div(total, glue::kThreads)), dim3(glue::kThreads),
                        0, as_stream(stream), gate_up, gu_stride, I, out, out_stride, total);
     return check_launch("mx_silu_mul");
+}
+
+extern "C" int mx_argmax_rows(const uint16_t* logits, int64_t stride, int32_t M, int32_t N, int64_t* out,
+                              int32_t* seq_lens, void* stream) {
+    clear_error();
+    if (M < 0 || N <= 0) return fail(MX_ERR_INVALID, "mx_argmax_rows: need M >= 0 and N > 0");
+    if (M == 0) return MX_OK;
+    if (!logits || !out) return fail(MX_ERR_NULL, "mx_argmax_rows: null pointer");
+    if (stride < N || stride % 8 || !glue::a16(logits))
+        return fail(MX_ERR_ALIGNMENT, "mx_argmax_rows: rows must be 16-byte aligned and cover N");
+    hipLaunchKernelGGL(glue::argmax_kernel, dim3(M), dim3(glue::kArgThreads), 0, as_stream(stream), logits, stride, N,
+                       out, seq_lens);
+    return check_launch("mx_argmax_rows");
 }

@@ -41,6 +41,33 @@ def _rows16(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _lens_ptr(lens_out: torch.Tensor | None, b: int):
+    if lens_out is None:
+        return None
+    if lens_out.dtype != torch.int32 or not lens_out.is_contiguous() or lens_out.numel() < b:
+        raise ValueError("lens_out must be a contiguous int32 tensor of at least B elements")
+    return lens_out.data_ptr()
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None,
+                seq_lens: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy tokens ``[M]`` (int64) of fp16 ``logits [M, N]``; ``seq_lens`` (int32) is advanced by one."""
+    _hip.require_device_tensor(logits, "logits")
+    if logits.dtype != torch.float16 or logits.dim() != 2:
+        raise ValueError("argmax_rows expects fp16 logits [M, N]")
+    lg = _rows16(logits)
+    m, n = (int(v) for v in lg.shape)
+    out = torch.empty(m, dtype=torch.int64, device=lg.device) if out is None else out
+    if out.dtype != torch.int64 or not out.is_contiguous() or out.numel() < m:
+        raise ValueError("out must be a contiguous int64 tensor of M elements")
+    if seq_lens is not None and (seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous()):
+        raise ValueError("seq_lens must be a contiguous int32 tensor")
+    _hip.check(_hip.load().mx_argmax_rows(lg.data_ptr(), lg.stride(0), m, n, out.data_ptr(),
+                                          seq_lens.data_ptr() if seq_lens is not None else None,
+                                          _hip.stream_handle(lg.device)), "mx_argmax_rows")
+    return out
+
+
 def rope_table(max_pos: int, head_dim: int, theta: float, device: torch.device | str) -> torch.Tensor:
     """``[max_pos, head_dim // 2, 2]`` fp32 ``(cos, sin)`` of ``pos * theta ** -(2i / head_dim)``."""
     half = head_dim // 2
@@ -87,8 +114,12 @@ def kv_append(k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.
 
 def qkv_rope_append(qkv: torch.Tensor, rope: torch.Tensor, positions: torch.Tensor, q_out: torch.Tensor,
                     k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int,
-                    num_kv_heads: int, err: torch.Tensor | None = None) -> torch.Tensor:
-    """Rotate q, k of ``qkv [B, (Hq + 2 Hkv) * D]`` at ``positions [B]``; q -> ``q_out``, k, v -> the pool."""
+                    num_kv_heads: int, err: torch.Tensor | None = None,
+                    lens_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Rotate q, k of ``qkv [B, (Hq + 2 Hkv) * D]`` at ``positions [B]``; q -> ``q_out``, k, v -> the pool.
+
+    ``lens_out`` (int32 ``[B]``, optional) receives ``positions + 1``.
+    """
     _hip.require_device_tensor(qkv, "qkv")
     dev = qkv.device
     nb, hkv, bs, d = k_layer.shape
@@ -112,14 +143,15 @@ def qkv_rope_append(qkv: torch.Tensor, rope: torch.Tensor, positions: torch.Tens
         qkv2.data_ptr(), qkv2.stride(0), b, num_heads, num_kv_heads, d, rope.data_ptr(), int(rope.shape[0]),
         pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0),
         k_layer.stride(1), tables.data_ptr(), tables.stride(0), int(tables.shape[1]), bs, nb,
-        err.data_ptr() if err is not None else None, _hip.stream_handle(dev)), "mx_qkv_rope_append")
+        err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b), _hip.stream_handle(dev)),
+        "mx_qkv_rope_append")
     return q_out
 
 
 def qkv_rope_append_splits(partials: torch.Tensor, splits: int, bias: torch.Tensor | None, rope: torch.Tensor,
                            positions: torch.Tensor, q_out: torch.Tensor, k_layer: torch.Tensor,
                            v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,
-                           err: torch.Tensor | None = None) -> torch.Tensor:
+                           err: torch.Tensor | None = None, lens_out: torch.Tensor | None = None) -> torch.Tensor:
     """:func:`qkv_rope_append` with the QKV projection as fp32 split partials ``[splits, B, width]``."""
     _hip.require_device_tensor(partials, "partials")
     dev = partials.device
@@ -138,8 +170,8 @@ def qkv_rope_append_splits(partials: torch.Tensor, splits: int, bias: torch.Tens
         partials.data_ptr(), splits, bias.data_ptr() if bias is not None else None, b, num_heads, num_kv_heads, d,
         rope.data_ptr(), int(rope.shape[0]), pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(),
         v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), tables.data_ptr(), tables.stride(0),
-        int(tables.shape[1]), bs, nb, err.data_ptr() if err is not None else None, _hip.stream_handle(dev)),
-        "mx_qkv_rope_append_splits")
+        int(tables.shape[1]), bs, nb, err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b),
+        _hip.stream_handle(dev)), "mx_qkv_rope_append_splits")
     return q_out
 
 
@@ -163,21 +195,31 @@ def add_rmsnorm_splits(partials: torch.Tensor, splits: int, bias: torch.Tensor |
 
 
 def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
-                out: torch.Tensor | None = None, residual_out: torch.Tensor | None = None) -> torch.Tensor:
-    """``h = x (+ residual)``; ``residual_out = h``; returns ``RMSNorm(h) * weight`` (fp16 ``[M, H]``)."""
+                out: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
+                rows: torch.Tensor | None = None) -> torch.Tensor:
+    """``h = x (+ residual)``; ``residual_out = h``; returns ``RMSNorm(h) * weight`` (fp16 ``[M, H]``).
+
+    With ``rows`` (int64 ``[M]``), row m of x is ``x[rows[m]]`` (an embedding lookup); an index
+    outside ``[0, len(x))`` reads a zero row (memory-safe; no device-side assert as in torch).
+    """
     _hip.require_device_tensor(x, "x")
     if x.dtype != torch.float16 or weight.dtype != torch.float16:
         raise ValueError("add_rmsnorm supports fp16")
     x2 = _rows16(x.reshape(-1, x.shape[-1]))
     m, h = x2.shape
+    if rows is not None:
+        if rows.dtype != torch.int64 or not rows.is_contiguous():
+            raise ValueError("rows must be a contiguous int64 tensor")
+        m = int(rows.numel())
     r2 = _rows16(residual.reshape(m, h)) if residual is not None else None
-    out = torch.empty_like(x2) if out is None else out
+    out = torch.empty((m, h), dtype=x2.dtype, device=x2.device) if out is None else out
     o2 = out.view(m, h)
     ro2 = residual_out.view(m, h) if residual_out is not None else None
     w = weight.contiguous()
     lib = _hip.load()
     _hip.check(lib.mx_add_rmsnorm(
-        x2.data_ptr(), x2.stride(0), r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0,
+        x2.data_ptr(), x2.stride(0), rows.data_ptr() if rows is not None else None, int(x2.shape[0]),
+        r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0,
         w.data_ptr(), m, h, float(eps), o2.data_ptr(), o2.stride(0),
         ro2.data_ptr() if ro2 is not None else None, ro2.stride(0) if ro2 is not None else 0,
         _hip.stream_handle(x.device)), "mx_add_rmsnorm")

@@ -18,7 +18,11 @@ current stream:
     a = silu(x Wg^T) * (x Wu^T)            mx_w8a16_gateup_swiglu (gate and up rows
                                            interleaved by 8, product in the epilogue)
     h += a Wdown^T                         mx_w8a16_linear (+ the next add_rmsnorm)
-    logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, torch argmax
+    logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, mx_argmax_rows
+
+The first norm gathers the embedding rows of the step's tokens itself, layer
+0's RoPE kernel writes the attention lengths (positions + 1) and the argmax
+kernel advances ``seq_lens``, so no torch kernel runs inside a step.
 
 A projection whose shape splits K (``mx_w8a16_splits`` > 1: qkv, o and down at
 batch 32) writes fp32 split partials instead (``mx_w8a16_linear_partials``)
@@ -44,8 +48,8 @@ from dataclasses import dataclass
 
 import torch
 
-from .decode_glue import (add_rmsnorm, add_rmsnorm_splits, qkv_rope_append, qkv_rope_append_splits, rope_table,
-                          silu_mul)
+from .decode_glue import (add_rmsnorm, add_rmsnorm_splits, argmax_rows, qkv_rope_append, qkv_rope_append_splits,
+                          rope_table, silu_mul)
 from .int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu, int8_linear,
                           int8_linear_partials, linear_splits, pack_weight, quantize_weight)
 from .paged_attention_hip import _decode as _paged_decode
@@ -104,6 +108,7 @@ class _Buffers:
     part: torch.Tensor    # fp32 split partials of the current split projection
     splits: dict          # projection name -> K splits at this batch size
     attn_lens: torch.Tensor  # int32 [B]
+    next: torch.Tensor    # int64 [B], greedy tokens
     err: torch.Tensor     # int32 [1], OR of the append kernels' error bits
 
 
@@ -232,6 +237,7 @@ class Int8DecodeModel:
                            mlp=e(batch, s.hidden), logits=e(batch, s.vocab),
                            part=torch.empty(part_elems, dtype=torch.float32, device=dev), splits=splits,
                            attn_lens=torch.zeros(batch, dtype=torch.int32, device=dev),
+                           next=torch.zeros(batch, dtype=torch.int64, device=dev),
                            err=torch.zeros(1, dtype=torch.int32, device=dev))
             self._buffers[batch] = buf
         return buf
@@ -244,34 +250,35 @@ class Int8DecodeModel:
         return flag
 
     def step(self, tokens: torch.Tensor, pool, block_tables: torch.Tensor, seq_lens: torch.Tensor,
-             timers: dict | None = None, return_logits: bool = False):
-        """Decode one token per row. ``seq_lens`` (int32) holds the KV length BEFORE this token
-        (= the token's position) and is advanced in place. Returns the greedy next tokens
-        ``[B]`` (int64, on device), and the fp16 logits ``[B, vocab]`` with ``return_logits``."""
+             timers: dict | None = None, return_logits: bool = False, out: torch.Tensor | None = None):
+        """Decode one token per row. ``tokens`` (int64) are this step's inputs; ``seq_lens``
+        (int32) holds the KV length BEFORE this token (= the token's position) and is advanced in
+        place. Returns the greedy next tokens ``[B]`` (int64, on device; written to ``out`` if
+        given, which may be ``tokens`` itself), and the fp16 logits ``[B, vocab]`` with
+        ``return_logits``."""
         s = self.shape
         bsz = int(tokens.shape[0])
         buf = self.buffers(bsz)
-        if seq_lens.dtype != torch.int32 or block_tables.dtype != torch.int32:
-            raise ValueError("seq_lens and block_tables must be int32 device tensors")
-        torch.add(seq_lens, 1, out=buf.attn_lens)
-        torch.index_select(self.embed, 0, tokens, out=buf.h)
+        if seq_lens.dtype != torch.int32 or block_tables.dtype != torch.int32 or tokens.dtype != torch.int64:
+            raise ValueError("seq_lens and block_tables must be int32 and tokens int64 device tensors")
         eps = s.rms_eps
         sp = buf.splits
         for li, layer in enumerate(self.layers):
-            if li == 0:
-                add_rmsnorm(buf.h, layer.ln_in, eps, out=buf.x)
+            if li == 0:  # h = embed[tokens]; x = RMSNorm(h)
+                add_rmsnorm(self.embed, layer.ln_in, eps, out=buf.x, residual_out=buf.h, rows=tokens)
             else:
                 self._norm_after_down(buf, layer.ln_in)
+            lens_out = buf.attn_lens if li == 0 else None
             k_layer = pool.k_layer_view(li)
             v_layer = pool.v_layer_view(li)
             if sp["qkv"] > 1:
                 self._partials(buf.x, layer.qkv, buf.part, timers, "qkv")
                 qkv_rope_append_splits(buf.part, sp["qkv"], layer.qkv[3], self.rope, seq_lens, buf.q, k_layer,
-                                       v_layer, block_tables, s.heads, s.kv_heads, err=buf.err)
+                                       v_layer, block_tables, s.heads, s.kv_heads, err=buf.err, lens_out=lens_out)
             else:
                 self._lin(buf.x, layer.qkv, buf.qkv, timers, "qkv")
                 qkv_rope_append(buf.qkv, self.rope, seq_lens, buf.q, k_layer, v_layer, block_tables, s.heads,
-                                s.kv_heads, err=buf.err)
+                                s.kv_heads, err=buf.err, lens_out=lens_out)
             ev = self._tick(timers, "attn")
             _paged_decode(buf.q.view(bsz, s.heads, 1, s.head_dim), k_layer, v_layer, block_tables, buf.attn_lens,
                           s.head_dim ** -0.5, s.group, out=buf.attn)
@@ -290,8 +297,7 @@ class Int8DecodeModel:
                 self._lin(buf.act, layer.down, buf.mlp, timers, "down")
         self._norm_after_down(buf, self.ln_final)
         self._lin(buf.x, self.lm_head, buf.logits, timers, "lm_head")
-        seq_lens.add_(1)
-        nxt = buf.logits.argmax(dim=-1)
+        nxt = argmax_rows(buf.logits, out=buf.next if out is None else out, seq_lens=seq_lens)
         return (nxt, buf.logits) if return_logits else nxt
 
     def _norm_after_down(self, buf: _Buffers, weight: torch.Tensor) -> None:

@@ -288,3 +288,78 @@ def test_split_consumers_equal_fp16_consumers():
     out_b = torch.empty_like(out_a)
     add_rmsnorm_splits(part_o, so, None, w, 1e-5, out_b, residual=rb, residual_out=rb)
     assert torch.equal(out_a, out_b) and torch.equal(ra, rb)
+
+
+def test_qkv_rope_append_writes_lengths():
+    """``lens_out`` receives ``positions + 1`` (the attention lengths after the append), also when a row's
+    slot lies outside its table."""
+    from runtime_amd.phase2.decode_glue import qkv_rope_append, rope_table
+
+    hq, hkv, d = 4, 2, 64
+    pool = _pool(8, hkv, 16, d)
+    rope = rope_table(64, d, 1e4, DEV)
+    qkv = torch.randn(3, (hq + 2 * hkv) * d, device=DEV).half()
+    q_out = torch.empty(3, hq * d, dtype=torch.float16, device=DEV)
+    positions = torch.tensor([0, 17, 40], dtype=torch.int32, device=DEV)
+    lens = torch.full((3,), -5, dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    qkv_rope_append(qkv, rope, positions, q_out, pool.k_layer_view(0), pool.v_layer_view(0),
+                    torch.tensor([[1, 2], [3, 4], [5, 6]], dtype=torch.int32, device=DEV), hq, hkv, err=err,
+                    lens_out=lens)
+    assert lens.cpu().tolist() == [1, 18, 41]
+    assert int(err.item()) == 1  # position 40 lies past row 2's two blocks (bit 1: slot outside the table)
+
+
+def test_add_rmsnorm_gathers_rows():
+    """``rows`` reads row ``rows[m]`` of x (the embedding lookup); an out-of-range index reads a zero row."""
+    from runtime_amd.phase2.decode_glue import add_rmsnorm
+
+    vocab, h = 1000, 896
+    g = torch.Generator().manual_seed(11)
+    emb = (torch.randn(vocab, h, generator=g) * 0.5).half()
+    w = (1.0 + 0.05 * torch.randn(h, generator=g)).half()
+    rows = torch.tensor([0, 999, 5, 5, 123, 998, 1000, -1], dtype=torch.int64)
+    valid = (rows >= 0) & (rows < vocab)
+    out = torch.empty(8, h, dtype=torch.float16, device=DEV)
+    h_out = torch.full((8, h), 3.0, dtype=torch.float16, device=DEV)
+    add_rmsnorm(emb.to(DEV), w.to(DEV), 1e-6, out=out, residual_out=h_out, rows=rows.to(DEV))
+    x = emb[rows.clamp(0, vocab - 1)] * valid[:, None].half()
+    ref_out, ref_h = og.add_rmsnorm(x, w, 1e-6)
+    assert torch.equal(h_out.cpu(), x)
+    _close(out[valid.to(DEV)], ref_out[valid], max_ulps=2)
+    assert float(out[~valid.to(DEV)].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("m,n", [(1, 8), (3, 128256), (32, 151936), (5, 1000)])
+def test_argmax_rows_matches_torch(m, n):
+    from runtime_amd.phase2.decode_glue import argmax_rows
+
+    g = torch.Generator().manual_seed(m * 1000 + n)
+    logits = torch.randn(m, n, generator=g).half()
+    got = argmax_rows(logits.to(DEV)).cpu()
+    assert got.dtype == torch.int64
+    assert torch.equal(got, logits.float().argmax(dim=-1))
+
+
+def test_argmax_rows_ties_nan_inf_and_lengths():
+    """First index on ties; NaN counts above every number (torch's convention, first NaN wins); -inf rows;
+    ``seq_lens`` advances by one per row; a strided logits view reads only its N columns."""
+    from runtime_amd.phase2.decode_glue import argmax_rows
+
+    n = 5001  # not a multiple of 8: the tail loop
+    base = torch.zeros(6, n + 7, dtype=torch.float16)
+    base[:, n:] = 100.0  # padding outside the view must not count
+    lg = base[:, :n]
+    lg[0, [17, 4000, 4999]] = 2.0                 # tie: first index
+    lg[1, :] = float("-inf")                      # all -inf: index 0
+    lg[2, 300] = float("nan"); lg[2, 10] = 65504  # NaN wins over the largest finite value
+    lg[3, [2500, 2501]] = float("nan")            # two NaNs: the first
+    lg[4, n - 1] = 1.0                            # last column
+    lg[5, :] = -1.0; lg[5, 1234] = float("inf")   # +inf
+    dev = base.to(DEV)[:, :n]
+    lens = torch.tensor([3, 0, 9, 1, 1, 2047], dtype=torch.int32, device=DEV)
+    out = torch.full((6,), -1, dtype=torch.int64, device=DEV)
+    argmax_rows(dev, out=out, seq_lens=lens)
+    assert out.cpu().tolist() == [17, 0, 300, 2500, n - 1, 1234]
+    assert out.cpu().tolist() == lg.float().argmax(dim=-1).tolist()
+    assert lens.cpu().tolist() == [4, 1, 10, 2, 2, 2048]
