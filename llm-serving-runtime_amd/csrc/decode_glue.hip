@@ -328,6 +328,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, 
 // Greedy token of each row: index of the largest logit, the first one on ties; NaN counts as
 // larger than any number (torch.argmax's convention). One workgroup of 1024 threads per row.
 constexpr int kArgThreads = 1024;
+constexpr int kArgU = 16;
 
 __device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
     const bool na = a != a, nb = b != b;
@@ -345,14 +346,28 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const uint16_t* __r
     float best = -__builtin_huge_valf();
     int bi = 0x7fffffff;
     const int chunks = N >> 3;
-    for (int c = tid; c < chunks; c += kArgThreads) {
-        const half8v v = as_h8(*reinterpret_cast<const uint4*>(row + c * 8));
+    // kArgU chunks per thread per memory round trip (indices clamped, compares masked):
+    // one round trip covers a 128K-entry vocabulary. arg_better is a total order, so
+    // the visiting order does not change the result.
+    for (int c0 = tid; c0 < chunks; c0 += kArgU * kArgThreads) {
+        half8v v[kArgU];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            if (arg_better((float)v[e], c * 8 + e, best, bi)) {
-                best = (float)v[e];
-                bi = c * 8 + e;
+        for (int u = 0; u < kArgU; ++u) {
+            const int c = c0 + u * kArgThreads;
+            v[u] = as_h8(*reinterpret_cast<const uint4*>(row + (c < chunks ? c : chunks - 1) * 8));
+        }
+#pragma unroll
+        for (int u = 0; u < kArgU; ++u) {
+            const int c = c0 + u * kArgThreads;
+            if (c < chunks) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (arg_better((float)v[u][e], c * 8 + e, best, bi)) {
+                        best = (float)v[u][e];
+                        bi = c * 8 + e;
+                    }
             }
+        }
     }
     for (int n = chunks * 8 + tid; n < N; n += kArgThreads)
         if (arg_better((float)row[n], n, best, bi)) {

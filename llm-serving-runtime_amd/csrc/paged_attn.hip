@@ -21,12 +21,18 @@
 // Kernel 1 (split): a wave walks its range; for each segment piece it
 //   * loads K rows as the A operand of v_mfma_f32_16x16x32_f16 (16 tokens x
 //     32 dims per instruction, one 128-bit load per lane), with the G query
-//     heads (zero padded to 16) as the B operand -> scores S[token][head];
+//     heads (zero padded to 16) as the B operand -> scores S[token][head]:
+//     lane l holds the scores of tokens 4*(l/16) + i, i < 4, for head l%16;
 //   * runs the online softmax in fp32 on the exp2 scale (scores are
 //     pre-multiplied by scale*log2(e); exp2(x*log2 e) == exp(x));
-//   * shares p[token][head] and the rescale factor through a per-wave LDS
-//     slot and accumulates P.V on the VALU from V rows loaded as contiguous
-//     1 KiB runs, fp32 accumulation;
+//   * accumulates P.V with v_mfma_f32_16x16x16_f16, contracting over the
+//     tile's 16 tokens. Each lane loads V for exactly the four tokens whose
+//     probabilities it already holds, at D/16 consecutive dims, so both
+//     operands are lane-local: MFMA e takes A[m][k] = V[token k][m*D/16 + e]
+//     and B[k][n] = p[token k][head n], and lane l accumulates output dims
+//     (4*(l/16) + i)*D/16 + e of head l%16. p enters the product rounded to
+//     fp16 (the reference's SDPA fallback also multiplies fp16
+//     probabilities into V); the denominator sums the same rounded values;
 //   * keeps P tiles of K/V loads in flight and reads the piece's block ids
 //     with one vector load (a range never exceeds 64 tiles).
 // A piece that is a whole segment is written as fp16 output; otherwise its
@@ -38,9 +44,12 @@
 // Kernel 2 (merge): one workgroup per segment reads its worker span, applies
 // the log-sum-exp merge of the partials and writes fp16 output (zeros for an
 // empty row). Each thread owns output elements and issues all of its loads
-// at once, so a merge costs two dependent memory round trips. Keeping the merge in its own launch keeps kernel
-// 1 free of device-scope fences: on gfx950 a release/acquire at agent scope
-// writes back and invalidates the XCD's L2.
+// at once, so a merge costs two dependent memory round trips. The merge has a
+// launch of its own because handing partials between workgroups inside one
+// launch costs more on gfx950 than the launch: an agent-scope release/acquire
+// writes back and invalidates the XCD's L2 (measured 2.6x slower at the bench
+// shape), and write-through atomic partials with a ticket counter still lost
+// (1.3x).
 #include "common.h"
 
 namespace mx {
@@ -145,36 +154,51 @@ __device__ __forceinline__ Seg locate(const Params& p, int64_t x, int lane) {
 
 __device__ __forceinline__ int64_t range_lo(int64_t w, int64_t T, int W) { return w * T / W; }
 
-template <int KK, int NL>
-struct TileRegs {
-    half8v k[KK];
-    half8v v[NL];
+// V fragment of one token held by a lane: D/16 consecutive dims.
+template <int D>
+struct VFragT;
+template <>
+struct VFragT<128> {
+    using type = half8v;
+    static __device__ __forceinline__ type load(const _Float16* p) { return load_half8(p); }
+};
+template <>
+struct VFragT<64> {
+    using type = half4v;
+    static __device__ __forceinline__ type load(const _Float16* p) {
+        return __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(p));
+    }
 };
 
-// Pipeline depth from the VGPRs of one tile stage (K and V, 4 per fragment)
-// after the G*8 accumulators.
-constexpr int pa_depth(int D, int G) {
-    const int d = (160 - 8 * G) / (4 * (D / 32 + D / 32));
-    return d < 2 ? 2 : (d > 4 ? 4 : d);
-}
+template <int KK, typename VF>
+struct TileRegs {
+    half8v k[KK];
+    VF v[4];  // tokens 4*(lane/16) + j
+};
+
+// Tiles of K/V loads in flight per wave. Two keep the HBM queues full at the
+// default worker count (a deeper pipeline measured slower on MI355X: more
+// outstanding random 4 KiB runs per channel) and leave room for four waves
+// per SIMD.
+#ifndef MX_PA_DEPTH
+#define MX_PA_DEPTH 2
+#endif
+constexpr int kDepth = MX_PA_DEPTH;
 
 template <int D, int BS, int G>
 __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
-    constexpr int KK = D / 32;       // MFMA k-steps over the head dim
-    constexpr int LPR = D / 8;       // lanes per token row when loading V
-    constexpr int RPL = 64 / LPR;    // token rows per V load instruction
-    constexpr int NL = kTile / RPL;  // V load instructions per tile
+    constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
+    constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
     constexpr int TPB = BS / kTile;  // tiles per KV block
-    constexpr int P = pa_depth(D, G);
+    constexpr int P = kDepth;
+    using VF = typename VFragT<D>::type;
+    using Regs = TileRegs<KK, VF>;
     const float kNegInf = -__builtin_huge_valf();
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int worker = blockIdx.x * kWaves + wave;
     const int g = lane >> 4, r = lane & 15;
-
-    __shared__ float s_p[kWaves][kTile][17];
-    __shared__ float s_alpha[kWaves][16];
 
     // Up to 64 rows: one read of seq_lens per wave, reused to locate every piece.
     const bool one_pass = p.B <= 64;
@@ -192,9 +216,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
     const int64_t hi = range_lo(worker + 1, T, W);
     int64_t x = range_lo(worker, T, W);
 
-    const int vrow = lane / LPR, vcol = (lane % LPR) * 8;
-    const int koff = r * D + 8 * g;
-    const int voff = vrow * D + vcol;
+    const int koff = r * D + 8 * g;         // K: token r, dims 8g + 32kk
+    const int voff = 4 * g * D + DPL * r;   // V: token 4g + j, dims DPL*r + e
 
     while (x < hi) {
         Seg sg;
@@ -250,11 +273,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
 
         float m_run = kNegInf;  // running max of head r (same in all 4 lane groups)
         float l_run = 0.0f;     // partial denominator over this lane's tokens
-        float acc[G][8];
+        float4v acc[DPL];       // acc[e][i]: head r, dim (4g + i) * DPL + e
 #pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+        for (int e = 0; e < DPL; ++e) acc[e] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
         const _Float16* kbase = p.k + (int64_t)kvh * p.kv_shead;
         const _Float16* vbase = p.v + (int64_t)kvh * p.kv_shead;
@@ -262,7 +283,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
         // Loads are unconditional: past the piece's last tile the index is clamped
         // (an L2 hit) and a skipped block reads block 0; only the compute below is
         // predicated, by wave-uniform flags, so waits count exact stages.
-        auto load_tile = [&](int j, TileRegs<KK, NL>& tr) {
+        auto load_tile = [&](int j, Regs& tr) {
             const int jc = j < nj ? j : nj - 1;
             const int pb = __builtin_amdgcn_readlane(my_pb, jc);
             const int t = t0 + jc;
@@ -272,10 +293,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_half8(kt + koff + 32 * kk);
 #pragma unroll
-            for (int jj = 0; jj < NL; ++jj) tr.v[jj] = load_half8(vt + voff + jj * RPL * D);
+            for (int jj = 0; jj < 4; ++jj) tr.v[jj] = VFragT<D>::load(vt + voff + jj * D);
         };
 
-        auto compute_tile = [&](int j, const TileRegs<KK, NL>& tr) {
+        auto compute_tile = [&](int j, const Regs& tr) {
             const int t = t0 + j;
             float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -288,43 +309,38 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
             const float mx = xor_max_16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            half4v pv;
             float psum = 0.0f;
-            __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pi = __builtin_amdgcn_exp2f(sc[i] - m_new);
-                s_p[wave][4 * g + i][r] = pi;
-                psum += pi;
+                pv[i] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - m_new);
+                psum += (float)pv[i];
             }
             l_run = l_run * alpha + psum;
-            const bool rescale = __builtin_amdgcn_ballot_w64(m_new != m_run) != 0;
+            if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
+            }
             m_run = m_new;
-            if (g == 0) s_alpha[wave][r] = alpha;
-            __builtin_amdgcn_wave_barrier();
-            // P.V on the VALU: this lane owns dims vcol..vcol+7 of tokens jj*RPL + vrow.
-            if (rescale) {
+            // V rows past the sequence end are zeroed: p is 0 there, but stale pool
+            // memory may hold Inf/NaN, and 0 * NaN would poison the sum.
+            VF v[4];
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const float a = s_alpha[wave][h];
+            for (int jj = 0; jj < 4; ++jj) v[jj] = tr.v[jj];
+            if (t * kTile + kTile > s_eff) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[h][e] *= a;
-                }
+                for (int jj = 0; jj < 4; ++jj)
+                    if (tok0 + jj >= s_eff) v[jj] = VF{};
             }
 #pragma unroll
-            for (int jj = 0; jj < NL; ++jj) {
-                const int tok = jj * RPL + vrow;
-#pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const float pj = s_p[wave][tok][h];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pj, (float)tr.v[jj][e], acc[h][e]);
-                }
+            for (int e = 0; e < DPL; ++e) {
+                const half4v a = {v[0][e], v[1][e], v[2][e], v[3][e]};
+                acc[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pv, acc[e], 0, 0, 0);
             }
-            __builtin_amdgcn_wave_barrier();
         };
 
         {
-            TileRegs<KK, NL> st[P];
+            Regs st[P];
 #pragma unroll
             for (int s = 0; s < P; ++s) load_tile(s, st[s]);
             for (int j0 = 0; j0 < nj; j0 += P) {
@@ -337,16 +353,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
             }
         }
 
-        // Wave totals: l over the 4 lane groups, acc over the token-row groups.
+        // Denominator of head r over the 4 lane groups; acc already sums all 16 tokens of a tile.
         l_run = xor_sum_16_32(l_run);
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float v = acc[h][e];
-                if (LPR == 8) v = xor8_sum(v);
-                acc[h][e] = xor_sum_16_32(v);
-            }
         const bool whole = t0 == 0 && t1 == nt;
         const int64_t seg = (int64_t)b * p.Hkv + kvh;
         const int64_t slot = worker + seg;
@@ -354,26 +362,31 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
             if (t0 == 0) p.seg_w[2 * seg] = worker;
             if (t1 == nt) p.seg_w[2 * seg + 1] = worker;
         }
-        if (lane < LPR) {
+        if (r < G) {
+            if (whole) {
+                _Float16* orow = p.out + (int64_t)b * p.o_sb + (int64_t)(h0 + r) * p.o_sh;
+                const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;  // 0: every block of the row was skipped
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float lh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_run), h));
-                if (whole) {
-                    half8v o;
+                for (int i = 0; i < 4; ++i) {
+                    VF o;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] = (_Float16)(acc[h][e] / lh);
-                    *reinterpret_cast<uint4*>(p.out + (int64_t)b * p.o_sb + (int64_t)(h0 + h) * p.o_sh + vcol) =
-                        __builtin_bit_cast(uint4, o);
-                } else {
-                    float4v* dst = reinterpret_cast<float4v*>(p.part_acc + (slot * G + h) * D + vcol);
-                    dst[0] = float4v{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-                    dst[1] = float4v{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+                    for (int e = 0; e < DPL; ++e) o[e] = (_Float16)(acc[e][i] * inv);
+                    *reinterpret_cast<VF*>(orow + (4 * g + i) * DPL) = o;
+                }
+            } else {
+                float* arow = p.part_acc + (slot * G + r) * D;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float4v* dst = reinterpret_cast<float4v*>(arow + (4 * g + i) * DPL);
+#pragma unroll
+                    for (int c = 0; c < DPL / 4; ++c)
+                        dst[c] = float4v{acc[4 * c][i], acc[4 * c + 1][i], acc[4 * c + 2][i], acc[4 * c + 3][i]};
+                }
+                if (g == 0) {
+                    p.part_ml[(slot * G + r) * 2 + 0] = m_run;
+                    p.part_ml[(slot * G + r) * 2 + 1] = l_run;
                 }
             }
-        }
-        if (!whole && g == 0 && r < G) {
-            p.part_ml[(slot * G + r) * 2 + 0] = m_run;
-            p.part_ml[(slot * G + r) * 2 + 1] = l_run;
         }
     }
 }

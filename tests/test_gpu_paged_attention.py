@@ -260,3 +260,24 @@ def test_hook_contract():
         reset_paged_decode_batch_metadata(tok)
     assert weights is None and out.shape == (2, 1, 8, 64)
     _check(out.transpose(1, 2), oracle_out(q, k, v, tables, sl, 0.125, 4))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_stale_nan_past_sequence_end(d):
+    """Slots past seq_len in a row's last block may hold anything a freed sequence (or an uninitialised pool)
+    left there, NaN and Inf included: they never reach the output (the reference loads them masked to 0,
+    paged_attention_triton.py:225-226)."""
+    lens = [5, 33, 130, 16, 1]
+    q, k, v, tables, sl = _random_case(51 + d, len(lens), 2, 4, d, 16, lens)
+    base = oracle_out(q, k, v, tables, sl, d**-0.5, 4)
+    k2, v2 = k.clone(), v.clone()
+    for b, s in enumerate(lens):
+        last = int(tables[b, (s - 1) // 16])
+        if s % 16:
+            k2[last, :, s % 16:] = float("nan")
+            v2[last, :, s % 16:] = float("inf") if b % 2 else float("nan")
+    for ct in (0, 16):
+        out, err = _abi_decode(q, k2, v2, tables, sl, d**-0.5, 4, ct)
+        assert err == 0
+        assert torch.isfinite(out.float()).all(), f"chunk_tokens={ct}"
+        _check(out, base, f"chunk_tokens={ct}")
