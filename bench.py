@@ -50,6 +50,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=1)
+    ap.add_argument("--traffic-probe", type=int, default=0, metavar="REPS",
+                    help="instead of the bench: REPS rounds of the step's paged-attention calls (one per layer, "
+                         "bench workload) and a 1 GiB copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     return ap.parse_args()
 
 
@@ -220,12 +223,79 @@ def time_family(run, launches: int, reps: int) -> float:
     return a.elapsed_time(b) * 1e-3 / (reps * launches)
 
 
+COPY_PROBE_BYTES = 1 << 30
+TRAFFIC_PROFILE = os.path.join(HERE, "profiles", "paged_attn_traffic_llama3_8b_b32.md")
+
+
+def measured_traffic(kernel: str, model: str, batch: int):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary (two rocprofv3 --pmc
+    passes, FETCH_SIZE and WRITE_SIZE, scaled by a 1 GiB copy), for the default workload only."""
+    import re
+
+    if model != "llama3-8b" or batch != 32 or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    with open(TRAFFIC_PROFILE) as f:
+        m = re.search(r"^bench-traffic: kernel=(\w+) bytes_per_launch=(\d+) algorithmic_bytes=(\d+)$", f.read(), re.M)
+    if not m or m.group(1) != kernel:
+        return None
+    return int(m.group(2)), int(m.group(3))
+
+
+def traffic_probe(args) -> int:
+    """Kernels for the HBM-traffic counter passes, nothing else: the bench's attention calls
+    (same contexts, pool, seed; one launch per layer so no launch re-reads the previous
+    one's K/V from the 256 MB MALL) and one copy of COPY_PROBE_BYTES, whose counter reading
+    calibrates FETCH_SIZE / WRITE_SIZE (it reads and writes exactly that many bytes)."""
+    import torch
+
+    from runtime_amd.phase2 import _hip
+    from runtime_amd.phase2.decode_step import LLAMA3_8B, QWEN2_05B, make_contexts
+    from runtime_amd.phase2.paged_attention_hip import _decode
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+    from oracle.paged_attention import attention_bytes
+
+    _hip.load()
+    dev = torch.device("cuda:0")
+    shape = LLAMA3_8B if args.model == "llama3-8b" else QWEN2_05B
+    n_layers = args.layers or shape.layers
+    bs = 16
+    headroom = args.warmup + args.steps + args.kernel_steps + 2  # the bench's table width
+    lens, tables = make_contexts(args.batch, args.ctx_lo, args.ctx_hi, bs, args.pool_blocks, headroom=headroom, seed=0)
+    pool = GpuKVBlockPool(num_blocks=args.pool_blocks, block_size_tokens=bs, num_layers=n_layers,
+                          num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16, device=dev)
+    pool._ensure_pools()
+    gk = torch.Generator(device=dev).manual_seed(1)
+    for t in (pool._k_pool, pool._v_pool):
+        flat = t.view(-1)
+        for i in range(0, flat.numel(), 1 << 28):
+            flat[i:i + (1 << 28)].normal_(generator=gk)
+    q = torch.randn(args.batch, shape.heads, 1, shape.head_dim, generator=gk, device=dev).half()
+    tables_d = tables.to(dev)
+    lens_d = (lens + 1).to(device=dev, dtype=torch.int32)
+    for _ in range(args.traffic_probe):
+        for li in range(n_layers):
+            _decode(q, pool.k_layer_view(li), pool.v_layer_view(li), tables_d, lens_d, shape.head_dim**-0.5,
+                    shape.group)
+    src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.float16, device=dev).normal_(generator=gk)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    attn_b = attention_bytes([x + 1 for x in lens.tolist()], shape.kv_heads, shape.head_dim, shape.heads, bs)
+    print(json.dumps({"probe": "paged_attn", "launches": args.traffic_probe * n_layers,
+                      "attn_bytes_per_launch": attn_b, "copy_bytes": COPY_PROBE_BYTES}), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               "(the path shards without exchange; see the design notes). Run with --gpus 1.", file=sys.stderr)
         return 2
+
+    if args.traffic_probe:
+        return traffic_probe(args)
 
     import torch
 
@@ -323,6 +393,7 @@ def main() -> int:
                    "frac": round(per_launch[k] / kdur[k] / 1e9 / HBM_PEAK_GBPS, 4)} for k in kdur}
 
     value = bsz / (ms * 1e-3)
+    traffic = measured_traffic(dominant, args.model, bsz) if n_layers == shape.layers else None
     out = {
         "metric": "decode tokens/sec + achieved HBM GB/s (% peak), int8-W linear + paged-attn",
         "value": round(value, 2),
@@ -347,7 +418,11 @@ def main() -> int:
         "step_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
         "step_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic[0] if traffic else None,
+                     "traffic_note": (f"HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE "
+                                      f"(copy-calibrated), profiles/{os.path.basename(TRAFFIC_PROFILE)}; "
+                                      f"{traffic[1]} algorithmic bytes at that run's contexts") if traffic else None},
         "kernels": kernels,
         "setup_s": round(setup_s, 1),
     }

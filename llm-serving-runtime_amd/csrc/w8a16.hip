@@ -13,10 +13,11 @@
 // fp16(0x6400 | byte) = 1024 + q + 128 and one packed fp16 add of -1152
 // recovers q exactly: the dequant is 2 v_perm_b32 + 2 v_pk_add_f16 per 4 weights.
 //
-// Work split: a workgroup owns NPW n-tiles (16*NPW output channels) for the
-// whole K; its waves take interleaved k-tiles (wave w: w, w+WAVES, ...) so
-// concurrent waves read adjacent kilobytes; partial sums meet in LDS. The
-// per-channel scale and the bias are applied once, in the epilogue.
+// Work split of the VALU GEMV (M <= 4): a workgroup owns NPW n-tiles (16*NPW
+// output channels) for the whole K; its waves take interleaved k-tiles (wave w:
+// w, w+WAVES, ...) so concurrent waves read adjacent kilobytes; partial sums
+// meet in LDS. The MFMA GEMM (M > 4) splits the other way, see gemm_mfma_kernel.
+// Both apply the per-channel scale and the bias once, in the epilogue.
 #include "common.h"
 
 namespace mx {
