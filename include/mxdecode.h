@@ -59,7 +59,8 @@ const char* mx_last_error(void);
 int mx_w8a16_quantize(const float* w, int64_t N, int64_t K, int8_t* q, uint16_t* scale, void* stream);
 
 /* Pack q[N, K] (int8, row stride K) into the 1 KiB tile layout read by
- * mx_w8a16_linear (N % 16 == 0, K % 64 == 0; N*K bytes). Bit-exact.
+ * mx_w8a16_linear (N % 16 == 0, K % 64 == 0; N*K bytes): 16 x 64 tiles,
+ * k-major (tile (nt, kt) at byte (kt*N/16 + nt)*1024). Bit-exact.
  * Reference: same load step, worker_server.py:194-205. */
 int mx_w8a16_pack(const int8_t* q, int64_t N, int64_t K, uint8_t* packed, void* stream);
 

@@ -109,13 +109,13 @@ int oracle_quantize_int8(const float* w, int64_t n, int64_t k, int8_t* q, uint16
 /* Tile pack: see oracle/int8_quant.py. Returns -1 on a bad shape. */
 int oracle_pack_tiles(const int8_t* q, int64_t n, int64_t k, uint8_t* packed) {
     if (n % 16 != 0 || k % 64 != 0) return -1;
-    int64_t kt_count = k / 64;
+    int64_t nt_count = n / 16;
     for (int64_t row = 0; row < n; ++row) {
         int64_t nt = row / 16, r = row % 16;
         for (int64_t col = 0; col < k; ++col) {
             int64_t kt = col / 64, g = (col % 64) / 16, j = col % 16;
             int64_t lane = g * 16 + r;
-            int64_t off = (nt * kt_count + kt) * 1024 + lane * 16 + j;
+            int64_t off = (kt * nt_count + nt) * 1024 + lane * 16 + j;
             packed[off] = (uint8_t)((uint8_t)q[row * k + col] ^ 0x80u);
         }
     }

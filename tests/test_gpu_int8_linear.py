@@ -258,3 +258,44 @@ def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
         pytest.skip("gate||up splits K at this shape; the epilogue fusion does not apply")
     got = int8_gateup_swiglu(x, pack_weight(iq), iscale, None, inter)
     assert torch.equal(got, want)
+
+
+# N chosen so that the unsplit launch takes each wide workgroup shape: about one
+# workgroup per CU with (waves, n-tiles per wave) = (5,1), (6,1), (7,1), (8,1), (8,2),
+# (8,4); 128032 (NT % 4 == 2) falls back to 4 waves of one n-tile.
+WIDE_N = [20000, 24000, 28672, 32000, 64000, 128000, 128032]
+
+
+@pytest.mark.parametrize("m", [16, 32])
+@pytest.mark.parametrize("n", WIDE_N)
+def test_linear_wide_workgroup_shapes(m, n):
+    from runtime_amd.phase2.int8_linear import linear_splits
+
+    k = 128
+    assert linear_splits(m, n, k) == 1
+    q, s = _quantized(7 + n + m, n, k)
+    rng = np.random.default_rng(n + m)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float16)
+    want = int8_quant.linear_ref_fp32(x, q, s, bias)
+    got = int8_linear(_cuda(x), pack_weight(_cuda(q)), _cuda(s), _cuda(bias), n).float().cpu().numpy()
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("m,inter", [(32, 10000), (16, 12000), (32, 16000)])
+def test_gateup_swiglu_epilogue_wide_shapes(m, inter):
+    """The SwiGLU epilogue at the 5-, 6- and 8-wave unsplit shapes equals the separate ops bit for bit."""
+    from runtime_amd.phase2.decode_glue import silu_mul
+    from runtime_amd.phase2.int8_linear import gateup_interleave, int8_gateup_swiglu, linear_splits
+
+    k = 128
+    g = torch.Generator(device="cuda").manual_seed(m + inter)
+    wg = torch.randn(inter, k, generator=g, device="cuda") * 0.02
+    wu = torch.randn(inter, k, generator=g, device="cuda") * 0.02
+    x = torch.randn(m, k, generator=g, device="cuda").half()
+    assert linear_splits(m, 2 * inter, k) == 1
+    plain_q, plain_s = quantize_weight(torch.cat([wg, wu]))
+    iq, iscale = quantize_weight(gateup_interleave(wg, wu))
+    want = silu_mul(int8_linear(x, pack_weight(plain_q), plain_s, None, 2 * inter))
+    got = int8_gateup_swiglu(x, pack_weight(iq), iscale, None, inter)
+    assert torch.equal(got, want)

@@ -120,13 +120,13 @@ def test_pack_layout_definition():
     n, k = 32, 192
     q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
     packed = int8_quant.pack_tiles(q)
-    kt_count = k // 64
+    nt_count = n // 16
     for row in range(n):
         for col in range(0, k, 7):
             nt, r = divmod(row, 16)
             kt, rem = divmod(col, 64)
             g, j = divmod(rem, 16)
-            off = (nt * kt_count + kt) * 1024 + (16 * g + r) * 16 + j
+            off = (kt * nt_count + nt) * 1024 + (16 * g + r) * 16 + j
             assert packed[off] == (int(q[row, col]) & 0xFF) ^ 0x80
     assert np.array_equal(packed, int8_quant_c.pack_tiles(q))
     assert np.array_equal(int8_quant.unpack_tiles(packed, n, k), q)
