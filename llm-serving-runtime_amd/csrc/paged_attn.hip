@@ -24,7 +24,8 @@
 //     heads (zero padded to 16) as the B operand -> scores S[token][head]:
 //     lane l holds the scores of tokens 4*(l/16) + i, i < 4, for head l%16;
 //   * runs the online softmax in fp32 on the exp2 scale (scores are
-//     pre-multiplied by scale*log2(e); exp2(x*log2 e) == exp(x));
+//     pre-multiplied by scale*log2(e); exp2(x*log2 e) == exp(x)), moving the
+//     reference maximum only when it rises by more than 2^8;
 //   * accumulates P.V with v_mfma_f32_16x16x16_f16, contracting over the
 //     tile's 16 tokens. Each lane loads V for exactly the four tokens whose
 //     probabilities it already holds, at D/16 consecutive dims, so both
@@ -83,6 +84,7 @@ constexpr int kMaxRangeTiles = 64;      // a worker's range fits one vector of b
 constexpr int kDefaultWorkers = 2048;   // 256 CUs x 8 resident waves on MI355X
 constexpr int kMinDefaultTiles = 4;     // default ranges are at least this long when T allows
 constexpr int kMaxChunkTokens = kMaxRangeTiles * kTile;
+constexpr float kLazyLog2 = 8.0f;       // rescale only when the running max rises by more than 2^8
 
 __device__ __forceinline__ half8v load_half8(const _Float16* p) {
     return __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(p));
@@ -307,21 +309,27 @@ __global__ __launch_bounds__(kWaves * 64) void decode_split_kernel(Params p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < s_eff) ? s[i] * p.scale_log2e : kNegInf;
             const float mx = xor_max_16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            // Lazy rescale: the reference point m_run moves only when a score exceeds it
+            // by more than kLazyLog2, so p = exp2(s - m_run) <= 2^kLazyLog2 (exact range
+            // for fp16, same relative rounding) and acc / l is unchanged. Rescaling all
+            // accumulators at every new maximum cost ~100 instructions on most early tiles.
+            const bool grow = mx > m_run + kLazyLog2;  // always true on the first tile
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+                const float m_new = grow ? mx : m_run;
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+                l_run *= alpha;
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
+                m_run = m_new;
+            }
             half4v pv;
             float psum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                pv[i] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - m_new);
+                pv[i] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - m_run);
                 psum += (float)pv[i];
             }
-            l_run = l_run * alpha + psum;
-            if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
-#pragma unroll
-                for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
-            }
-            m_run = m_new;
+            l_run += psum;
             // V rows past the sequence end are zeroed: p is 0 there, but stale pool
             // memory may hold Inf/NaN, and 0 * NaN would poison the sum.
             VF v[4];
