@@ -40,7 +40,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--batch", type=int, default=None, help="rows (default 32; 128 for --workload prefix-batch)")
+    ap.add_argument("--workload", choices=["decode", "prefix-batch"], default="decode",
+                    help="decode: the headline step (default). prefix-batch: 128 rows in 16 groups of 8 sharing "
+                         "a 1024-token prefix (aliased blocks), contexts U[1, 8192], 16 rows finish and 16 join "
+                         "every 16 steps")
     ap.add_argument("--model", choices=["llama3-8b", "qwen2-0.5b"], default="llama3-8b")
     ap.add_argument("--layers", type=int, default=None, help="override layer count (diagnostics only)")
     ap.add_argument("--ctx-lo", type=int, default=128)
@@ -53,7 +57,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="REPS",
                     help="instead of the bench: REPS rounds of the step's paged-attention calls (one per layer, "
                          "bench workload) and a 1 GiB copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
-    return ap.parse_args()
+    args = ap.parse_args()
+    if args.batch is None:
+        args.batch = 128 if args.workload == "prefix-batch" else 32
+    return args
 
 
 def cpu_info() -> dict:
@@ -287,6 +294,137 @@ def traffic_probe(args) -> int:
     return 0
 
 
+PREFIX_GROUPS, PREFIX_TOKENS, ROTATE_EVERY = 16, 1024, 16
+
+
+def prefix_batch_bench(args) -> int:
+    """Shared-prefix continuous batch on the native step: ``args.batch`` rows in 16 groups
+    whose rows alias one 1024-token prefix (block ids shared, stored once), contexts
+    U[1, 8192]. Every 16 steps the rows b with b % 8 == epoch % 8 finish and new requests
+    of the same group join their slots (freed blocks reused; tables, lengths and tokens
+    rewritten in place between replays of one captured step graph, all inside the timed
+    region). ``value`` is tokens/s; the HBM figure counts weights + unique K/V bytes."""
+    import torch
+
+    from runtime_amd.phase2 import _hip
+    from runtime_amd.phase2.decode_step import LLAMA3_8B, QWEN2_05B, Int8DecodeModel
+    from runtime_amd.phase2.paged_attention_hip import _decode
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+    from runtime_amd.phase2.prefix_batch import PrefixBatch
+
+    _hip.load()
+    dev = torch.device("cuda:0")
+    shape = LLAMA3_8B if args.model == "llama3-8b" else QWEN2_05B
+    n_layers = args.layers or shape.layers
+    bsz, bs = args.batch, 16
+    lo, hi = 1, 8192
+    total_steps = args.warmup + args.steps + 2
+    num_blocks = 40960
+    t_setup = time.perf_counter()
+    pb = PrefixBatch(batch=bsz, groups=PREFIX_GROUPS, prefix_tokens=PREFIX_TOKENS, lo=lo, hi=hi, block_size=bs,
+                     num_blocks=num_blocks, headroom=total_steps + ROTATE_EVERY, seed=0)
+    model = Int8DecodeModel(shape, device=dev, seed=0, layers=n_layers)
+    pool = GpuKVBlockPool(num_blocks=num_blocks, block_size_tokens=bs, num_layers=n_layers,
+                          num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16, device=dev)
+    pool._ensure_pools()
+    gk = torch.Generator(device=dev).manual_seed(1)
+    for t in (pool._k_pool, pool._v_pool):
+        flat = t.view(-1)
+        for i in range(0, flat.numel(), 1 << 28):
+            flat[i:i + (1 << 28)].normal_(generator=gk)
+    tables_d = torch.zeros(bsz, pb.max_blocks, dtype=torch.int32, device=dev)
+    seq_lens = torch.zeros(bsz, dtype=torch.int32, device=dev)
+    pb.upload(tables_d, seq_lens)
+    gt = torch.Generator().manual_seed(2)
+    tokens = torch.randint(0, shape.vocab, (bsz,), generator=gt).to(dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    def step():
+        model.step(tokens, pool, tables_d, seq_lens, out=tokens)
+
+    for _ in range(args.warmup):
+        step()
+        pb.advance(1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    pb.advance(1)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    pb.advance(1)  # the capture ran the step once
+    torch.cuda.synchronize()
+
+    kv_token_bytes = n_layers * shape.kv_heads * shape.head_dim * 2 * 2  # K and V, every layer
+    uniq, logical, rotated = [], [], 0
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for k in range(args.steps):
+        if k and k % ROTATE_EVERY == 0:
+            epoch = k // ROTATE_EVERY
+            rows = [b for b in range(bsz) if b % 8 == epoch % 8]
+            pb.rotate(rows)
+            pb.upload(tables_d, seq_lens)
+            tokens[rows] = torch.randint(0, shape.vocab, (len(rows),), generator=gt).to(dev)
+            rotated += len(rows)
+        uniq.append(pb.unique_tokens(1))
+        logical.append(pb.logical_tokens(1))
+        graph.replay()
+        pb.advance(1)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    assert seq_lens.cpu().tolist() == pb.lens.tolist(), "device lengths diverged from the schedule"
+
+    # Attention family at the final state (32 launches per step, one graph), as in the headline bench.
+    s_ = model.shape
+    q = torch.randn(bsz, s_.heads, 1, s_.head_dim, generator=gk, device=dev).half()
+    lens_attn = (seq_lens + 1).to(torch.int32)
+
+    def attn():
+        for li in range(n_layers):
+            _decode(q, pool.k_layer_view(li), pool.v_layer_view(li), tables_d, lens_attn, s_.head_dim**-0.5, s_.group)
+    attn_s = time_family(attn, n_layers, args.kernel_steps)
+    # One attention launch (one layer) reads these K/V bytes at the final state.
+    final_uniq = pb.unique_tokens(1) * shape.kv_heads * shape.head_dim * 2 * 2
+    final_logical = pb.logical_tokens(1) * shape.kv_heads * shape.head_dim * 2 * 2
+
+    lin = model.linear_bytes(bsz)
+    weight_bytes = n_layers * (lin["qkv"] + lin["o"] + lin["gate_up"] + lin["down"]) + lin["lm_head"]
+    uniq_b = sum(uniq) / len(uniq) * kv_token_bytes
+    logical_b = sum(logical) / len(logical) * kv_token_bytes
+    value = bsz / (ms * 1e-3)
+    out = {
+        "metric": "decode tokens/sec + achieved HBM GB/s (% peak), int8-W linear + paged-attn",
+        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "w8a16 (int8 weights, fp16 activations/KV, fp32 accumulate)",
+        "data": "synthetic (random-init weights quantized on device, random K/V)",
+        "config": {
+            "workload": f"{args.model}-shaped int8 decode step, {bsz} rows in {PREFIX_GROUPS} groups sharing a "
+                        f"{PREFIX_TOKENS}-token prefix (aliased blocks), contexts U[{lo},{hi}], {bsz // 8} rows "
+                        f"finish and join every {ROTATE_EVERY} steps",
+            "batch": bsz, "layers": n_layers, "block_size": bs, "pool_blocks": num_blocks, "hip_graph": True,
+            "parallelism": "none (1 GPU)", "rows_rotated": rotated,
+        },
+        "kv_logical_bytes_per_step": int(logical_b), "kv_unique_bytes_per_step": int(uniq_b),
+        "weight_bytes_per_step": weight_bytes,
+        "step_gbps_unique": round((weight_bytes + uniq_b) / (ms * 1e-3) / 1e9, 1),
+        "step_hbm_frac_unique": round((weight_bytes + uniq_b) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "attn": {"avg_us": round(attn_s * 1e6, 2), "unique_bytes": final_uniq, "logical_bytes": final_logical,
+                 "gbps_unique": round(final_uniq / attn_s / 1e9, 1),
+                 "gbps_logical": round(final_logical / attn_s / 1e9, 1)},
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -296,6 +434,8 @@ def main() -> int:
 
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.workload == "prefix-batch":
+        return prefix_batch_bench(args)
 
     import torch
 

@@ -78,10 +78,12 @@ int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, c
                     const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t N, int64_t y_stride,
                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* Number of K splits the MFMA path uses for this shape (1 <= M <= 64): 1 means
+/* Number of K splits the MFMA path uses for this shape (1 <= M <= 128): 1 means
  * mx_w8a16_linear writes y directly; above 1, mx_w8a16_linear_partials can
  * hand the split partials to a consumer that sums them itself (the decode
- * glue kernels below), saving mx_w8a16_linear's separate reduce launch. */
+ * glue kernels below), saving mx_w8a16_linear's separate reduce launch.
+ * Returns 1 for M > 128, where no partials entry exists (mx_w8a16_linear runs
+ * 128-row chunks, each planned as M = 128). */
 int mx_w8a16_splits(int64_t M, int64_t N, int64_t K);
 
 /* The split-K part of mx_w8a16_linear without the reduction:
@@ -100,7 +102,7 @@ int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K, int64_t x_
  * gu_stride >= 2K). The MLP's down projection of a gate||up projection
  * (transformers' down_proj(act_fn(gate_proj(x)) * up_proj(x)), reached from
  * worker_server.py:771-775) without materialising the product. Requires
- * 4 < M <= 64 (the MFMA path); smaller batches use mx_silu_mul and
+ * 4 < M <= 128 (the MFMA path); smaller batches use mx_silu_mul and
  * mx_w8a16_linear. */
 int mx_w8a16_linear_swiglu(const uint16_t* gate_up, int64_t M, int64_t K, int64_t gu_stride, const uint8_t* packed,
                            const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t N, int64_t y_stride,
@@ -117,7 +119,7 @@ int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t M, int64_t 
  * 8t + [0, 8) (scale and bias reordered the same way), quantized and packed
  * as usual. Replaces transformers' act_fn(gate_proj(x)) * up_proj(x) (reached
  * from worker_server.py:771-775) with one launch and half the output bytes.
- * Requires 4 < M <= 64 and mx_w8a16_splits(M, 2I, K) == 1. */
+ * Requires M > 4 (rows are processed 128 at a time) and mx_w8a16_splits(min(M, 128), 2I, K) == 1. */
 int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                            const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I, int64_t y_stride,
                            void* stream);

@@ -425,6 +425,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
 
 // Largest M handled by the VALU GEMV; above it the MFMA kernel runs.
 constexpr int kValuMaxM = 4;
+constexpr int kMaxRows = 128;  // rows per MFMA launch (8 m-tiles); larger M runs in chunks
 constexpr int kGemvWaves = 8;
 constexpr int kMfmaWaves = 4;
 constexpr int kWideGrid = 256;    // at least this many n-groups: no K split
@@ -439,9 +440,16 @@ constexpr int gemv_depth(int M) { return clamp_depth(160 / (4 + 8 * M)); }
 #ifndef MX_GEMM_DEPTH_SMALL_M
 #define MX_GEMM_DEPTH_SMALL_M 8
 #endif
-constexpr int mfma_depth(int MT) { return MT <= 2 ? MX_GEMM_DEPTH_SMALL_M : 6; }
+constexpr int mfma_depth(int MT) { return MT <= 2 ? MX_GEMM_DEPTH_SMALL_M : (MT <= 4 ? 6 : 4); }
 
-// Launch plan for one chunk of at most 64 rows.
+// m-tiles of a chunk of M rows: instantiated for 1, 2, 3, 4, 6 and 8 (5 and 7 round
+// up; rows past M read row M-1 and their results are dropped).
+constexpr int mt_for(int M) {
+    const int mt = (M + 15) / 16;
+    return mt <= 4 ? mt : (mt <= 6 ? 6 : 8);
+}
+
+// Launch plan for one chunk of at most kMaxRows rows.
 struct Plan {
     bool valu;
     int MT, KS;
@@ -467,7 +475,7 @@ static Plan plan_for(int M, int NT, int KT) {
         return pl;
     }
     pl.valu = false;
-    pl.MT = (M + 15) / 16;
+    pl.MT = mt_for(M);
     pl.KS = splits_for(NT, KT);
     return pl;
 }
@@ -550,7 +558,9 @@ static void launch_mfma_mt(int MT, const uint16_t* x, int64_t xs, int M, const u
         case 1: launch_mfma<1, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
         case 2: launch_mfma<2, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
         case 3: launch_mfma<3, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        default: launch_mfma<4, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 4: launch_mfma<4, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 6: launch_mfma<6, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        default: launch_mfma<8, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
     }
 }
 
@@ -591,7 +601,7 @@ extern "C" int mx_w8a16_pack(const int8_t* q, int64_t N, int64_t K, uint8_t* pac
 
 extern "C" size_t mx_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || N % w8a16::kTileN || K % w8a16::kTileK) return 0;
-    const int mc = (int)(M < 64 ? M : 64);  // rows are processed in chunks of at most 64
+    const int mc = (int)(M < w8a16::kMaxRows ? M : w8a16::kMaxRows);  // rows are processed in chunks
     return w8a16::workspace_for(mc, (int)(N / w8a16::kTileN), (int)(K / w8a16::kTileK));
 }
 
@@ -617,8 +627,8 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
     const int KT = (int)(K / w8a16::kTileK);
     hipStream_t st = as_stream(stream);
     float* partial = static_cast<float*>(workspace);
-    for (int64_t m0 = 0; m0 < M; m0 += 64) {
-        const int mc = (int)((M - m0) < 64 ? (M - m0) : 64);
+    for (int64_t m0 = 0; m0 < M; m0 += w8a16::kMaxRows) {
+        const int mc = (int)((M - m0) < w8a16::kMaxRows ? (M - m0) : w8a16::kMaxRows);
         const uint16_t* xc = x + m0 * x_stride;
         uint16_t* yc = y + m0 * y_stride;
         w8a16::Plan pl = w8a16::plan_for(mc, NT, KT);
@@ -643,7 +653,7 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
 }
 
 extern "C" int mx_w8a16_splits(int64_t M, int64_t N, int64_t K) {
-    if (M <= 0 || M > 64 || N <= 0 || K <= 0 || N % w8a16::kTileN || K % w8a16::kTileK) return 1;
+    if (M <= 0 || M > w8a16::kMaxRows || N <= 0 || K <= 0 || N % w8a16::kTileN || K % w8a16::kTileK) return 1;
     return w8a16::plan_for((int)M, (int)(N / w8a16::kTileN), (int)(K / w8a16::kTileK)).KS;
 }
 
@@ -651,8 +661,8 @@ extern "C" int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K,
                                         const uint8_t* packed, const uint16_t* scale, int64_t N, float* partials,
                                         size_t partials_bytes, void* stream) {
     if (!x || !packed || !scale || !partials) return fail(MX_ERR_NULL, "mx_w8a16_linear_partials: null pointer");
-    if (M <= 0 || M > 64 || N <= 0 || K <= 0)
-        return fail(MX_ERR_INVALID, "mx_w8a16_linear_partials: need 1 <= M <= 64 and positive N, K");
+    if (M <= 0 || M > w8a16::kMaxRows || N <= 0 || K <= 0)
+        return fail(MX_ERR_INVALID, "mx_w8a16_linear_partials: need 1 <= M <= %d and positive N, K", w8a16::kMaxRows);
     if (N % w8a16::kTileN || K % w8a16::kTileK)
         return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_linear_partials: need N %% 16 == 0 and K %% 64 == 0");
     if (x_stride < K) return fail(MX_ERR_INVALID, "mx_w8a16_linear_partials: x row stride must cover K");
@@ -679,8 +689,8 @@ extern "C" int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K,
 static int swiglu_checks(const char* what, const uint16_t* gu, int64_t M, int64_t K, int64_t gu_stride,
                          const uint8_t* packed, const uint16_t* scale, int64_t N) {
     if (!gu || !packed || !scale) return fail(MX_ERR_NULL, "%s: null pointer", what);
-    if (M <= w8a16::kValuMaxM || M > 64 || N <= 0 || K <= 0)
-        return fail(MX_ERR_UNSUPPORTED, "%s: needs %d < M <= 64 and positive N, K (M=%lld)", what, w8a16::kValuMaxM,
+    if (M <= w8a16::kValuMaxM || M > w8a16::kMaxRows || N <= 0 || K <= 0)
+        return fail(MX_ERR_UNSUPPORTED, "%s: needs %d < M <= 128 and positive N, K (M=%lld)", what, w8a16::kValuMaxM,
                     (long long)M);
     if (N % w8a16::kTileN || K % w8a16::kTileK)
         return fail(MX_ERR_UNSUPPORTED, "%s: need N %% 16 == 0 and K %% 64 == 0", what);
@@ -734,8 +744,8 @@ extern "C" int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, i
                                       const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I,
                                       int64_t y_stride, void* stream) {
     if (!x || !packed || !scale || !y) return fail(MX_ERR_NULL, "mx_w8a16_gateup_swiglu: null pointer");
-    if (M <= w8a16::kValuMaxM || M > 64 || I <= 0 || K <= 0)
-        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: needs %d < M <= 64 (M=%lld)", w8a16::kValuMaxM,
+    if (M <= w8a16::kValuMaxM || M > 0x7fffffff || I <= 0 || K <= 0)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: needs M > %d (M=%lld)", w8a16::kValuMaxM,
                     (long long)M);
     if (I % 8 || K % w8a16::kTileK)
         return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: need I %% 8 == 0 and K %% 64 == 0");
@@ -745,16 +755,23 @@ extern "C" int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, i
     const int NT = (int)(2 * I / w8a16::kTileN), KT = (int)(K / w8a16::kTileK);
     if ((int64_t)NT * w8a16::kTileN != 2 * I || K * 64 > 0x7fffffff)
         return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: bad shape");
-    const w8a16::Plan pl = w8a16::plan_for((int)M, NT, KT);
-    if (pl.KS != 1)
+    if (w8a16::splits_for(NT, KT) != 1)
         return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: shape splits K (mx_w8a16_splits(M, 2I, K) = %d)",
-                    pl.KS);
+                    w8a16::splits_for(NT, KT));
     hipStream_t st = as_stream(stream);
-    switch (pl.MT) {
-        case 1: w8a16::launch_mfma<1, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
-        case 2: w8a16::launch_mfma<2, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
-        case 3: w8a16::launch_mfma<3, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
-        default: w8a16::launch_mfma<4, false, true>(x, x_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, 1, nullptr, st); break;
+    // Rows in chunks of at most kMaxRows (the MFMA kernel's largest m-tile count), as mx_w8a16_linear.
+    for (int64_t m0 = 0; m0 < M; m0 += w8a16::kMaxRows) {
+        const int mc = (int)(M - m0 < w8a16::kMaxRows ? M - m0 : w8a16::kMaxRows);
+        const uint16_t* xc = x + m0 * x_stride;
+        uint16_t* yc = y + m0 * y_stride;
+        switch (w8a16::mt_for(mc)) {
+            case 1: w8a16::launch_mfma<1, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
+            case 2: w8a16::launch_mfma<2, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
+            case 3: w8a16::launch_mfma<3, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
+            case 4: w8a16::launch_mfma<4, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
+            case 6: w8a16::launch_mfma<6, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
+            default: w8a16::launch_mfma<8, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
+        }
     }
     return check_launch("mx_w8a16_gateup_swiglu");
 }

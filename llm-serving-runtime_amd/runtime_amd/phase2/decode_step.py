@@ -230,6 +230,8 @@ class Int8DecodeModel:
                       "gate_up": (2 * s.intermediate, s.hidden), "down": (s.hidden, s.intermediate),
                       "lm_head": (s.vocab, s.hidden)}
             splits = {k: linear_splits(batch, n, kk) for k, (n, kk) in shapes.items()}
+            # The fused gate||up runs rows 128 at a time and needs an unsplit chunk.
+            splits["gate_up_chunk"] = linear_splits(min(batch, 128), *shapes["gate_up"])
             part_elems = max([splits[k] * batch * shapes[k][0] for k in shapes if splits[k] > 1] + [4])
             buf = _Buffers(h=e(batch, s.hidden), x=e(batch, s.hidden), qkv=e(batch, s.qkv_out),
                            q=e(batch, s.heads * s.head_dim), attn=e(batch, s.heads, 1, s.head_dim),
@@ -313,7 +315,7 @@ class Int8DecodeModel:
         """act = silu(gate) * up from the interleaved gate||up weight."""
         packed, scale, n, bias = w
         ev = self._tick(timers, "gate_up")
-        if bsz > 4 and buf.splits["gate_up"] == 1:
+        if bsz > 4 and buf.splits["gate_up_chunk"] == 1:
             int8_gateup_swiglu(buf.x, packed, scale, bias, n // 2, out=buf.act)
         else:
             int8_linear(buf.x, packed, scale, bias, n, out=buf.gu)

@@ -159,7 +159,7 @@ def _gate_up_rows(gate_up: torch.Tensor) -> torch.Tensor:
 
 def int8_linear_swiglu(gate_up: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
                        out_features: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``y = (silu(g) * u) @ (q*s)^T + b`` for ``gate_up = [g | u]`` fp16 ``[M, 2K]``, 4 < M <= 64.
+    """``y = (silu(g) * u) @ (q*s)^T + b`` for ``gate_up = [g | u]`` fp16 ``[M, 2K]``, 4 < M <= 128.
 
     The product is formed inside the GEMM's x staging (same rounding as
     ``mx_silu_mul``), so it is never written out.

@@ -56,8 +56,12 @@ def test_paged_attn_workspace_layout_is_host_computable():
     assert lib.mx_w8a16_workspace_bytes(1, 4096, 14336) == 0
     assert [lib.mx_w8a16_splits(32, n, k) for n, k in ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336))] \
         == [8, 8, 1, 8]
-    assert lib.mx_w8a16_splits(4, 4096, 4096) == 1 and lib.mx_w8a16_splits(65, 4096, 4096) == 1
-    assert lib.mx_w8a16_workspace_bytes(200, 4096, 14336) == lib.mx_w8a16_workspace_bytes(64, 4096, 14336)
+    # GEMV rows (M <= 4) never split; rows run in chunks of at most 128, and above one
+    # chunk there is no partials entry, so splits reports 1.
+    assert lib.mx_w8a16_splits(4, 4096, 4096) == 1 and lib.mx_w8a16_splits(65, 4096, 4096) == 8
+    assert lib.mx_w8a16_splits(128, 4096, 4096) == 8 and lib.mx_w8a16_splits(129, 4096, 4096) == 1
+    assert lib.mx_w8a16_workspace_bytes(200, 4096, 14336) == lib.mx_w8a16_workspace_bytes(128, 4096, 14336)
+    assert lib.mx_w8a16_workspace_bytes(128, 4096, 14336) == 8 * 128 * 4096 * 4
 
 
 def _status(rc: int, expected: int) -> None:

@@ -128,6 +128,12 @@ def test_native_step_qwen2_shape():
 
 
 @pytest.mark.timeout(600)
+def test_native_step_more_than_64_rows():
+    """72 rows: the linears and the fused gate||up take rows 64 at a time, without K splits."""
+    _run(om.random_qwen2(seed=3, num_hidden_layers=2, vocab_size=32768), batch=72, lo=16, hi=48, seed=3, graph=True)
+
+
+@pytest.mark.timeout(600)
 def test_native_step_llama3_shape_graph_replay():
     hf = om.random_llama(seed=2, num_hidden_layers=2, vocab_size=32768)
     _run(hf, batch=32, lo=48, hi=160, seed=2, graph=True)

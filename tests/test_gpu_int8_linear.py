@@ -61,7 +61,7 @@ def test_quantize_and_pack_bit_exact_config1():
     assert hashlib.sha256(pack_weight(q).cpu().numpy().tobytes()).hexdigest() == doc["packed_sha256"]
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 48, 64, 65, 100])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 48, 64, 65, 80, 100, 112, 128, 129, 200])
 def test_linear_matches_oracle_across_batch(m):
     n, k = 256, 512
     q, s = _quantized(100 + m, n, k)
@@ -101,7 +101,7 @@ def test_linear_config1_golden():
     np.testing.assert_allclose(y, int8_quant.linear_ref_fp32(x.numpy(), q, s), atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("m", [5, 8, 16, 32, 48, 64, 80])
+@pytest.mark.parametrize("m", [5, 8, 16, 32, 48, 64, 80, 128, 150])
 def test_linear_split_k_path_and_unsplit_fallback(m):
     """N=256, K=8192: few n-blocks and a long K, so the planner splits K over workgroups (fp32 partials +
     reduce); calling without a workspace must give the same answer through the unsplit kernel."""
@@ -171,10 +171,12 @@ def test_quantize_model_swaps_linears():
     np.testing.assert_allclose(y.float().cpu().numpy(), int8_quant.linear_ref_fp32(x, q, s, b), atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 4096), (4096, 14336)])
-def test_split_partials_sum_to_linear_output(n, k):
-    """qkv, o and down at M=32 split K: the partials, summed bias-first in split order and
-    rounded, are exactly mx_w8a16_linear's output (its reduce adds in that order)."""
+@pytest.mark.parametrize("n,k,m", [(6144, 4096, 32), (4096, 4096, 32), (4096, 14336, 32), (4096, 4096, 100),
+                                   (4096, 14336, 128)])
+def test_split_partials_sum_to_linear_output(n, k, m):
+    """qkv, o and down at M=32 (and up to one 128-row chunk) split K: the partials, summed
+    bias-first in split order and rounded, are exactly mx_w8a16_linear's output (its reduce
+    adds in that order)."""
     from runtime_amd.phase2.int8_linear import (int8_linear, int8_linear_partials, linear_splits, pack_weight,
                                                 quantize_weight)
 
@@ -182,14 +184,14 @@ def test_split_partials_sum_to_linear_output(n, k):
     w = torch.randn(n, k, generator=g, device="cuda") * 0.02
     q, s = quantize_weight(w)
     packed = pack_weight(q)
-    x = torch.randn(32, k, generator=g, device="cuda").half()
+    x = torch.randn(m, k, generator=g, device="cuda").half()
     bias = (torch.randn(n, generator=g, device="cuda") * 0.1).half()
-    splits = linear_splits(32, n, k)
+    splits = linear_splits(m, n, k)
     assert splits == 8
-    part = torch.full((splits * 32 * n,), float("nan"), dtype=torch.float32, device="cuda")
+    part = torch.full((splits * m * n,), float("nan"), dtype=torch.float32, device="cuda")
     assert int8_linear_partials(x, packed, s, n, part) == splits
-    acc = bias.float().unsqueeze(0).expand(32, n).clone()
-    for sp in part.view(splits, 32, n):
+    acc = bias.float().unsqueeze(0).expand(m, n).clone()
+    for sp in part.view(splits, m, n):
         acc = acc + sp
     y = int8_linear(x, packed, s, bias, n)
     assert torch.equal(acc.half(), y)
@@ -236,7 +238,8 @@ def test_swiglu_linear_equals_silu_mul_then_linear(m, n, k):
         int8_linear_swiglu(gu[:4], packed, s, bias, n)  # M <= 4 takes the GEMV path, not fused
 
 
-@pytest.mark.parametrize("m,inter,k", [(32, 14336, 4096), (7, 4864, 896), (64, 1024, 256)])
+@pytest.mark.parametrize("m,inter,k", [(32, 14336, 4096), (7, 4864, 896), (64, 1024, 256), (128, 1024, 256),
+                                        (70, 4864, 896), (100, 14336, 4096)])
 def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     """gate||up with interleaved rows and the SwiGLU product in the epilogue equals the plain
     [gate | up] projection followed by mx_silu_mul, bit for bit."""
@@ -254,7 +257,7 @@ def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     iq, iscale = quantize_weight(inter_w)
     assert torch.equal(gateup_interleave(plain_s[:inter], plain_s[inter:]), iscale)  # row-wise quantization
     want = silu_mul(int8_linear(x, pack_weight(plain_q), plain_s, None, 2 * inter))
-    if linear_splits(m, 2 * inter, k) != 1:
+    if linear_splits(min(m, 128), 2 * inter, k) != 1:
         pytest.skip("gate||up splits K at this shape; the epilogue fusion does not apply")
     got = int8_gateup_swiglu(x, pack_weight(iq), iscale, None, inter)
     assert torch.equal(got, want)
