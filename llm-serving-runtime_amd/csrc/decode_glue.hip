@@ -213,8 +213,12 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendPar
     }
 }
 
-constexpr int kNormMaxChunks = 8;  // H <= kThreads * 8 * kNormMaxChunks = 16384
+// One workgroup per row. 512 threads keep one 8-column chunk per thread at H = 4096, so
+// all of a row's split partials (8 x 16 KB at the bench shape) are in flight at once.
+constexpr int kNormThreads = 512;
+constexpr int kNormMaxChunks = 4;  // H <= kNormThreads * 8 * kNormMaxChunks = 16384
 
+template <int T>
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -223,7 +227,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     __syncthreads();
     float s = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    for (int w = 0; w < T / 64; ++w) s += red[w];
     return s;
 }
 
@@ -254,16 +258,16 @@ struct NormParams {
 // residual (each thread reads its chunks before it writes them); out must not alias residual_out.
 // KS < 0: fp16 x rows; KS >= 0: split partials (see sum_splits).
 template <int KS>
-__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(NormParams p) {
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(NormParams p) {
     constexpr bool SPLIT = KS >= 0;
-    __shared__ float red[kThreads / 64];
+    __shared__ float red[kNormThreads / 64];
     const int m = blockIdx.x;
     const int chunks = p.H >> 3;
     half8v h[kNormMaxChunks];
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kNormMaxChunks; ++u) {
-        const int c = threadIdx.x + u * kThreads;
+        const int c = threadIdx.x + u * kNormThreads;
         if (c < chunks) {
             half8v v;
             if (SPLIT) {
@@ -289,10 +293,10 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(NormParams p) {
             h[u] = v;
         }
     }
-    const float scale = rsqrtf(block_sum(ss, red) / (float)p.H + p.eps);
+    const float scale = rsqrtf(block_sum<kNormThreads>(ss, red) / (float)p.H + p.eps);
 #pragma unroll
     for (int u = 0; u < kNormMaxChunks; ++u) {
-        const int c = threadIdx.x + u * kThreads;
+        const int c = threadIdx.x + u * kNormThreads;
         if (c < chunks) {
             const half8v g = as_h8(ld16(p.w + c * 8));
             half8v o;
@@ -330,71 +334,99 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, 
 constexpr int kArgThreads = 1024;
 constexpr int kArgU = 16;
 
-__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
-    const bool na = a != a, nb = b != b;
-    if (na != nb) return na;
-    if (na || a == b) return ia < ib;
-    return a > b;
+// Greedy argmax of one fp16 row in two passes over the row (torch's convention: the
+// first index on ties, any NaN counts above every number and the first NaN wins):
+//   1. the row maximum with packed fp16 max (v_pk_max_f16, NaNs ignored) and a NaN
+//      flag from the bits ((x & 0x7fff) + 0x3ff overflows into bit 15 exactly for NaN);
+//   2. the first index whose value equals the maximum (fp16 compare, so -0 == +0), or
+//      the first NaN if the row has one.
+// About two VALU operations per element per pass; a per-element branchy comparison
+// ran at ~20 and made the kernel VALU-bound (22 us for 32 x 128256 on MI355X).
+// kArgU chunks of 8 per thread are loaded per memory round trip (indices clamped).
+__device__ __forceinline__ uint32_t nan_bits(uint32_t w) { return ((w & 0x7fff7fffu) + 0x03ff03ffu) & 0x80008000u; }
+
+template <typename F>
+__device__ __forceinline__ void for_row_chunks(const _Float16* row, int chunks, int tid, F&& f) {
+    for (int c0 = tid; c0 < chunks; c0 += kArgU * kArgThreads) {
+        uint4 v[kArgU];
+#pragma unroll
+        for (int u = 0; u < kArgU; ++u) {
+            const int c = c0 + u * kArgThreads;
+            v[u] = *reinterpret_cast<const uint4*>(row + (c < chunks ? c : chunks - 1) * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < kArgU; ++u) f(c0 + u * kArgThreads, v[u]);
+    }
 }
 
 __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t ls, int N,
                                                              int64_t* __restrict__ out, int32_t* seq_lens) {
-    __shared__ float s_v[kArgThreads / 64];
-    __shared__ int s_i[kArgThreads / 64];
+    constexpr int kW = kArgThreads / 64;
+    __shared__ float s_max[kW];
+    __shared__ int s_nan[kW], s_idx[kW];
     const int m = blockIdx.x, tid = threadIdx.x;
     const _Float16* row = reinterpret_cast<const _Float16*>(logits) + (int64_t)m * ls;
-    float best = -__builtin_huge_valf();
-    int bi = 0x7fffffff;
     const int chunks = N >> 3;
-    // kArgU chunks per thread per memory round trip (indices clamped, compares masked):
-    // one round trip covers a 128K-entry vocabulary. arg_better is a total order, so
-    // the visiting order does not change the result.
-    for (int c0 = tid; c0 < chunks; c0 += kArgU * kArgThreads) {
-        half8v v[kArgU];
+
+    // Pass 1: maximum and NaN flag. A clamped (repeated) chunk changes neither.
+    half2v mx = {(_Float16)(-__builtin_huge_valf()), (_Float16)(-__builtin_huge_valf())};
+    uint32_t nan = 0;
+    for_row_chunks(row, chunks, tid, [&](int, const uint4& v) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int u = 0; u < kArgU; ++u) {
-            const int c = c0 + u * kArgThreads;
-            v[u] = as_h8(*reinterpret_cast<const uint4*>(row + (c < chunks ? c : chunks - 1) * 8));
+        for (int j = 0; j < 4; ++j) {
+            mx = __builtin_elementwise_max(mx, __builtin_bit_cast(half2v, w[j]));
+            nan |= nan_bits(w[j]);
         }
-#pragma unroll
-        for (int u = 0; u < kArgU; ++u) {
-            const int c = c0 + u * kArgThreads;
-            if (c < chunks) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (arg_better((float)v[u][e], c * 8 + e, best, bi)) {
-                        best = (float)v[u][e];
-                        bi = c * 8 + e;
-                    }
-            }
-        }
+    });
+    float best = fmaxf((float)mx[0], (float)mx[1]);
+    for (int n = chunks * 8 + tid; n < N; n += kArgThreads) {
+        const uint16_t bits = logits[(int64_t)m * ls + n];
+        nan |= nan_bits(bits);
+        best = fmaxf(best, (float)row[n]);
     }
-    for (int n = chunks * 8 + tid; n < N; n += kArgThreads)
-        if (arg_better((float)row[n], n, best, bi)) {
-            best = (float)row[n];
-            bi = n;
-        }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o);
-        const int oi = __shfl_xor(bi, o);
-        if (arg_better(ov, oi, best, bi)) {
-            best = ov;
-            bi = oi;
-        }
-    }
+    for (int o = 32; o > 0; o >>= 1) best = fmaxf(best, __shfl_xor(best, o));
+    const bool wave_nan = __builtin_amdgcn_ballot_w64(nan != 0) != 0;
     if ((tid & 63) == 0) {
-        s_v[tid >> 6] = best;
-        s_i[tid >> 6] = bi;
+        s_max[tid >> 6] = best;
+        s_nan[tid >> 6] = wave_nan;
     }
     __syncthreads();
+    bool any_nan = false;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+        best = fmaxf(best, s_max[w]);
+        any_nan |= s_nan[w] != 0;
+    }
+    const _Float16 bh = (_Float16)best;  // exact: the maximum of fp16 values
+
+    // Pass 2: first matching index of this thread (chunks are visited in index order).
+    int first = 0x7fffffff;
+    auto match = [&](uint32_t w) -> uint32_t {  // 2-bit mask for the two halves of w
+        if (any_nan) {
+            const uint32_t nb = nan_bits(w);
+            return (nb >> 15 & 1u) | (nb >> 30 & 2u);
+        }
+        const half2v h = __builtin_bit_cast(half2v, w);
+        return (uint32_t)(h[0] == bh) | ((uint32_t)(h[1] == bh) << 1);
+    };
+    // The second read of the row hits L2; keeping the first read's 64 VGPRs live across
+    // the block reduction instead measured slower (15.8 vs 10.9 us at 32 x 128256).
+    for_row_chunks(row, chunks, tid, [&](int c, const uint4& v) {
+        const uint32_t mask = match(v.x) | match(v.y) << 2 | match(v.z) << 4 | match(v.w) << 6;
+        if (c < chunks && mask != 0 && first == 0x7fffffff) first = c * 8 + __builtin_ctz(mask);
+    });
+    for (int n = chunks * 8 + tid; n < N && first == 0x7fffffff; n += kArgThreads)
+        if (match(logits[(int64_t)m * ls + n]) & 1u) first = n;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) first = min(first, __shfl_xor(first, o));
+    if ((tid & 63) == 0) s_idx[tid >> 6] = first;
+    __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < kArgThreads / 64; ++w)
-            if (arg_better(s_v[w], s_i[w], best, bi)) {
-                best = s_v[w];
-                bi = s_i[w];
-            }
-        out[m] = bi;
+#pragma unroll
+        for (int w = 1; w < kW; ++w) first = min(first, s_idx[w]);
+        out[m] = first;
         if (seq_lens) seq_lens[m] += 1;
     }
 }
@@ -499,13 +531,13 @@ static int add_rmsnorm_common(const char* what, glue::NormParams& p, int32_t M, 
     if (M < 0) return fail(MX_ERR_INVALID, "%s: M must be >= 0", what);
     if (M == 0) return MX_OK;
     if (!p.w || !p.out) return fail(MX_ERR_NULL, "%s: null pointer", what);
-    if (p.H <= 0 || p.H % 8 || p.H > glue::kThreads * 8 * glue::kNormMaxChunks)
+    if (p.H <= 0 || p.H % 8 || p.H > glue::kNormThreads * 8 * glue::kNormMaxChunks)
         return fail(MX_ERR_INVALID, "%s: need H %% 8 == 0 and H <= %d (H=%d)", what,
-                    glue::kThreads * 8 * glue::kNormMaxChunks, p.H);
+                    glue::kNormThreads * 8 * glue::kNormMaxChunks, p.H);
     if (p.os % 8 || (p.res && p.rs % 8) || (p.res_out && p.ros % 8) || !glue::a16(p.w) || !glue::a16(p.out) ||
         (p.res && !glue::a16(p.res)) || (p.res_out && !glue::a16(p.res_out)))
         return fail(MX_ERR_ALIGNMENT, "%s: rows need 16-byte alignment", what);
-    const dim3 grid(M), block(glue::kThreads);
+    const dim3 grid(M), block(glue::kNormThreads);
     hipStream_t st = as_stream(stream);
     if (!p.part) hipLaunchKernelGGL(glue::add_rmsnorm_kernel<-1>, grid, block, 0, st, p);
     else if (p.splits == 2) hipLaunchKernelGGL(glue::add_rmsnorm_kernel<2>, grid, block, 0, st, p);
