@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 6
+#define MX_ABI_VERSION 7
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -261,6 +261,20 @@ int mx_add_rmsnorm_splits(const float* partials, int32_t splits, const uint16_t*
  * KV lengths past the token just decoded. */
 int mx_argmax_rows(const uint16_t* logits, int64_t stride, int32_t M, int32_t N, int64_t* out, int32_t* seq_lens,
                    void* stream);
+
+/* SwiGLU of the interleaved gate||up projection used by mx_w8a16_gateup_swiglu
+ * (rows 16t + [0, 8) gate channels 8t + [0, 8), rows 16t + [8, 16) the matching
+ * up channels): out[m, 8t + e] = fp16(fp16(silu(g)) * u), with g and u rounded
+ * to fp16 as that projection's output is. Input is either its fp16 output rows
+ * (gate_up, [M, 2I], row stride gu_stride; partials NULL) or its split-K
+ * partials (partials [splits][M][2I] from mx_w8a16_linear_partials plus bias,
+ * summed bias-first in split order exactly as mx_w8a16_linear's reduce;
+ * gate_up NULL). For the shapes mx_w8a16_gateup_swiglu does not take (M <= 4,
+ * or gate||up split over K): HF MLP act_fn(gate_proj(x)) * up_proj(x),
+ * reached from worker_server.py:771-775. I % 8 == 0. */
+int mx_swiglu_interleaved(const uint16_t* gate_up, int64_t gu_stride, const float* partials, int32_t splits,
+                          const uint16_t* bias, int32_t M, int32_t I, uint16_t* out, int64_t out_stride,
+                          void* stream);
 
 /* out[m, i] = fp16(fp16(silu(gate_up[m, i])) * gate_up[m, I + i]) for i < I
  * (I % 8 == 0): the SwiGLU product between the fused gate||up projection and

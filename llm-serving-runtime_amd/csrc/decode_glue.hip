@@ -329,6 +329,44 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, 
     st16(out + m * os + c * 8, as_u4(o));
 }
 
+// SwiGLU of the interleaved gate||up projection (rows 16t + [0, 8) are gate channels
+// 8t + [0, 8), rows 16t + [8, 16) the matching up channels): out[m, 8t + e] =
+// fp16(fp16(silu(g)) * u) with g, u rounded to fp16 as the projection's own output is.
+// KS < 0: g, u from its fp16 output rows; KS >= 0: from its split-K partials [splits][M][2I]
+// plus bias, summed bias-first in split order (bit-identical to mx_w8a16_linear's reduce).
+// One thread per (row, group of 8 channels).
+template <int KS>
+__global__ __launch_bounds__(kThreads) void swiglu_interleaved_kernel(const uint16_t* gu, int64_t gs, const float* part,
+                                                                      int splits, const uint16_t* bias, int I,
+                                                                      uint16_t* out, int64_t os, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= total) return;
+    const int groups = I >> 3;
+    const int t = (int)(i % groups);
+    const int64_t m = i / groups;
+    _Float16 g[8], u[8];
+    if (KS < 0) {
+        const half8v gv = as_h8(ld16(gu + m * gs + 16 * t));
+        const half8v uv = as_h8(ld16(gu + m * gs + 16 * t + 8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            g[e] = gv[e];
+            u[e] = uv[e];
+        }
+    } else {
+        const int64_t n2 = 2 * (int64_t)I, stride = (total / groups) * n2;  // M * 2I per split
+        sum_splits<(KS > 0 ? KS : 0), 8>(part, splits, stride, m * n2 + 16 * t, bias, 16 * t, g);
+        sum_splits<(KS > 0 ? KS : 0), 8>(part, splits, stride, m * n2 + 16 * t + 8, bias, 16 * t + 8, u);
+    }
+    half8v o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const _Float16 sg = (_Float16)silu_f32((float)g[e]);
+        o[e] = (_Float16)((float)sg * (float)u[e]);
+    }
+    st16(out + m * os + 8 * t, as_u4(o));
+}
+
 // Greedy token of each row: index of the largest logit, the first one on ties; NaN counts as
 // larger than any number (torch.argmax's convention). One workgroup of 1024 threads per row.
 constexpr int kArgThreads = 1024;
@@ -590,6 +628,37 @@ extern "C" int mx_silu_mul(const uint16_t* gate_up, int64_t gu_stride, int32_t M
     hipLaunchKernelGGL(glue::silu_mul_kernel, dim3((unsigned)ceil_div(total, glue::kThreads)), dim3(glue::kThreads),
                        0, as_stream(stream), gate_up, gu_stride, I, out, out_stride, total);
     return check_launch("mx_silu_mul");
+}
+
+extern "C" int mx_swiglu_interleaved(const uint16_t* gate_up, int64_t gu_stride, const float* partials,
+                                     int32_t splits, const uint16_t* bias, int32_t M, int32_t I, uint16_t* out,
+                                     int64_t out_stride, void* stream) {
+    clear_error();
+    if (M < 0) return fail(MX_ERR_INVALID, "mx_swiglu_interleaved: M must be >= 0");
+    if (M == 0) return MX_OK;
+    if (!out || (!gate_up) == (!partials))
+        return fail(MX_ERR_NULL, "mx_swiglu_interleaved: need out and exactly one of gate_up / partials");
+    if (I <= 0 || I % 8) return fail(MX_ERR_INVALID, "mx_swiglu_interleaved: need I %% 8 == 0 (I=%d)", I);
+    if (out_stride < I || out_stride % 8 || !glue::a16(out))
+        return fail(MX_ERR_ALIGNMENT, "mx_swiglu_interleaved: output rows must be 16-byte aligned and cover I");
+    if (gate_up && (gu_stride < 2 * (int64_t)I || gu_stride % 8 || !glue::a16(gate_up)))
+        return fail(MX_ERR_ALIGNMENT, "mx_swiglu_interleaved: gate_up rows must be 16-byte aligned and cover 2I");
+    if (partials && (splits < 1 || !glue::a16(partials) || (bias && !glue::a16(bias))))
+        return fail(MX_ERR_INVALID, "mx_swiglu_interleaved: need splits >= 1 and 16-byte aligned partials and bias");
+    const int64_t total = (int64_t)M * (I / 8);
+    const dim3 grid((unsigned)ceil_div(total, glue::kThreads)), block(glue::kThreads);
+    hipStream_t st = as_stream(stream);
+    if (gate_up) hipLaunchKernelGGL(glue::swiglu_interleaved_kernel<-1>, grid, block, 0, st, gate_up, gu_stride,
+                                    nullptr, 0, nullptr, I, out, out_stride, total);
+    else if (splits == 2) hipLaunchKernelGGL(glue::swiglu_interleaved_kernel<2>, grid, block, 0, st, nullptr, 0,
+                                             partials, splits, bias, I, out, out_stride, total);
+    else if (splits == 4) hipLaunchKernelGGL(glue::swiglu_interleaved_kernel<4>, grid, block, 0, st, nullptr, 0,
+                                             partials, splits, bias, I, out, out_stride, total);
+    else if (splits == 8) hipLaunchKernelGGL(glue::swiglu_interleaved_kernel<8>, grid, block, 0, st, nullptr, 0,
+                                             partials, splits, bias, I, out, out_stride, total);
+    else hipLaunchKernelGGL(glue::swiglu_interleaved_kernel<0>, grid, block, 0, st, nullptr, 0, partials, splits,
+                            bias, I, out, out_stride, total);
+    return check_launch("mx_swiglu_interleaved");
 }
 
 extern "C" int mx_argmax_rows(const uint16_t* logits, int64_t stride, int32_t M, int32_t N, int64_t* out,

@@ -83,6 +83,12 @@ constexpr int kTile = 16;               // tokens per MFMA tile
 constexpr int kMaxRangeTiles = 64;      // a worker's range fits one vector of block ids
 constexpr int kDefaultWorkers = 2048;   // 256 CUs x 8 waves on MI355X
 constexpr int kMinDefaultTiles = 4;     // default ranges are at least this long when T allows
+// Default workers per segment on average (the merge reads 16 pieces per memory round trip),
+// but never fewer than one worker per CU. Measured on the Qwen2-0.5B shape (B 16, 2 kv-heads,
+// contexts U[512, 2048]): 4-tile ranges (~20 pieces per segment) 19.6 us per call, ~8
+// pieces 15.3 us; at the Llama-3-8B bench shape the cap is not reached (2048 workers).
+constexpr int kPiecesPerSegment = 8;
+constexpr int kMinWorkers = 256;
 constexpr int kMaxChunkTokens = kMaxRangeTiles * kTile;
 constexpr float kLazyLog2 = 8.0f;       // rescale only when the running max rises by more than 2^8
 
@@ -497,7 +503,9 @@ static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // count, so W >= ceil(T_max / 64) keeps each range within one vector of block
 // ids. chunk_tokens > 0 asks for ranges of about that many tokens at T_max;
 // 0 picks kDefaultWorkers (one round of resident waves on the chip), fewer
-// when that would make ranges shorter than kMinDefaultTiles tiles.
+// when that would make ranges shorter than kMinDefaultTiles tiles or cut a
+// segment into more than kPiecesPerSegment pieces on average (but at least
+// kMinWorkers).
 static int resolve_workers(int chunk_tokens, int B, int Hkv, int max_blocks, int block_size) {
     const int64_t row_tiles_max = ceil_div((int64_t)max_blocks * block_size, kTile);
     const int64_t t_max = (int64_t)B * Hkv * row_tiles_max;
@@ -507,6 +515,9 @@ static int resolve_workers(int chunk_tokens, int B, int Hkv, int max_blocks, int
         w = ceil_div(t_max, chunk_tokens / kTile);
     } else {
         w = ceil_div(t_max, kMinDefaultTiles);
+        const int64_t per_seg = (int64_t)B * Hkv * kPiecesPerSegment;
+        const int64_t cap = per_seg > kMinWorkers ? per_seg : kMinWorkers;
+        if (w > cap) w = cap;
         if (w > kDefaultWorkers) w = kDefaultWorkers;
     }
     if (w < floor_w) w = floor_w;

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -65,6 +65,7 @@ SIGNATURES = {
         [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, ctypes.c_float, _p, _i64, _p, _i64, _p],
     ),
     "mx_argmax_rows": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p]),
+    "mx_swiglu_interleaved": (ctypes.c_int, [_p, _i64, _p, _i32, _p, _i32, _i32, _p, _i64, _p]),
     "mx_qkv_rope_append_splits": (
         ctypes.c_int,
         [_p, _i32, _p, _i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _i32, _i32,

@@ -12,6 +12,8 @@
   the producing linear's split-K partials (``int8_linear_partials``) and
   forming its fp16 output on the fly;
 * :func:`silu_mul` — SwiGLU's ``silu(gate) * up``;
+* :func:`swiglu_interleaved` — the same for the interleaved gate||up projection, from its
+  fp16 output or its split-K partials;
 * :func:`rope_table` — the fp32 ``(cos, sin)`` table the fused RoPE reads,
   computed like transformers' default rotary embedding
   (``inv_freq = theta ** -(2i / D)``, angle ``pos * inv_freq`` in fp32).
@@ -223,6 +225,39 @@ def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: tor
         w.data_ptr(), m, h, float(eps), o2.data_ptr(), o2.stride(0),
         ro2.data_ptr() if ro2 is not None else None, ro2.stride(0) if ro2 is not None else 0,
         _hip.stream_handle(x.device)), "mx_add_rmsnorm")
+    return out
+
+
+def swiglu_interleaved(gate_up: torch.Tensor | None, inter: int, partials: torch.Tensor | None = None,
+                       splits: int = 0, bias: torch.Tensor | None = None, rows: int | None = None,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(g) * u`` of the interleaved gate||up projection (``gateup_interleave`` row order).
+
+    From its fp16 output ``gate_up [M, 2*inter]``, or (``gate_up=None``) from its split-K
+    ``partials`` (``[splits, rows, 2*inter]`` fp32, :func:`int8_linear_partials`) plus ``bias``,
+    rounded as the projection's own output. Returns fp16 ``[M, inter]``.
+    """
+    if (gate_up is None) == (partials is None):
+        raise ValueError("give exactly one of gate_up and partials")
+    if gate_up is not None:
+        _hip.require_device_tensor(gate_up, "gate_up")
+        g2 = _rows16(gate_up.reshape(-1, gate_up.shape[-1]))
+        m = int(g2.shape[0])
+        if g2.dtype != torch.float16 or g2.shape[1] != 2 * inter:
+            raise ValueError("gate_up must be fp16 [M, 2*inter]")
+        dev = g2.device
+    else:
+        _hip.require_device_tensor(partials, "partials")
+        if rows is None or partials.dtype != torch.float32 or partials.numel() < splits * rows * 2 * inter:
+            raise ValueError("partials must be fp32 [splits, rows, 2*inter] (give rows and splits)")
+        m, dev = int(rows), partials.device
+    out = torch.empty(m, inter, dtype=torch.float16, device=dev) if out is None else out
+    o2 = out.view(m, inter)
+    b = bias.contiguous() if bias is not None else None
+    _hip.check(_hip.load().mx_swiglu_interleaved(
+        g2.data_ptr() if gate_up is not None else None, g2.stride(0) if gate_up is not None else 0,
+        partials.data_ptr() if partials is not None else None, int(splits), b.data_ptr() if b is not None else None,
+        m, int(inter), o2.data_ptr(), o2.stride(0), _hip.stream_handle(dev)), "mx_swiglu_interleaved")
     return out
 
 

@@ -36,9 +36,9 @@ Llama / Qwen2 style (pre-norm, rotate-half RoPE, GQA, SwiGLU, untied int8
 lm_head); :meth:`Int8DecodeModel.from_hf` loads the weights of an HF
 ``LlamaForCausalLM`` / ``Qwen2ForCausalLM``. The gate||up weight is stored
 with gate and up rows interleaved in groups of 8 (``gateup_interleave``);
-where the fused epilogue does not apply (batch <= 4, or a batch whose
-gate||up GEMM splits K) the projection runs plain, its output is put back in
-[gate | up] order and ``mx_silu_mul`` forms the product.
+where the fused epilogue does not apply, ``mx_swiglu_interleaved`` forms the
+product from the projection's split-K partials (a gate||up GEMM that splits K,
+e.g. Qwen2-0.5B at batch 16) or from its fp16 output (batch <= 4, GEMV).
 """
 
 from __future__ import annotations
@@ -49,8 +49,8 @@ from dataclasses import dataclass
 import torch
 
 from .decode_glue import (add_rmsnorm, add_rmsnorm_splits, argmax_rows, qkv_rope_append, qkv_rope_append_splits,
-                          rope_table, silu_mul)
-from .int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu, int8_linear,
+                          rope_table, swiglu_interleaved)
+from .int8_linear import (gateup_interleave, int8_gateup_swiglu, int8_linear,
                           int8_linear_partials, linear_splits, pack_weight, quantize_weight)
 from .paged_attention_hip import _decode as _paged_decode
 
@@ -317,9 +317,13 @@ class Int8DecodeModel:
         ev = self._tick(timers, "gate_up")
         if bsz > 4 and buf.splits["gate_up_chunk"] == 1:
             int8_gateup_swiglu(buf.x, packed, scale, bias, n // 2, out=buf.act)
+        elif buf.splits["gate_up"] > 1:  # split over K: the SwiGLU consumer sums the partials
+            int8_linear_partials(buf.x, packed, scale, n, buf.part)
+            swiglu_interleaved(None, n // 2, partials=buf.part, splits=buf.splits["gate_up"], bias=bias, rows=bsz,
+                               out=buf.act)
         else:
             int8_linear(buf.x, packed, scale, bias, n, out=buf.gu)
-            silu_mul(gateup_deinterleave(buf.gu).contiguous(), out=buf.act)
+            swiglu_interleaved(buf.gu, n // 2, out=buf.act)
         self._tock(timers, "gate_up", ev)
 
     def _partials(self, x, w, part, timers, name):

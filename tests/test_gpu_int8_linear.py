@@ -302,3 +302,44 @@ def test_gateup_swiglu_epilogue_wide_shapes(m, inter):
     want = silu_mul(int8_linear(x, pack_weight(plain_q), plain_s, None, 2 * inter))
     got = int8_gateup_swiglu(x, pack_weight(iq), iscale, None, inter)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("m,inter,k", [(16, 4864, 896), (3, 1024, 256), (32, 14336, 4096), (100, 4864, 896)])
+def test_swiglu_interleaved_equals_separate_ops(m, inter, k):
+    """mx_swiglu_interleaved from the interleaved projection's fp16 output, and (where the shape
+    splits K) from its split partials + bias, equals the [gate | up] projection followed by
+    mx_silu_mul, bit for bit."""
+    from runtime_amd.phase2.decode_glue import silu_mul, swiglu_interleaved
+    from runtime_amd.phase2.int8_linear import gateup_interleave, int8_linear_partials, linear_splits
+
+    g = torch.Generator(device="cuda").manual_seed(m * 7 + inter + k)
+    wg = torch.randn(inter, k, generator=g, device="cuda") * 0.02
+    wu = torch.randn(inter, k, generator=g, device="cuda") * 0.02
+    bg = (torch.randn(inter, generator=g, device="cuda") * 0.1).half()
+    bu = (torch.randn(inter, generator=g, device="cuda") * 0.1).half()
+    x = torch.randn(m, k, generator=g, device="cuda").half()
+    plain_q, plain_s = quantize_weight(torch.cat([wg, wu]))
+    want = silu_mul(int8_linear(x, pack_weight(plain_q), plain_s, torch.cat([bg, bu]), 2 * inter))
+    iq, iscale = quantize_weight(gateup_interleave(wg, wu))
+    ibias = gateup_interleave(bg, bu)
+    packed = pack_weight(iq)
+    y = int8_linear(x, packed, iscale, ibias, 2 * inter)
+    assert torch.equal(swiglu_interleaved(y, inter), want)
+    splits = linear_splits(m, 2 * inter, k)
+    if splits > 1:
+        part = torch.full((splits * m * 2 * inter,), float("nan"), dtype=torch.float32, device="cuda")
+        assert int8_linear_partials(x, packed, iscale, 2 * inter, part) == splits
+        got = swiglu_interleaved(None, inter, partials=part, splits=splits, bias=ibias, rows=m)
+        assert torch.equal(got, want)
+
+
+def test_swiglu_interleaved_rejects_bad_arguments():
+    from runtime_amd.phase2.decode_glue import swiglu_interleaved
+
+    y = torch.zeros(4, 32, device="cuda").half()
+    with pytest.raises(ValueError):
+        swiglu_interleaved(y, 8)  # 2*inter != 32
+    with pytest.raises(ValueError):
+        swiglu_interleaved(y, 16, partials=torch.zeros(8, device="cuda"), splits=2, rows=4)  # both inputs
+    with pytest.raises(ValueError):
+        swiglu_interleaved(None, 16, partials=torch.zeros(8, device="cuda"), splits=2, rows=4)  # too small
