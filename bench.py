@@ -41,10 +41,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=None, help="rows (default 32; 128 for --workload prefix-batch)")
-    ap.add_argument("--workload", choices=["decode", "prefix-batch"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefix-batch", "linear-sweep", "attention"], default="decode",
                     help="decode: the headline step (default). prefix-batch: 128 rows in 16 groups of 8 sharing "
                          "a 1024-token prefix (aliased blocks), contexts U[1, 8192], 16 rows finish and 16 join "
-                         "every 16 steps")
+                         "every 16 steps. linear-sweep: the single int8 linear (4096x4096, M=1) and the "
+                         "Llama-3-8B projections at M in {1, 8, 32, 64}. attention: one paged decode call on "
+                         "the config-2 inputs (B 32, contexts U[128, 4096], pool 16384 blocks)")
     ap.add_argument("--model", choices=["llama3-8b", "qwen2-0.5b"], default="llama3-8b")
     ap.add_argument("--layers", type=int, default=None, help="override layer count (diagnostics only)")
     ap.add_argument("--ctx-lo", type=int, default=128)
@@ -425,6 +427,188 @@ def prefix_batch_bench(args) -> int:
     return 0
 
 
+def graph_time(run, launches: int, reps: int = 4) -> float:
+    """Seconds per launch of ``run`` (``launches`` kernel calls), captured once and replayed."""
+    import torch
+
+    run()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3 / (reps * launches)
+
+
+def linear_sweep_bench(args) -> int:
+    """Config 1 (x [1, 4096] @ W [4096, 4096], seed 0) and config 4 (the Llama-3-8B projections,
+    seed 1000 + shape index, M in {1, 8, 32, 64}) through ``int8_linear``. Weights are
+    N(0, 0.02) quantized on the device; each timed graph walks over enough distinct weight
+    copies (> 512 MB) that no launch reads its weights from the 256 MB MALL. Bytes are the
+    algorithmic N*K + 2N + 2MK + 2MN. The CPU oracle (fp32, pre-dequantized weights and with
+    the dequantization per call) is timed on config 1."""
+    import numpy as np
+    import torch
+
+    from oracle import int8_quant
+    from runtime_amd.phase2 import _hip
+    from runtime_amd.phase2.int8_linear import int8_linear, pack_weight, quantize_weight
+
+    _hip.load()
+    dev = torch.device("cuda:0")
+    shapes = [("config1", 4096, 4096, [1])] + [(n, k, nn, [1, 8, 32, 64]) for n, k, nn in
+                                               (("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 28672),
+                                                ("down", 14336, 4096))]
+    rows = []
+    for idx, (name, k, n, ms) in enumerate(shapes):
+        g = torch.Generator(device=dev).manual_seed(0 if name == "config1" else 1000 + idx - 1)
+        copies = max(4, math.ceil(600e6 / (n * k)))
+        weights = []
+        for _ in range(copies):
+            q, sc = quantize_weight(torch.randn(n, k, generator=g, device=dev) * 0.02)
+            weights.append((pack_weight(q), sc))
+        for m in ms:
+            x = torch.randn(m, k, generator=g, device=dev).half()
+            y = torch.empty(m, n, dtype=torch.float16, device=dev)
+
+            def run():
+                for packed, sc in weights:
+                    int8_linear(x, packed, sc, None, n, out=y)
+            t = graph_time(run, copies)
+            byts = n * k + 2 * n + 2 * m * k + 2 * m * n
+            rows.append({"shape": name, "m": m, "n": n, "k": k, "avg_us": round(t * 1e6, 2),
+                         "gbps": round(byts / t / 1e9, 1), "frac": round(byts / t / 1e9 / HBM_PEAK_GBPS, 4)})
+            print(f"[linear] {name} M={m}: {t * 1e6:.2f} us, {byts / t / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+        del weights
+        torch.cuda.empty_cache()
+    # CPU oracle on config 1.
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+    q, sc = int8_quant.quantize_per_channel(w)
+    xh = rng.standard_normal((1, 4096)).astype(np.float16)
+    wd = torch.from_numpy(int8_quant.dequantize(q, sc))
+    xf = torch.from_numpy(xh.astype(np.float32))
+    qt, st = torch.from_numpy(q), torch.from_numpy(sc.astype(np.float32))
+    reps = 200
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        xf @ wd.T
+    t_pre = (time.perf_counter() - t0) / reps
+    t0 = time.perf_counter()
+    for _ in range(20):
+        xf @ (qt.float() * st[:, None]).T
+    t_deq = (time.perf_counter() - t0) / 20
+    c1 = rows[0]
+    byts1 = 4096 * 4096 + 2 * 4096 + 2 * 4096 + 2 * 4096
+    out = {
+        "metric": "int8 linear algorithmic HBM GB/s (config 1; config 4 sweep in 'sweep')",
+        "value": c1["gbps"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "w8a16 (int8 weights, fp16 activations, fp32 accumulate)",
+        "data": "synthetic (N(0,0.02) weights quantized on device)",
+        "config": {"workload": "int8 linear: 4096x4096 at M=1 (config 1); Llama-3-8B qkv/o/gate_up/down at "
+                               "M in {1,8,32,64} (config 4)"},
+        "roofline": {"bound": "hbm", "kernel": "config1", "achieved": c1["gbps"], "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": c1["frac"], "traffic": None},
+        "sweep": rows,
+        "cpu_baseline": {"value": round(byts1 / t_pre / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+                         "sample": "config 1 on the CPU oracle (fp32 x @ dequantized W^T, weights dequantized "
+                                   "once); with the dequantization in each call: "
+                                   f"{byts1 / t_deq / 1e9:.2f} GB/s",
+                         "us_per_call": round(t_pre * 1e6, 1), "us_per_call_dequant": round(t_deq * 1e6, 1)},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def attention_bench(args) -> int:
+    """Config 2: ``torch.manual_seed(0)``; seq_lens ~ U{128..4096} for 32 rows; each row takes
+    ceil(S/16) ids from one randperm(16384); q [32, 32, 1, 128] and K/V N(0, 1) fp16; scale
+    1/sqrt(128). The timed graph walks over 32 layer copies of the pool (one call per layer,
+    as in the decode step) so no call re-reads K/V from the MALL. The CPU oracle (per-row fp32
+    paged attention) is timed on the same inputs."""
+    import torch
+
+    from oracle.paged_attention import attention_bytes, decode_rows_fp32
+    from runtime_amd.phase2 import _hip
+    from runtime_amd.phase2.paged_attention_hip import _decode
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    _hip.load()
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, bs, nb, L = 32, 32, 8, 128, 16, 16384, 32
+    torch.manual_seed(0)
+    lens = torch.randint(128, 4097, (B,))
+    perm = torch.randperm(nb)
+    nblk = [math.ceil(int(x) / bs) for x in lens]
+    tables = torch.zeros(B, max(nblk), dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(nblk):
+        tables[b, :n] = perm[used:used + n].to(torch.int32)
+        used += n
+    q = torch.randn(B, Hq, 1, D).half()
+    pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=bs, num_layers=L, num_kv_heads=Hkv, head_dim=D,
+                          dtype=torch.float16, device=dev)
+    pool._ensure_pools()
+    gk = torch.Generator(device=dev).manual_seed(0)
+    for t in (pool._k_pool, pool._v_pool):
+        flat = t.view(-1)
+        for i in range(0, flat.numel(), 1 << 28):
+            flat[i:i + (1 << 28)].normal_(generator=gk)
+    qd, td, ld = q.to(dev), tables.to(dev), lens.to(device=dev, dtype=torch.int32)
+    scale = D**-0.5
+
+    def run():
+        for li in range(L):
+            _decode(qd, pool.k_layer_view(li), pool.v_layer_view(li), td, ld, scale, Hq // Hkv)
+    t = graph_time(run, L, reps=max(2, args.kernel_steps))
+    byts = attention_bytes(lens.tolist(), Hkv, D, Hq, bs)
+    # CPU oracle on layer 0's blocks.
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    ids = torch.unique(tables[tables >= 0])
+    kc = pool.k_layer_view(0)[ids.to(dev)].cpu()
+    vc = pool.v_layer_view(0)[ids.to(dev)].cpu()
+    remap = torch.full((nb,), -1, dtype=torch.int32)
+    remap[ids] = torch.arange(ids.numel(), dtype=torch.int32)
+    tc = remap[tables.long()]
+    decode_rows_fp32(q, kc, vc, tc, lens.tolist(), scale, Hq // Hkv)  # warm
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        decode_rows_fp32(q, kc, vc, tc, lens.tolist(), scale, Hq // Hkv)
+    t_cpu = (time.perf_counter() - t0) / reps
+    achieved = byts / t / 1e9
+    out = {
+        "metric": "paged decode attention algorithmic HBM GB/s (config 2)", "value": round(achieved, 1),
+        "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "avg_us": round(t * 1e6, 2),
+        "dtype": "fp16 K/V and q, fp32 softmax and accumulation",
+        "data": "synthetic (N(0,1) K/V, q; torch.manual_seed(0) contexts and block ids)",
+        "config": {"workload": "paged decode attention, B 32, Hq 32, Hkv 8, D 128, block 16, contexts "
+                               "U[128,4096], pool 16384 blocks x 32 layers", "bytes_per_call": byts},
+        "roofline": {"bound": "hbm", "kernel": "attn", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+        "cpu_baseline": {"value": round(byts / t_cpu / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+                         "sample": "one call of the per-row fp32 oracle (oracle.paged_attention.decode_rows_fp32) "
+                                   "on the same inputs", "ms_per_call": round(t_cpu * 1e3, 1)},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -436,6 +620,10 @@ def main() -> int:
         return traffic_probe(args)
     if args.workload == "prefix-batch":
         return prefix_batch_bench(args)
+    if args.workload == "linear-sweep":
+        return linear_sweep_bench(args)
+    if args.workload == "attention":
+        return attention_bench(args)
 
     import torch
 

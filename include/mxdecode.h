@@ -119,7 +119,8 @@ int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t M, int64_t 
  * 8t + [0, 8) (scale and bias reordered the same way), quantized and packed
  * as usual. Replaces transformers' act_fn(gate_proj(x)) * up_proj(x) (reached
  * from worker_server.py:771-775) with one launch and half the output bytes.
- * Requires M > 4 (rows are processed 128 at a time) and mx_w8a16_splits(min(M, 128), 2I, K) == 1. */
+ * Rows are processed 128 at a time; the shape must not split K
+ * (mx_w8a16_splits(min(M, 128), 2I, K) == 1, true for every M when it holds at M = 128). */
 int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                            const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I, int64_t y_stride,
                            void* stream);

@@ -435,8 +435,9 @@ constexpr int kMinSplitTiles = 4; // k-tiles per split
 
 // Pipeline depth from the VGPRs one stage costs (4 per 1 KiB weight tile, 8
 // per x row fragment of 32 bytes) after the accumulators.
-constexpr int clamp_depth(int d) { return d < 2 ? 2 : (d > 8 ? 8 : d); }
-constexpr int gemv_depth(int M) { return clamp_depth(160 / (4 + 8 * M)); }
+// GEMV pipeline depth per M (a stage holds 4 VGPRs of weights and 8 per x row); at M = 2
+// a depth of 8 reached 256 VGPRs and spilled.
+constexpr int gemv_depth(int M) { return M <= 1 ? 8 : (M == 2 ? 6 : (M == 3 ? 5 : 4)); }
 #ifndef MX_GEMM_DEPTH_SMALL_M
 #define MX_GEMM_DEPTH_SMALL_M 8
 #endif
@@ -469,7 +470,11 @@ static int splits_for(int NT, int KT) {
 static Plan plan_for(int M, int NT, int KT) {
     Plan pl{};
     pl.KS = 1;
-    if (M <= kValuMaxM) {
+    // The VALU GEMV takes M <= 4 unless the n-groups alone fill the chip: there the
+    // MFMA kernel's wide workgroups stream faster even with 15 padding rows (gate||up
+    // at M = 1: 33.2 us GEMV, 23 us MFMA), while split shapes keep the GEMV, which needs
+    // no reduce (4096 x 4096 at M = 1: 6.3 us).
+    if (M <= kValuMaxM && splits_for(NT, KT) > 1) {
         pl.valu = true;
         pl.MT = M;
         return pl;
@@ -492,7 +497,7 @@ static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const u
                        xs, w, s, b, y, ys, KT);
 }
 
-// Workgroup shape of an unsplit launch at M <= 32: about one workgroup per CU,
+// Workgroup shape of an unsplit launch at M <= 64: about one workgroup per CU,
 // each as wide as possible, so that one x k-tile staged in LDS feeds as many
 // weight tiles as possible. Every workgroup re-reads all of x: with 4-wave
 // workgroups a CU loads as many x bytes as weight bytes, and those loads, not
@@ -528,7 +533,7 @@ static void launch_shape(const uint16_t* x, int64_t xs, int M, const uint8_t* w,
 template <int MT, bool SW, bool GU = false>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
-    if constexpr (MT <= 2 && !SW) {
+    if constexpr (MT <= 4 && !SW) {
         if (KS == 1) {
             const WideShape ws = wide_shape(NT, GU);
 #define MX_WIDE(W, NPW)                                                                                     \
@@ -744,9 +749,8 @@ extern "C" int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, i
                                       const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I,
                                       int64_t y_stride, void* stream) {
     if (!x || !packed || !scale || !y) return fail(MX_ERR_NULL, "mx_w8a16_gateup_swiglu: null pointer");
-    if (M <= w8a16::kValuMaxM || M > 0x7fffffff || I <= 0 || K <= 0)
-        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: needs M > %d (M=%lld)", w8a16::kValuMaxM,
-                    (long long)M);
+    if (M <= 0 || M > 0x7fffffff || I <= 0 || K <= 0)
+        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: needs M >= 1 (M=%lld)", (long long)M);
     if (I % 8 || K % w8a16::kTileK)
         return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: need I %% 8 == 0 and K %% 64 == 0");
     if (x_stride < K || y_stride < I) return fail(MX_ERR_INVALID, "mx_w8a16_gateup_swiglu: row strides too short");

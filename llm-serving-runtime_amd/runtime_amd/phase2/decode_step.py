@@ -38,7 +38,8 @@ lm_head); :meth:`Int8DecodeModel.from_hf` loads the weights of an HF
 with gate and up rows interleaved in groups of 8 (``gateup_interleave``);
 where the fused epilogue does not apply, ``mx_swiglu_interleaved`` forms the
 product from the projection's split-K partials (a gate||up GEMM that splits K,
-e.g. Qwen2-0.5B at batch 16) or from its fp16 output (batch <= 4, GEMV).
+e.g. Qwen2-0.5B at batch 16) or from its fp16 output (the VALU GEMV, which
+takes batches of at most 4 rows on shapes that split).
 """
 
 from __future__ import annotations
@@ -315,7 +316,7 @@ class Int8DecodeModel:
         """act = silu(gate) * up from the interleaved gate||up weight."""
         packed, scale, n, bias = w
         ev = self._tick(timers, "gate_up")
-        if bsz > 4 and buf.splits["gate_up_chunk"] == 1:
+        if buf.splits["gate_up_chunk"] == 1:
             int8_gateup_swiglu(buf.x, packed, scale, bias, n // 2, out=buf.act)
         elif buf.splits["gate_up"] > 1:  # split over K: the SwiGLU consumer sums the partials
             int8_linear_partials(buf.x, packed, scale, n, buf.part)

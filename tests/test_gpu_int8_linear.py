@@ -269,7 +269,7 @@ def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
 WIDE_N = [20000, 24000, 28672, 32000, 64000, 128000, 128032]
 
 
-@pytest.mark.parametrize("m", [16, 32])
+@pytest.mark.parametrize("m", [1, 3, 16, 32, 64])
 @pytest.mark.parametrize("n", WIDE_N)
 def test_linear_wide_workgroup_shapes(m, n):
     from runtime_amd.phase2.int8_linear import linear_splits
@@ -285,7 +285,7 @@ def test_linear_wide_workgroup_shapes(m, n):
     np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("m,inter", [(32, 10000), (16, 12000), (32, 16000)])
+@pytest.mark.parametrize("m,inter", [(32, 10000), (16, 12000), (32, 16000), (2, 14336), (64, 14336)])
 def test_gateup_swiglu_epilogue_wide_shapes(m, inter):
     """The SwiGLU epilogue at the 5-, 6- and 8-wave unsplit shapes equals the separate ops bit for bit."""
     from runtime_amd.phase2.decode_glue import silu_mul
