@@ -266,8 +266,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 // the lanes holding gate channel c and up channel c differ by 8 and one lane swap
 // pairs them. y is [M, N/2] and receives fp16(fp16(silu(g)) * u), g and u rounded to
 // fp16 first as the unfused gate/up projections are. Needs one K split.
-template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false>
-__global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
+//
+// KW > 1 (split partials only): the workgroup's waves form KW groups of WAVES / KW that
+// walk the KW equal parts of the split's k-range side by side, each with its own x
+// staging; their accumulators are summed in LDS (part 0 first) before the one partial of
+// the split is written. The host requires KT % (KS * KW) == 0, so every group takes the
+// same number of steps and meets every barrier.
+// Waves per SIMD the plain 4-wave, MT <= 2 instances must fit: left free the compiler uses
+// 226 VGPRs (2 waves per SIMD), so a 768-workgroup launch (qkv at M=32) ran in 1.5 rounds;
+// at 3 it takes 166 VGPRs without spills and one round (qkv 12.5 -> 10.3 us on MI355X).
+#ifndef MX_GEMM_MIN_WAVES
+#define MX_GEMM_MIN_WAVES 3
+#endif
+template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false, int KW = 1>
+__global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && KW == 1) ? MX_GEMM_MIN_WAVES : 1) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
                                                                const uint16_t* __restrict__ bias,
@@ -275,28 +287,33 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
                                                                float* __restrict__ partial) {
     constexpr int ROWS = MT * 16;
     constexpr int RS = kTileK + 8;  // LDS row stride (halfs): 144 bytes, rows start 4 banks apart
+    constexpr int WN = WAVES / KW;  // waves per k part, each owning NPW n-tiles
+    static_assert(WN * KW == WAVES && (KW == 1 || !GU), "k parts split only partial launches");
     constexpr int XCH = ROWS * 8;   // 16-byte chunks of one x k-tile
-    constexpr int XC = (XCH + WAVES * 64 - 1) / (WAVES * 64);
-    __shared__ __attribute__((aligned(16))) _Float16 xl[2][ROWS * RS];
+    constexpr int XC = (XCH + WN * 64 - 1) / (WN * 64);
+    __shared__ __attribute__((aligned(16))) _Float16 xl[KW][2][ROWS * RS];
 
     const int ks = blockIdx.y, KS = gridDim.y;
-    const int kt_lo = (int)((int64_t)ks * KT / KS);
-    const int nj = (int)((int64_t)(ks + 1) * KT / KS) - kt_lo;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kw = wave / WN, wn = wave - kw * WN;
+    const int kt_split = (int)((int64_t)ks * KT / KS);
+    const int nj = ((int)((int64_t)(ks + 1) * KT / KS) - kt_split) / KW;
+    const int kt_lo = kt_split + kw * nj;
+    const int ltid = tid - kw * WN * 64;  // thread index within the k part
     const int lane = tid & 63;
     const int g = lane >> 4, r = lane & 15;
-    const int nt_w = (blockIdx.x * WAVES + wave) * NPW;
+    const int nt_w = (blockIdx.x * WN + wn) * NPW;
     const bool valid = nt_w < NT;                 // NT % NPW == 0: a wave is all in or all out
     const int nt_c = valid ? nt_w : NT - NPW;     // out-of-range waves load (and drop) the last tiles
     const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt_c * 64;  // tile (nt_c + p, kt): + (kt*NT + p)*64
 
-    // x chunks of this thread: chunk c = tid + u*WAVES*64 (wrapped when the tile has
+    // x chunks of this thread: chunk c = ltid + u*WN*64 (wrapped when the tile has
     // fewer chunks than threads; the duplicate writes store identical bytes).
     int xsrc[XC], xdst[XC];
 #pragma unroll
     for (int u = 0; u < XC; ++u) {
-        const int c = (tid + u * WAVES * 64) % XCH;
+        const int c = (ltid + u * WN * 64) % XCH;
         const int row = c / 8, col = (c % 8) * 8;
         const int rc = row < M ? row : M - 1;
         xsrc[u] = (int)(rc * xs) + col;
@@ -331,7 +348,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
     // it was read; every wave finished that read before the barrier in between.
     int step = 0;
     auto compute = [&](const St& st) {
-        _Float16* buf = xl[step & 1];
+        _Float16* buf = xl[kw][step & 1];
 #pragma unroll
         for (int u = 0; u < XC; ++u) {
             if (SW) {
@@ -393,6 +410,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_mfma_kernel(const uint16_t* _
             }
         return;
     }
+    if constexpr (KW > 1) {
+        // Parts 1.. hand their accumulators to part 0 through LDS; every wave reaches this
+        // barrier (out-of-range waves too) before any of them leaves.
+        __shared__ float4v red[KW - 1][WN][NPW][MT][64];
+        if (kw > 0) {
+#pragma unroll
+            for (int p = 0; p < NPW; ++p)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) red[kw - 1][wn][p][mt][lane] = acc[p][mt];
+        }
+        __syncthreads();
+        if (kw > 0) return;
+#pragma unroll
+        for (int q = 0; q < KW - 1; ++q)
+#pragma unroll
+            for (int p = 0; p < NPW; ++p)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) acc[p][mt] += red[q][wn][p][mt][lane];
+    }
     if (!valid) return;
 #pragma unroll
     for (int p = 0; p < NPW; ++p) {
@@ -453,12 +489,24 @@ constexpr int mt_for(int M) {
 // Launch plan for one chunk of at most kMaxRows rows.
 struct Plan {
     bool valu;
-    int MT, KS;
+    int MT, KS;  // KS: partials written (k ranges of the launch / KW)
+    int KW;      // k parts per workgroup, summed in LDS
 };
 
-// K splits for the MFMA kernel: none when the n-groups alone fill the chip,
-// else the smallest power of two that gives kSplitGrid workgroups (measured at
-// M=32 on Llama-3-8B shapes: qkv and o take 8 splits, down 8, gate_up none).
+// k parts per workgroup of a split launch (M <= 64): the split's 8-wave workgroups hold
+// two k parts of 4 waves each, so a launch of the same waves writes half the partials and
+// their consumers read half as much (decode step at batch 32: o and down write 2 MB instead
+// of 4 MB; step 4.69 -> 4.66 ms on MI355X together with the occupancy bound below).
+#ifndef MX_GEMM_KPARTS
+#define MX_GEMM_KPARTS 2
+#endif
+constexpr int kKParts = MX_GEMM_KPARTS;
+
+// K ranges of the MFMA launch: none when the n-groups alone fill the chip, else the
+// smallest power of two that gives kSplitGrid 4-wave workgroups' worth of waves (at M=32
+// on the Llama-3-8B shapes: qkv, o and down 8, gate_up none). plan_for then pairs ranges
+// into k parts of one workgroup where that keeps one round: o and down write 4 partials,
+// qkv (384 groups of parts would need 1.5 rounds) writes 8.
 static int splits_for(int NT, int KT) {
     const int groups = (NT + kMfmaWaves - 1) / kMfmaWaves;
     if (groups >= kWideGrid) return 1;
@@ -470,6 +518,7 @@ static int splits_for(int NT, int KT) {
 static Plan plan_for(int M, int NT, int KT) {
     Plan pl{};
     pl.KS = 1;
+    pl.KW = 1;
     // The VALU GEMV takes M <= 4 unless the n-groups alone fill the chip: there the
     // MFMA kernel's wide workgroups stream faster even with 15 padding rows (gate||up
     // at M = 1: 33.2 us GEMV, 23 us MFMA), while split shapes keep the GEMV, which needs
@@ -481,7 +530,15 @@ static Plan plan_for(int M, int NT, int KT) {
     }
     pl.valu = false;
     pl.MT = mt_for(M);
-    pl.KS = splits_for(NT, KT);
+    const int ranges = splits_for(NT, KT);
+    // k parts only when the launch of kKParts * 4-wave workgroups stays one round at one
+    // workgroup per CU (these workgroups need more than half a CU's wave slots).
+    const int groups = ceil_div(NT, kMfmaWaves);
+    pl.KW = kKParts > 1 && pl.MT <= 4 && ranges % kKParts == 0 && ranges / kKParts > 1 && KT % ranges == 0 &&
+                    groups * (ranges / kKParts) <= kWideGrid
+                ? kKParts
+                : 1;
+    pl.KS = ranges / pl.KW;
     return pl;
 }
 
@@ -519,20 +576,26 @@ static WideShape wide_shape(int NT, bool npw1_only) {
     return WideShape{kMfmaWaves, 1};
 }
 
-template <int MT, int NPW, int WAVES, bool SW, bool GU>
+template <int MT, int NPW, int WAVES, bool SW, bool GU, int KW = 1>
 static void launch_shape(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                          uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
     constexpr int P = NPW == 1 ? mfma_depth(MT) : (NPW == 2 ? 6 : 4);
-    const int groups = ceil_div(NT, WAVES * NPW);
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, WAVES, P, SW, GU>), dim3(groups, KS), dim3(WAVES * 64), 0, st, x, xs,
-                       M, w, s, b, y, ys, KT, NT, partial);
+    const int groups = ceil_div(NT, (WAVES / KW) * NPW);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, WAVES, P, SW, GU, KW>), dim3(groups, KS), dim3(WAVES * 64), 0, st, x,
+                       xs, M, w, s, b, y, ys, KT, NT, partial);
 }
 
 // The MFMA kernel alone: KS == 1 writes fp16 y, KS > 1 writes the scaled fp32
-// partials [KS][M][N] to `partial` (no bias).
+// partials [KS][M][N] to `partial` (no bias), each from KW k parts of its workgroups.
 template <int MT, bool SW, bool GU = false>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
-                        uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
+                        uint16_t* y, int64_t ys, int NT, int KT, int KS, int KW, float* partial, hipStream_t st) {
+    if constexpr (MT <= 4 && !GU && kKParts > 1) {
+        if (KS > 1 && KW == kKParts) {
+            launch_shape<MT, 1, kMfmaWaves * kKParts, SW, GU, kKParts>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);
+            return;
+        }
+    }
     if constexpr (MT <= 4 && !SW) {
         if (KS == 1) {
             const WideShape ws = wide_shape(NT, GU);
@@ -557,15 +620,15 @@ static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, 
 
 template <bool SW = false>
 static void launch_mfma_mt(int MT, const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s,
-                           const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial,
+                           const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, int KS, int KW, float* partial,
                            hipStream_t st) {
     switch (MT) {
-        case 1: launch_mfma<1, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        case 2: launch_mfma<2, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        case 3: launch_mfma<3, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        case 4: launch_mfma<4, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        case 6: launch_mfma<6, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
-        default: launch_mfma<8, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st); break;
+        case 1: launch_mfma<1, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, KW, partial, st); break;
+        case 2: launch_mfma<2, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, KW, partial, st); break;
+        case 3: launch_mfma<3, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, KW, partial, st); break;
+        case 4: launch_mfma<4, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, KW, partial, st); break;
+        case 6: launch_mfma<6, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, KW, partial, st); break;
+        default: launch_mfma<8, SW>(x, xs, M, w, s, b, y, ys, NT, KT, KS, KW, partial, st); break;
     }
 }
 
@@ -638,7 +701,7 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
         uint16_t* yc = y + m0 * y_stride;
         w8a16::Plan pl = w8a16::plan_for(mc, NT, KT);
         // Split-K needs the caller's workspace; without enough of it run unsplit.
-        if (pl.KS > 1 && (!workspace || workspace_bytes < w8a16::workspace_for(mc, NT, KT))) pl.KS = 1;
+        if (pl.KS > 1 && (!workspace || workspace_bytes < w8a16::workspace_for(mc, NT, KT))) pl.KS = pl.KW = 1;
         if (pl.valu) {
             switch (mc) {
                 case 1: w8a16::launch_gemv<1>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
@@ -647,7 +710,7 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
                 default: w8a16::launch_gemv<4>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
             }
         } else {
-            w8a16::launch_mfma_mt(pl.MT, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, pl.KS, partial,
+            w8a16::launch_mfma_mt(pl.MT, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, pl.KS, pl.KW, partial,
                                   st);
             if (pl.KS > 1) w8a16::launch_reduce(partial, pl.KS, mc, (int)N, bias, yc, y_stride, st);
         }
@@ -684,7 +747,7 @@ extern "C" int mx_w8a16_linear_partials(const uint16_t* x, int64_t M, int64_t K,
     if (partials_bytes < (size_t)pl.KS * M * N * sizeof(float))
         return fail(MX_ERR_WORKSPACE, "mx_w8a16_linear_partials: partials need %zu bytes, got %zu",
                     (size_t)pl.KS * M * N * sizeof(float), partials_bytes);
-    w8a16::launch_mfma_mt(pl.MT, x, x_stride, (int)M, packed, scale, nullptr, nullptr, 0, NT, KT, pl.KS, partials,
+    w8a16::launch_mfma_mt(pl.MT, x, x_stride, (int)M, packed, scale, nullptr, nullptr, 0, NT, KT, pl.KS, pl.KW, partials,
                           as_stream(stream));
     return check_launch("mx_w8a16_linear_partials");
 }
@@ -718,10 +781,10 @@ extern "C" int mx_w8a16_linear_swiglu(const uint16_t* gate_up, int64_t M, int64_
         return fail(MX_ERR_ALIGNMENT, "mx_w8a16_linear_swiglu: workspace must be 16-byte aligned");
     const int NT = (int)(N / w8a16::kTileN), KT = (int)(K / w8a16::kTileK);
     w8a16::Plan pl = w8a16::plan_for((int)M, NT, KT);
-    if (pl.KS > 1 && (!workspace || workspace_bytes < w8a16::workspace_for((int)M, NT, KT))) pl.KS = 1;
+    if (pl.KS > 1 && (!workspace || workspace_bytes < w8a16::workspace_for((int)M, NT, KT))) pl.KS = pl.KW = 1;
     float* partial = static_cast<float*>(workspace);
     hipStream_t st = as_stream(stream);
-    w8a16::launch_mfma_mt<true>(pl.MT, gate_up, gu_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, pl.KS,
+    w8a16::launch_mfma_mt<true>(pl.MT, gate_up, gu_stride, (int)M, packed, scale, bias, y, y_stride, NT, KT, pl.KS, pl.KW,
                                 partial, st);
     if (pl.KS > 1) w8a16::launch_reduce(partial, pl.KS, (int)M, (int)N, bias, y, y_stride, st);
     return check_launch("mx_w8a16_linear_swiglu");
@@ -740,7 +803,7 @@ extern "C" int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t 
     if (partials_bytes < (size_t)pl.KS * M * N * sizeof(float))
         return fail(MX_ERR_WORKSPACE, "mx_w8a16_linear_partials_swiglu: partials need %zu bytes",
                     (size_t)pl.KS * M * N * sizeof(float));
-    w8a16::launch_mfma_mt<true>(pl.MT, gate_up, gu_stride, (int)M, packed, scale, nullptr, nullptr, 0, NT, KT, pl.KS,
+    w8a16::launch_mfma_mt<true>(pl.MT, gate_up, gu_stride, (int)M, packed, scale, nullptr, nullptr, 0, NT, KT, pl.KS, pl.KW,
                                 partials, as_stream(stream));
     return check_launch("mx_w8a16_linear_partials_swiglu");
 }
@@ -769,12 +832,12 @@ extern "C" int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, i
         const uint16_t* xc = x + m0 * x_stride;
         uint16_t* yc = y + m0 * y_stride;
         switch (w8a16::mt_for(mc)) {
-            case 1: w8a16::launch_mfma<1, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
-            case 2: w8a16::launch_mfma<2, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
-            case 3: w8a16::launch_mfma<3, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
-            case 4: w8a16::launch_mfma<4, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
-            case 6: w8a16::launch_mfma<6, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
-            default: w8a16::launch_mfma<8, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, nullptr, st); break;
+            case 1: w8a16::launch_mfma<1, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
+            case 2: w8a16::launch_mfma<2, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
+            case 3: w8a16::launch_mfma<3, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
+            case 4: w8a16::launch_mfma<4, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
+            case 6: w8a16::launch_mfma<6, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
+            default: w8a16::launch_mfma<8, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
         }
     }
     return check_launch("mx_w8a16_gateup_swiglu");

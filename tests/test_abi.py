@@ -49,13 +49,16 @@ def test_paged_attn_workspace_layout_is_host_computable():
     assert lib.mx_paged_attn_error_offset(4, 8, 2, 64, 8, 16, 0) % 256 == 0
     # Split-K partials when the n-groups (4 n-tiles of 16 channels each) alone would leave
     # fewer than 256 workgroups: qkv, o and down at M=32 split K 8 ways; gate_up (448
-    # groups) and the GEMV (M <= 4) do not.
-    assert lib.mx_w8a16_workspace_bytes(32, 4096, 14336) == 8 * 32 * 4096 * 4
-    assert lib.mx_w8a16_workspace_bytes(32, 4096, 4096) == 8 * 32 * 4096 * 4
+    # groups) and the GEMV (M <= 4) do not. o and down (64 groups) pair their 8 k ranges
+    # into 2 parts of one workgroup (256 workgroups, one round) and write 4 partials; qkv
+    # (96 groups: 384 paired workgroups) writes 8.
+    assert lib.mx_w8a16_workspace_bytes(32, 4096, 14336) == 4 * 32 * 4096 * 4
+    assert lib.mx_w8a16_workspace_bytes(32, 4096, 4096) == 4 * 32 * 4096 * 4
+    assert lib.mx_w8a16_workspace_bytes(32, 6144, 4096) == 8 * 32 * 6144 * 4
     assert lib.mx_w8a16_workspace_bytes(32, 28672, 4096) == 0
     assert lib.mx_w8a16_workspace_bytes(1, 4096, 14336) == 0
     assert [lib.mx_w8a16_splits(32, n, k) for n, k in ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336))] \
-        == [8, 8, 1, 8]
+        == [8, 4, 1, 4]
     # GEMV rows (M <= 4) never split; rows run in chunks of at most 128, and above one
     # chunk there is no partials entry, so splits reports 1.
     assert lib.mx_w8a16_splits(4, 4096, 4096) == 1 and lib.mx_w8a16_splits(65, 4096, 4096) == 8

@@ -187,7 +187,7 @@ def test_split_partials_sum_to_linear_output(n, k, m):
     x = torch.randn(m, k, generator=g, device="cuda").half()
     bias = (torch.randn(n, generator=g, device="cuda") * 0.1).half()
     splits = linear_splits(m, n, k)
-    assert splits == 8
+    assert splits > 1
     part = torch.full((splits * m * n,), float("nan"), dtype=torch.float32, device="cuda")
     assert int8_linear_partials(x, packed, s, n, part) == splits
     acc = bias.float().unsqueeze(0).expand(m, n).clone()
