@@ -184,7 +184,21 @@ def family_launches(model, pool, tables, seq_lens, bsz, dev) -> dict:
         return run
 
     nl = len(model.layers)
-    out["qkv"] = (lin("qkv", x_h), nl)
+    if model.uses_fused_qkv(bsz):
+        from runtime_amd.phase2.decode_glue import qkv_linear_rope_append
+
+        buf = model.buffers(bsz)
+
+        def qkv_rope():
+            # As the step runs it: the QKV projection with RoPE and the K/V append in its
+            # epilogue (it rewrites the slots at seq_lens, which the next step writes anyway).
+            for li, layer in enumerate(model.layers):
+                packed, scale, _, bias = layer.qkv
+                qkv_linear_rope_append(x_h, packed, scale, bias, model.rope, seq_lens, buf.q, pool.k_layer_view(li),
+                                       pool.v_layer_view(li), tables, s.heads, s.kv_heads, err=buf.err)
+        out["qkv"] = (qkv_rope, nl)
+    else:
+        out["qkv"] = (lin("qkv", x_h), nl)
     out["o"] = (lin("o", x_a), nl)
     buf = model.buffers(bsz)
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 7
+#define MX_ABI_VERSION 8
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -232,6 +232,26 @@ int mx_qkv_rope_append_splits(const float* partials, int32_t splits, const uint1
                               int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
                               int32_t block_size, int32_t num_pool_blocks, int32_t* err, int32_t* lens_out,
                               void* stream);
+
+/* The QKV projection and mx_qkv_rope_append_splits in one launch, for the
+ * decode step's first two kernels per layer: q = the rotated q heads of
+ * x[M, K] W^T (+ bias) (W the packed fused-QKV weight, N = (Hq + 2*Hkv) * D
+ * rows in the order q, k, v), k rotated and v appended at position
+ * positions[m], with everything else (q_out layout, pool slots, errors,
+ * lens_out) as in mx_qkv_rope_append. The result is bit for bit that of
+ * mx_w8a16_linear_partials followed by mx_qkv_rope_append_splits whenever
+ * mx_w8a16_splits(M, N, K) == 8 (the decode step's qkv at 5 <= M <= 32 on the
+ * Llama-3-8B shape): each of the kernel's 8 waves accumulates one of those
+ * split ranges. Replaces the HF q/k/v projections, apply_rotary_pos_emb and
+ * BlockPagedBatchLayer.update's write (worker_server.py:771-775,
+ * paged_kv_cache.py:121-157). 1 <= M <= 32; D in {64, 128}; K % 64 == 0;
+ * M > 32 returns MX_ERR_UNSUPPORTED (use the two-launch path). */
+int mx_w8a16_qkv_rope_append(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
+                             const uint16_t* scale, const uint16_t* bias, int32_t Hq, int32_t Hkv, int32_t D,
+                             const float* rope, int32_t max_pos, const int32_t* positions, uint16_t* q_out,
+                             int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
+                             const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, int32_t block_size,
+                             int32_t num_pool_blocks, int32_t* err, int32_t* lens_out, void* stream);
 
 /* h = residual ? fp16(x + residual) : x;  residual_out (if not NULL) = h;
  * out = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * weight), per row of H

@@ -7,17 +7,12 @@
 // Every kernel is HBM/latency bound element-wise work: one thread per 16-byte chunk,
 // 128-bit loads and stores, no LDS except the RMSNorm row reduction.
 #include "common.h"
+#include "glue_common.h"
 
 namespace mx {
 namespace glue {
 
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
-
-__device__ __forceinline__ half8v as_h8(uint4 v) { return __builtin_bit_cast(half8v, v); }
-__device__ __forceinline__ uint4 as_u4(half8v v) { return __builtin_bit_cast(uint4, v); }
 
 // Linear output element(s) from split-K partials: fp16(bias[col] + sum_s part[s*split_stride + off]),
 // the value mx_w8a16_linear would have written (its reduce adds the bias, then the splits in order).
@@ -53,20 +48,7 @@ __device__ __forceinline__ void sum_splits(const float* part, int splits, int64_
         }
     }
 #pragma unroll
-    for (int e = 0; e < E; ++e) out[e] = (_Float16)acc[e];
-}
-
-// Where token `pos` of row `b` lives in the pool, or -1 when its logical block is past the
-// table or its physical id is outside the pool (the token is then skipped and flagged).
-__device__ __forceinline__ int64_t slot_offset(const int32_t* bt, int64_t bt_sb, int max_blocks, int b, int pos,
-                                               int bs, int num_pool_blocks, int64_t sblk, int64_t shead, int head,
-                                               int D) {
-    if (pos < 0) return -1;
-    const int lb = pos / bs;
-    if (lb >= max_blocks) return -1;
-    const int phys = bt[(int64_t)b * bt_sb + lb];
-    if (phys < 0 || phys >= num_pool_blocks) return -1;
-    return (int64_t)phys * sblk + (int64_t)head * shead + (int64_t)(pos - lb * bs) * D;
+    for (int e = 0; e < E; ++e) out[e] = (_Float16)pin_f32(acc[e]);
 }
 
 struct AppendParams {
@@ -172,10 +154,9 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendPar
             const float2* cs = p.rope + (int64_t)pos * half + j;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float2 f = cs[e];
-                const float a = (float)x1[e], bb = (float)x2[e];
-                o1[e] = (_Float16)(a * f.x - bb * f.y);
-                o2[e] = (_Float16)(bb * f.x + a * f.y);
+                const half2v o = rope_rotate(x1[e], x2[e], cs[e]);
+                o1[e] = o[0];
+                o2[e] = o[1];
             }
         } else if (p.err && c == 0) {
             atomicOr(p.err, 2);

@@ -22,44 +22,10 @@
 // meet in LDS. The MFMA GEMM (M > 4) splits the other way, see gemm_mfma_kernel.
 // Both apply the per-channel scale and the bias once, in the epilogue.
 #include "common.h"
+#include "w8a16_tiles.h"
 
 namespace mx {
 namespace w8a16 {
-
-constexpr int kTileN = 16;
-constexpr int kTileK = 64;
-constexpr uint32_t kMagic = 0x64646464u;
-constexpr uint32_t kSelLo = 0x04010400u;  // bytes 0,1 -> fp16 pair (0x64:b0, 0x64:b1)
-constexpr uint32_t kSelHi = 0x04030402u;  // bytes 2,3 -> fp16 pair (0x64:b2, 0x64:b3)
-
-struct U32x4 {
-    uint32_t a, b, c, d;
-};
-
-// 8 biased bytes (two dwords) -> 8 exact fp16 weights.
-__device__ __forceinline__ half8v dequant8(uint32_t d0, uint32_t d1) {
-    const U32x4 raw{__builtin_amdgcn_perm(kMagic, d0, kSelLo), __builtin_amdgcn_perm(kMagic, d0, kSelHi),
-                    __builtin_amdgcn_perm(kMagic, d1, kSelLo), __builtin_amdgcn_perm(kMagic, d1, kSelHi)};
-    const half8v bias = (_Float16)(-1152.0f);
-    return __builtin_bit_cast(half8v, raw) + bias;
-}
-
-__device__ __forceinline__ half8v load_half8(const _Float16* p) {
-    return __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(p));
-}
-
-__device__ __forceinline__ float dot8(half8v a, half8v b, float acc) {
-    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 0, 1), __builtin_shufflevector(b, b, 0, 1), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 2, 3), __builtin_shufflevector(b, b, 2, 3), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 4, 5), __builtin_shufflevector(b, b, 4, 5), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 6, 7), __builtin_shufflevector(b, b, 6, 7), acc, false);
-    return acc;
-}
-
-__device__ __forceinline__ uint16_t f2h_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
-__device__ __forceinline__ float h2f(const uint16_t* p, int64_t i) {
-    return (float)reinterpret_cast<const _Float16*>(p)[i];
-}
 
 // ---------------------------------------------------------------------------
 // Quantize: one workgroup of 256 threads per output channel.
@@ -123,43 +89,6 @@ __global__ __launch_bounds__(256) void pack_kernel(const int8_t* __restrict__ q,
     const uint4 dst{src.x ^ flip, src.y ^ flip, src.z ^ flip, src.w ^ flip};
     *reinterpret_cast<uint4*>(packed + idx * 16) = dst;
 }
-
-// ---------------------------------------------------------------------------
-// Per-wave software pipeline. A wave owns the k-tiles kt = wave + j*WAVES,
-// j < nj, of the workgroup's n-tiles. Stage s of P holds the weight tiles and
-// the x fragments of one k-tile; the loads for k-tile j+P are issued as soon
-// as k-tile j has been consumed, so P k-tiles (P*NPW KiB of weights plus their
-// x fragments) stay in flight per wave.
-//
-// Every load is issued unconditionally: past the last k-tile the index is
-// clamped (the reload hits L2), and x rows past M read row M-1 (MFMA rows are
-// independent, those C rows are discarded). With no loads under a branch the
-// compiler can wait for exactly the oldest stage (s_waitcnt vmcnt(N)) instead
-// of draining every load in flight. Addresses are a wave-uniform base plus a
-// fixed 32-bit lane offset.
-// ---------------------------------------------------------------------------
-// The stage loop shared by both kernels. Prologue: stages 0..P-1 (indices
-// clamped when nj < P). Full rounds issue the loads of tile j+P right after
-// tile j is consumed, unconditionally. The last round and a half issue only
-// the loads still in range, then drain.
-#define PIPELINE_BODY(P, nj, st, load, COMPUTE)                  \
-    _Pragma("unroll") for (int s = 0; s < P; ++s) load(s, st[s]); \
-    int j0 = 0;                                                     \
-    for (; j0 + 2 * P <= nj; j0 += P) {                             \
-        _Pragma("unroll") for (int s = 0; s < P; ++s) {             \
-            COMPUTE;                                                \
-            load(j0 + s + P, st[s]);                                \
-        }                                                           \
-    }                                                               \
-    _Pragma("unroll") for (int s = 0; s < P; ++s) {                 \
-        if (j0 + s < nj) {                                          \
-            COMPUTE;                                                \
-            if (j0 + s + P < nj) load(j0 + s + P, st[s]);           \
-        }                                                           \
-    }                                                               \
-    _Pragma("unroll") for (int s = 0; s < P; ++s) {                 \
-        if (j0 + P + s < nj) { COMPUTE; }                           \
-    }
 
 template <int NPW, int XV>
 struct Stage {
@@ -456,7 +385,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
     const int m = (int)(idx / N), n = (int)(idx % N);
     float v = bias ? h2f(bias, n) : 0.0f;
     for (int k = 0; k < KS; ++k) v += partial[(int64_t)k * M * N + idx];
-    y[(int64_t)m * ys + n] = f2h_bits(v);
+    y[(int64_t)m * ys + n] = f2h_bits(pin_f32(v));
 }
 
 // Largest M handled by the VALU GEMV; above it the MFMA kernel runs.

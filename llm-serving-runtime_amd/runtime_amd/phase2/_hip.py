@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -70,6 +70,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_p, _i32, _p, _i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _i32, _i32,
          _p, _p, _p],
+    ),
+    "mx_w8a16_qkv_rope_append": (
+        ctypes.c_int,
+        [_p, _i64, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64,
+         _i32, _i32, _i32, _p, _p, _p],
     ),
     "mx_add_rmsnorm_splits": (
         ctypes.c_int,

@@ -177,6 +177,46 @@ def qkv_rope_append_splits(partials: torch.Tensor, splits: int, bias: torch.Tens
     return q_out
 
 
+QKV_ROPE_MAX_ROWS = 32
+
+
+def qkv_linear_rope_append(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+                           rope: torch.Tensor, positions: torch.Tensor, q_out: torch.Tensor, k_layer: torch.Tensor,
+                           v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,
+                           err: torch.Tensor | None = None, lens_out: torch.Tensor | None = None) -> torch.Tensor:
+    """The int8 QKV projection of ``x [B, K]`` (packed fused-QKV weight, ``B <= 32``) and
+    :func:`qkv_rope_append_splits` in one launch (``mx_w8a16_qkv_rope_append``)."""
+    _hip.require_device_tensor(x, "x")
+    dev = x.device
+    nb, hkv, bs, d = k_layer.shape
+    x2 = _rows16(x.reshape(-1, x.shape[-1]))
+    b, k = (int(v) for v in x2.shape)
+    if hkv != num_kv_heads:
+        raise ValueError("num_kv_heads does not match the pool")
+    if not 1 <= b <= QKV_ROPE_MAX_ROWS:
+        raise ValueError(f"the fused QKV + RoPE launch takes 1..{QKV_ROPE_MAX_ROWS} rows, got {b}")
+    if scale.numel() != (num_heads + 2 * num_kv_heads) * d:
+        raise ValueError("scale must have (Hq + 2 Hkv) * D entries")
+    if rope.dtype != torch.float32 or rope.dim() != 3 or rope.shape[1:] != (d // 2, 2) or not rope.is_contiguous():
+        raise ValueError("rope must be a contiguous fp32 [max_pos, D/2, 2] table")
+    tables = _i32(block_tables, dev)
+    pos = _i32(positions.reshape(-1), dev)
+    if tables.shape[0] != b or pos.shape[0] != b:
+        raise ValueError("batch dimension mismatch")
+    q2 = q_out.reshape(b, -1)
+    if q2.data_ptr() != q_out.data_ptr() or q2.stride(-1) != 1 or q2.shape[-1] != num_heads * d:
+        raise ValueError("q_out must be a row-major [B, Hq * D] buffer")
+    lib = _hip.load()
+    _hip.check(lib.mx_w8a16_qkv_rope_append(
+        x2.data_ptr(), b, k, x2.stride(0), packed.data_ptr(), scale.data_ptr(),
+        bias.data_ptr() if bias is not None else None, num_heads, num_kv_heads, d, rope.data_ptr(),
+        int(rope.shape[0]), pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(), v_layer.data_ptr(),
+        k_layer.stride(0), k_layer.stride(1), tables.data_ptr(), tables.stride(0), int(tables.shape[1]), bs, nb,
+        err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b), _hip.stream_handle(dev)),
+        "mx_w8a16_qkv_rope_append")
+    return q_out
+
+
 def add_rmsnorm_splits(partials: torch.Tensor, splits: int, bias: torch.Tensor | None, weight: torch.Tensor,
                        eps: float, out: torch.Tensor, residual: torch.Tensor | None = None,
                        residual_out: torch.Tensor | None = None) -> torch.Tensor:

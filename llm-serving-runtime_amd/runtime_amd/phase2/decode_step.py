@@ -11,8 +11,9 @@ current stream:
 
     x = RMSNorm(h)                         mx_add_rmsnorm (fused with the residual add
                                            of the previous layer's MLP)
-    qkv = x Wqkv^T (+b)                    mx_w8a16_linear
-    q, K/V slot <- RoPE(qkv), v            mx_qkv_rope_append
+    qkv = x Wqkv^T (+b)                    mx_w8a16_qkv_rope_append (one launch for
+    q, K/V slot <- RoPE(qkv), v            both lines at batch <= 32; else
+                                           mx_w8a16_linear + mx_qkv_rope_append)
     a = paged_attention(q, pool)           mx_paged_attn_decode
     h += a Wo^T;  x = RMSNorm(h)           mx_w8a16_linear, mx_add_rmsnorm
     a = silu(x Wg^T) * (x Wu^T)            mx_w8a16_gateup_swiglu (gate and up rows
@@ -49,8 +50,8 @@ from dataclasses import dataclass
 
 import torch
 
-from .decode_glue import (add_rmsnorm, add_rmsnorm_splits, argmax_rows, qkv_rope_append, qkv_rope_append_splits,
-                          rope_table, swiglu_interleaved)
+from .decode_glue import (QKV_ROPE_MAX_ROWS, add_rmsnorm, add_rmsnorm_splits, argmax_rows, qkv_linear_rope_append,
+                          qkv_rope_append, qkv_rope_append_splits, rope_table, swiglu_interleaved)
 from .int8_linear import (gateup_interleave, int8_gateup_swiglu, int8_linear,
                           int8_linear_partials, linear_splits, pack_weight, quantize_weight)
 from .paged_attention_hip import _decode as _paged_decode
@@ -134,6 +135,9 @@ class Int8DecodeModel:
         self.device = torch.device(device)
         self.n_layers = layers if layers is not None else shape.layers
         self.rope = rope_table(max_positions, shape.head_dim, shape.rope_theta, self.device)
+        # QKV projection + RoPE + append as one launch where it applies (uses_fused_qkv);
+        # False keeps the two-launch path (split partials or fp16 rows, then the RoPE kernel).
+        self.fuse_qkv_rope = True
         self._buffers: dict[int, _Buffers] = {}
         self.layers: list[_Layer] = []
         if not init:
@@ -274,7 +278,13 @@ class Int8DecodeModel:
             lens_out = buf.attn_lens if li == 0 else None
             k_layer = pool.k_layer_view(li)
             v_layer = pool.v_layer_view(li)
-            if sp["qkv"] > 1:
+            if self.uses_fused_qkv(bsz):
+                ev = self._tick(timers, "qkv")
+                packed, scale, _, bias = layer.qkv
+                qkv_linear_rope_append(buf.x, packed, scale, bias, self.rope, seq_lens, buf.q, k_layer, v_layer,
+                                       block_tables, s.heads, s.kv_heads, err=buf.err, lens_out=lens_out)
+                self._tock(timers, "qkv", ev)
+            elif sp["qkv"] > 1:
                 self._partials(buf.x, layer.qkv, buf.part, timers, "qkv")
                 qkv_rope_append_splits(buf.part, sp["qkv"], layer.qkv[3], self.rope, seq_lens, buf.q, k_layer,
                                        v_layer, block_tables, s.heads, s.kv_heads, err=buf.err, lens_out=lens_out)
@@ -302,6 +312,10 @@ class Int8DecodeModel:
         self._lin(buf.x, self.lm_head, buf.logits, timers, "lm_head")
         nxt = argmax_rows(buf.logits, out=buf.next if out is None else out, seq_lens=seq_lens)
         return (nxt, buf.logits) if return_logits else nxt
+
+    def uses_fused_qkv(self, bsz: int) -> bool:
+        """Whether the step's QKV projection and RoPE + append run as one launch at this batch."""
+        return self.fuse_qkv_rope and bsz <= QKV_ROPE_MAX_ROWS and self.shape.head_dim in (64, 128)
 
     def _norm_after_down(self, buf: _Buffers, weight: torch.Tensor) -> None:
         """x = RMSNorm(h + down output) * weight; h updated in place."""
