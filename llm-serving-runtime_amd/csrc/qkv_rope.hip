@@ -128,6 +128,27 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
         PIPELINE_BODY(kDepth, nj, st, load, compute(st[s]))
     }
 
+    // Rotation factors and pool slots of the epilogue thread's rows, loaded before the
+    // barrier so that they arrive while the workgroup waits for its slowest wave.
+    const int c = jt * kTileN + r;  // dim of the pair's first element within the head
+    float2 cs[4];
+    int64_t dst[4];
+    if (epi) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = (tid >> 6) * 16 + 4 * g + i;
+            const int ps = pos[i];
+            const bool live = m < p.M && ps >= 0 && ps < p.max_pos;
+            cs[i] = live && head < p.Hq + p.Hkv ? p.rope[(int64_t)ps * (D / 2) + c] : float2{0.0f, 0.0f};
+            dst[i] = -1;
+            if (live && head >= p.Hq) {
+                const int kvh = head < p.Hq + p.Hkv ? head - p.Hq : head - p.Hq - p.Hkv;
+                dst[i] = glue::slot_offset(p.bt, p.bt_sb, p.max_blocks, m, ps, p.bs, p.num_pool_blocks, p.sblk,
+                                           p.shead, kvh, D);
+            }
+        }
+    }
+
     // Scaled accumulators (the split partials) to LDS; acc[t][mt][i] is row
     // 16 mt + 4 g + i, column 16 nt + r of tile t.
     const int n0 = nt0 * kTileN + r, n1 = nt1 * kTileN + r;
@@ -163,7 +184,6 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
             s1[i] += v1[i];
         }
     }
-    const int c = jt * kTileN + r;  // dim of the pair's first element within the head
     const bool flag_lane = r == 0 && jt == 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -175,7 +195,7 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
         if (pp == 0 && r == 0 && p.lens_out) p.lens_out[m] = ps + 1;
         if (head < p.Hq + p.Hkv) {
             half2v o = {(_Float16)0.0f, (_Float16)0.0f};
-            if (pos_ok) o = glue::rope_rotate(x1, x2, p.rope[(int64_t)ps * (D / 2) + c]);
+            if (pos_ok) o = glue::rope_rotate(x1, x2, cs[i]);
             else if (p.err && flag_lane) atomicOr(p.err, 2);
             if (head < p.Hq) {
                 _Float16* q = reinterpret_cast<_Float16*>(p.q_out) + (int64_t)m * p.q_stride + (int64_t)head * D + c;
@@ -184,21 +204,16 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
                 continue;
             }
             if (!pos_ok) continue;
-            const int64_t dst = glue::slot_offset(p.bt, p.bt_sb, p.max_blocks, m, ps, p.bs, p.num_pool_blocks, p.sblk,
-                                                  p.shead, head - p.Hq, D);
-            if (dst < 0) {
+            if (dst[i] < 0) {
                 if (p.err && flag_lane) atomicOr(p.err, 1);
                 continue;
             }
-            _Float16* k = reinterpret_cast<_Float16*>(p.k_pool) + dst + c;
+            _Float16* k = reinterpret_cast<_Float16*>(p.k_pool) + dst[i] + c;
             k[0] = o[0];
             k[D / 2] = o[1];
         } else {
-            if (ps >= p.max_pos) continue;  // flagged by the q/k heads of the row
-            const int64_t dst = glue::slot_offset(p.bt, p.bt_sb, p.max_blocks, m, ps, p.bs, p.num_pool_blocks, p.sblk,
-                                                  p.shead, head - p.Hq - p.Hkv, D);
-            if (dst < 0) continue;  // flagged by the k head of the row
-            _Float16* v = reinterpret_cast<_Float16*>(p.v_pool) + dst + c;
+            if (dst[i] < 0) continue;  // position or slot outside the tables: flagged by the q/k heads
+            _Float16* v = reinterpret_cast<_Float16*>(p.v_pool) + dst[i] + c;
             v[0] = x1;
             v[D / 2] = x2;
         }
