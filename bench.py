@@ -10,7 +10,7 @@ embeddings are random. Inputs are resident in HBM before timing starts.
 
 Prints ONE JSON line. ``value`` = decode tokens/s of the whole step (B tokens per
 step), timed over ``--steps`` HIP-graph replays of the step after ``--warmup``
-eager steps. ``roofline`` is for the kernel family with the most time per
+eager steps, the capture and 2 untimed replays. ``roofline`` is for the kernel family with the most time per
 step: each family's launches of one step (same inputs, same stream) are captured
 into their own graph and replayed ``--kernel-steps`` times back-to-back between
 two HIP events, which gives its average launch duration without host launch
@@ -319,6 +319,7 @@ def traffic_probe(args) -> int:
 
 
 PREFIX_GROUPS, PREFIX_TOKENS, ROTATE_EVERY = 16, 1024, 16
+GRAPH_WARMUP = 2
 
 
 def prefix_batch_bench(args) -> int:
@@ -342,7 +343,7 @@ def prefix_batch_bench(args) -> int:
     n_layers = args.layers or shape.layers
     bsz, bs = args.batch, 16
     lo, hi = 1, 8192
-    total_steps = args.warmup + args.steps + 2
+    total_steps = args.warmup + 1 + GRAPH_WARMUP + args.steps
     num_blocks = 40960
     t_setup = time.perf_counter()
     pb = PrefixBatch(batch=bsz, groups=PREFIX_GROUPS, prefix_tokens=PREFIX_TOKENS, lo=lo, hi=hi, block_size=bs,
@@ -379,31 +380,55 @@ def prefix_batch_bench(args) -> int:
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        step()
-    pb.advance(1)  # the capture ran the step once
+        step()  # recorded, not run: the lengths do not advance
+    for _ in range(GRAPH_WARMUP):  # the first replays of a new graph carry one-time costs
+        graph.replay()
+        pb.advance(1)
     torch.cuda.synchronize()
+    assert seq_lens.cpu().tolist() == pb.lens.tolist(), "device lengths diverged from the schedule"
 
     kv_token_bytes = n_layers * shape.kv_heads * shape.head_dim * 2 * 2  # K and V, every layer
-    uniq, logical, rotated = [], [], 0
+
+    def rotation(k: int) -> list[int]:
+        """Rows that finish before step k (every ROTATE_EVERY steps, one row in 8)."""
+        if k == 0 or k % ROTATE_EVERY:
+            return []
+        return [b for b in range(bsz) if b % 8 == (k // ROTATE_EVERY) % 8]
+
+    # Timed: the step graph plus the join/finish work (host schedule, table and length
+    # uploads, new tokens) every ROTATE_EVERY steps.
+    rotated = 0
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for k in range(args.steps):
-        if k and k % ROTATE_EVERY == 0:
-            epoch = k // ROTATE_EVERY
-            rows = [b for b in range(bsz) if b % 8 == epoch % 8]
+        rows = rotation(k)
+        if rows:
             pb.rotate(rows)
-            pb.upload(tables_d, seq_lens)
+            pb.upload_rows(rows, tables_d, seq_lens)
             tokens[rows] = torch.randint(0, shape.vocab, (len(rows),), generator=gt).to(dev)
             rotated += len(rows)
-        uniq.append(pb.unique_tokens(1))
-        logical.append(pb.logical_tokens(1))
         graph.replay()
         pb.advance(1)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     assert seq_lens.cpu().tolist() == pb.lens.tolist(), "device lengths diverged from the schedule"
+
+    # Byte accounting, outside the timed region: the same seeded host schedule replayed on the
+    # CPU, counting each step's K/V tokens read (logical) and stored (unique).
+    acct = PrefixBatch(batch=bsz, groups=PREFIX_GROUPS, prefix_tokens=PREFIX_TOKENS, lo=lo, hi=hi, block_size=bs,
+                       num_blocks=num_blocks, headroom=total_steps + ROTATE_EVERY, seed=0)
+    acct.advance(args.warmup + 1 + GRAPH_WARMUP)
+    uniq, logical = [], []
+    for k in range(args.steps):
+        rows = rotation(k)
+        if rows:
+            acct.rotate(rows)
+        uniq.append(acct.unique_tokens(1))
+        logical.append(acct.logical_tokens(1))
+        acct.advance(1)
+    assert acct.lens.tolist() == pb.lens.tolist()
 
     # Attention family at the final state (32 launches per step, one graph), as in the headline bench.
     s_ = model.shape
@@ -664,7 +689,7 @@ def main() -> int:
     n_layers = args.layers or shape.layers
     bsz = args.batch
     bs = 16
-    total_steps = args.warmup + args.steps + args.kernel_steps + 2
+    total_steps = args.warmup + 1 + GRAPH_WARMUP + args.steps + args.kernel_steps + 2
     lens, tables = make_contexts(bsz, args.ctx_lo, args.ctx_hi, bs, args.pool_blocks, headroom=total_steps, seed=0)
     t_setup = time.perf_counter()
     model = Int8DecodeModel(shape, device=dev, seed=0, layers=n_layers)
@@ -701,6 +726,8 @@ def main() -> int:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step()
+        for _ in range(GRAPH_WARMUP):  # untimed: the first replays of a new graph carry one-time costs
+            graph.replay()
         torch.cuda.synchronize()
 
     lens_before = seq_lens.cpu().tolist()

@@ -154,6 +154,19 @@ class PrefixBatch:
         tables_d.copy_(self.tables)
         lens_d.copy_(self.lens)
 
+    def upload_rows(self, rows: list[int], tables_d: torch.Tensor, lens_d: torch.Tensor) -> None:
+        """:meth:`upload` for the table rows in ``rows`` only (the slots :meth:`rotate` just
+        refilled); every other table row is unchanged since the last upload. All lengths are
+        copied, as the decode step advances them on the device."""
+        if rows:
+            part = torch.zeros(len(rows), self.max_blocks, dtype=torch.int32)
+            for j, b in enumerate(rows):
+                blocks = self.rows[b].blocks
+                part[j, :len(blocks)] = torch.tensor(blocks, dtype=torch.int32)
+            idx = torch.tensor(rows, dtype=torch.int64, device=tables_d.device)
+            tables_d.index_copy_(0, idx, part.to(tables_d.device))
+        lens_d.copy_(self.lens)
+
     # -- byte accounting ---------------------------------------------------------
     def logical_tokens(self, extra: int = 0) -> int:
         """K/V tokens the rows attend over (each row counts its prefix), with ``extra`` more per row."""

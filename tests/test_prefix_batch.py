@@ -93,6 +93,23 @@ def test_upload_keeps_device_tensor_addresses():
     assert torch.equal(tables_d, pb.tables) and torch.equal(lens_d, pb.lens)
 
 
+def test_upload_rows_equals_full_upload():
+    """After a rotation, rewriting only the refilled rows gives the full table; stale entries past a
+    refilled row's new blocks are cleared."""
+    pb = _batch()
+    tables_d = torch.empty(16, pb.max_blocks, dtype=torch.int32)
+    lens_d = torch.empty(16, dtype=torch.int32)
+    pb.upload(tables_d, lens_d)
+    for k in range(1, 4):
+        rows = [b for b in range(16) if b % 4 == k]
+        pb.advance(2)
+        pb.rotate(rows, lengths=[5 + 60 * j for j in range(len(rows))])
+        pb.upload_rows(rows, tables_d, lens_d)
+        assert torch.equal(tables_d, pb.tables) and torch.equal(lens_d, pb.lens)
+    pb.upload_rows([], tables_d, lens_d)
+    assert torch.equal(lens_d, pb.lens)
+
+
 def test_given_lengths():
     pb = _batch(lengths=[70 + b for b in range(16)])
     assert pb.lens.tolist() == [70 + b for b in range(16)]
