@@ -195,8 +195,13 @@ def qkv_linear_rope_append(x: torch.Tensor, packed: torch.Tensor, scale: torch.T
         raise ValueError("num_kv_heads does not match the pool")
     if not 1 <= b <= QKV_ROPE_MAX_ROWS:
         raise ValueError(f"the fused QKV + RoPE launch takes 1..{QKV_ROPE_MAX_ROWS} rows, got {b}")
-    if scale.numel() != (num_heads + 2 * num_kv_heads) * d:
-        raise ValueError("scale must have (Hq + 2 Hkv) * D entries")
+    n = (num_heads + 2 * num_kv_heads) * d
+    if scale.numel() != n or (bias is not None and bias.numel() != n):
+        raise ValueError("scale (and bias) must have (Hq + 2 Hkv) * D entries")
+    if packed.dtype != torch.uint8 or packed.numel() != n * k or not packed.is_contiguous():
+        raise ValueError(f"packed must be the contiguous uint8 tile layout of a [{n}, {k}] weight")
+    for t, name in ((packed, "packed"), (scale, "scale")) + (((bias, "bias"),) if bias is not None else ()):
+        _hip.require_device_tensor(t, name)
     if rope.dtype != torch.float32 or rope.dim() != 3 or rope.shape[1:] != (d // 2, 2) or not rope.is_contiguous():
         raise ValueError("rope must be a contiguous fp32 [max_pos, D/2, 2] table")
     tables = _i32(block_tables, dev)

@@ -15,6 +15,8 @@ AWQ load: it swaps the decoder-layer projections of an HF model in place.
 
 from __future__ import annotations
 
+import threading
+
 import torch
 from torch import nn
 
@@ -27,19 +29,26 @@ DEFAULT_TARGETS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj
 
 # Split-K partials of mx_w8a16_linear: one growable buffer per device, shared by
 # every call on that device (calls on one stream are serialised; concurrent
-# streams must not use this module's cache at the same time).
+# streams must not use this module's cache at the same time). A buffer that is
+# outgrown stays allocated: graphs captured while it was current keep its address.
 _workspaces: dict[torch.device, torch.Tensor] = {}
+_retired: list[torch.Tensor] = []
+_ws_lock = threading.Lock()
 
 
 def _workspace(device: torch.device, nbytes: int) -> tuple[int | None, int]:
     if nbytes == 0:
         return None, 0
-    ws = _workspaces.get(device)
-    if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("int8 linear workspace must be sized before graph capture; run the step once eagerly")
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[device] = ws
+    with _ws_lock:
+        ws = _workspaces.get(device)
+        if ws is None or ws.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("int8 linear workspace must be sized before graph capture; "
+                                   "run the step once eagerly")
+            if ws is not None:
+                _retired.append(ws)
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _workspaces[device] = ws
     return ws.data_ptr(), ws.numel()
 
 

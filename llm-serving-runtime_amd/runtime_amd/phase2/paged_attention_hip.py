@@ -111,7 +111,9 @@ def workspace_error_flag(device: torch.device | None = None) -> int:
     """OR of the error words of all cached workspaces (one host sync). Nonzero: an
     out-of-range block id was met and skipped since the workspace was created."""
     flag = 0
-    for key, ws in _workspaces.items():
+    with _ws_lock:
+        cached = list(_workspaces.items())
+    for key, ws in cached:
         if device is not None and key[0] != device:
             continue
         off = int(_hip.load().mx_paged_attn_error_offset(*key[1:]))

@@ -343,3 +343,33 @@ def test_swiglu_interleaved_rejects_bad_arguments():
         swiglu_interleaved(y, 16, partials=torch.zeros(8, device="cuda"), splits=2, rows=4)  # both inputs
     with pytest.raises(ValueError):
         swiglu_interleaved(None, 16, partials=torch.zeros(8, device="cuda"), splits=2, rows=4)  # too small
+
+
+def test_workspace_growth_keeps_captured_graphs_valid():
+    """A graph captured while the split-K workspace was small still replays correctly after a larger
+    shape has grown the workspace: the outgrown buffer stays allocated, so nothing else reuses the
+    address the graph holds (checked over several replays with allocator churn in between)."""
+    from runtime_amd.phase2.int8_linear import int8_linear, linear_splits, pack_weight, quantize_weight
+
+    g = torch.Generator(device="cuda").manual_seed(91)
+    n, k, m = 4096, 4096, 32
+    assert linear_splits(m, n, k) > 1
+    q, s = quantize_weight(torch.randn(n, k, generator=g, device="cuda") * 0.02)
+    pk = pack_weight(q)
+    x = torch.randn(m, k, generator=g, device="cuda").half()
+    want = int8_linear(x, pk, s, None, n)
+    y = torch.empty_like(want)
+    int8_linear(x, pk, s, None, n, out=y)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        int8_linear(x, pk, s, None, n, out=y)
+    # A larger split shape grows the workspace past the captured one.
+    q2, s2 = quantize_weight(torch.randn(n, 14336, generator=g, device="cuda") * 0.02)
+    int8_linear(torch.randn(128, 14336, generator=g, device="cuda").half(), pack_weight(q2), s2, None, n)
+    for _ in range(3):
+        junk = [torch.full((1 << 20,), float("nan"), device="cuda") for _ in range(8)]
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want)
+        del junk

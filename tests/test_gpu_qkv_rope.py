@@ -169,12 +169,18 @@ def test_fused_positions_outside_tables_and_lengths():
         assert _ulps(a, b) <= 2 if a.dtype == torch.float16 else torch.equal(a, b)
 
 
-def test_fused_refuses_more_than_32_rows():
+def test_fused_rejects_bad_arguments():
+    """More than 32 rows, a packed weight or bias of the wrong size: ValueError before any launch."""
     hq, hkv, d, hidden = 4, 2, 64, 256
     c = _setup(hq, hkv, d, hidden, 33, False, seed=40)
     k, v = _pool_layer(c["nb"], hkv, c["bs"], d, seed=7)
     with pytest.raises(ValueError):
         _fused(c, hq, hkv, d, k, v)
+    c = _setup(hq, hkv, d, hidden, 4, False, seed=41)
+    for key, bad in (("packed", c["packed"][:-64]), ("bias", torch.zeros(c["n"] - 16, dtype=torch.float16,
+                                                                          device=DEV))):
+        with pytest.raises(ValueError):
+            _fused({**c, key: bad}, hq, hkv, d, k, v)
 
 
 @pytest.mark.timeout(600)
