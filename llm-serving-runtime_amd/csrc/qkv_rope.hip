@@ -95,8 +95,8 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
     };
     auto load = [&](int j, St& st) {
         const int kt = kt_lo + (j < nj ? j : nj - 1);
-        st.w[0] = wb[((int64_t)kt * p.NT + nt0) * 64 + lane];
-        st.w[1] = wb[((int64_t)kt * p.NT + nt1) * 64 + lane];
+        st.w[0] = w8a16::load_wtile(wb + ((int64_t)kt * p.NT + nt0) * 64 + lane);
+        st.w[1] = w8a16::load_wtile(wb + ((int64_t)kt * p.NT + nt1) * 64 + lane);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const uint4* src = reinterpret_cast<const uint4*>(xb + xoff[mt] + kt * kTileK);

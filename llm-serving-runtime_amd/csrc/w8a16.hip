@@ -116,7 +116,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 
     auto load = [&](int j, Stage<1, 2 * M>& st) {
         const int kt = wave + (j < nj ? j : nj - 1) * WAVES;
-        st.w[0] = (wbase + (int64_t)kt * NT * 64)[lane];
+        st.w[0] = load_wtile(wbase + (int64_t)kt * NT * 64 + lane);
         const _Float16* xk = xbase + kt * kTileK;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && K
     auto load = [&](int j, St& st) {
         const int kt = kt_lo + (j < nj ? j : nj - 1);
 #pragma unroll
-        for (int p = 0; p < NPW; ++p) st.w[p] = (wbase + ((int64_t)kt * NT + p) * 64)[lane];
+        for (int p = 0; p < NPW; ++p) st.w[p] = load_wtile(wbase + ((int64_t)kt * NT + p) * 64 + lane);
 #pragma unroll
         for (int u = 0; u < XC; ++u) {
             st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
