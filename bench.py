@@ -60,6 +60,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="REPS",
                     help="instead of the bench: REPS rounds of the step's paged-attention calls (one per layer, "
                          "bench workload) and a 1 GiB copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--stream-shared-kv", action="store_true",
+                    help="prefix-batch: read the aliased K/V with streaming loads (no MX_PA_SHARED_BLOCKS), "
+                         "for comparison")
     args = ap.parse_args()
     if args.batch is None:
         args.batch = 128 if args.workload == "prefix-batch" else 32
@@ -349,6 +352,7 @@ def prefix_batch_bench(args) -> int:
     pb = PrefixBatch(batch=bsz, groups=PREFIX_GROUPS, prefix_tokens=PREFIX_TOKENS, lo=lo, hi=hi, block_size=bs,
                      num_blocks=num_blocks, headroom=total_steps + ROTATE_EVERY, seed=0)
     model = Int8DecodeModel(shape, device=dev, seed=0, layers=n_layers)
+    model.shared_kv_blocks = not args.stream_shared_kv  # rows of a group alias the prefix blocks
     pool = GpuKVBlockPool(num_blocks=num_blocks, block_size_tokens=bs, num_layers=n_layers,
                           num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16, device=dev)
     pool._ensure_pools()
@@ -437,7 +441,8 @@ def prefix_batch_bench(args) -> int:
 
     def attn():
         for li in range(n_layers):
-            _decode(q, pool.k_layer_view(li), pool.v_layer_view(li), tables_d, lens_attn, s_.head_dim**-0.5, s_.group)
+            _decode(q, pool.k_layer_view(li), pool.v_layer_view(li), tables_d, lens_attn, s_.head_dim**-0.5, s_.group,
+                    shared_blocks=model.shared_kv_blocks)
     attn_s = time_family(attn, n_layers, args.kernel_steps)
     # One attention launch (one layer) reads these K/V bytes at the final state.
     final_uniq = pb.unique_tokens(1) * shape.kv_heads * shape.head_dim * 2 * 2

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 8
+#define MX_ABI_VERSION 9
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -158,11 +158,20 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  *      the value the workspace was sized for. A
  *      second, small kernel on the same stream merges the ranges of a
  *      sequence that more than one wave touched.
+ * flags: 0 or MX_PA_SHARED_BLOCKS. Without it K and V are read with the
+ *      streaming (non-temporal) cache policy, right when each block id occurs
+ *      in one row of block_tables. Set it when rows alias blocks (a shared
+ *      prefix): the default policy then keeps a group's repeated reads of the
+ *      same blocks in L2 / MALL. Results are the same either way. No reference
+ *      counterpart: the reference copies prefix blocks per request
+ *      (runtime/phase2/worker_server.py:1442-1449), so its rows never alias.
  * Supported: D in {64, 128}; block_size in {16, 32}; Hq = G * Hkv, G in 1..8.
  * The workspace holds fp32 split partials and the error word; zero it once at
  * allocation so the error word starts clear. Concurrent calls must not share
  * a workspace. out rows must be 16-byte aligned (o_sb, o_sh multiples of 8).
  * ------------------------------------------------------------------------- */
+#define MX_PA_SHARED_BLOCKS 1u
+
 size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                      int32_t block_size, int32_t chunk_tokens);
 
@@ -170,7 +179,8 @@ int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const ui
                          int64_t kv_sblk, int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb,
                          int32_t max_blocks, const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
                          int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out, int64_t o_sb,
-                         int64_t o_sh, void* workspace, size_t workspace_bytes, int32_t chunk_tokens, void* stream);
+                         int64_t o_sh, void* workspace, size_t workspace_bytes, int32_t chunk_tokens, uint32_t flags,
+                         void* stream);
 
 /* Byte offset of the int32 error word inside a paged-attention workspace
  * (nonzero after a call that met an out-of-range block id). Reading it needs a

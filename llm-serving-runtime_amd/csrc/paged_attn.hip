@@ -96,16 +96,27 @@ __device__ __forceinline__ half8v load_half8(const _Float16* p) {
     return __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(p));
 }
 
-// K and V are read once per call: non-temporal loads (the streaming cache policy) keep
-// them from displacing other lines. Measured at the bench shape: 62.0 -> 58.6-60.3 us
-// per call against the default policy.
+// K/V loads. When every block id occurs in one row only, K and V are read once per call
+// and STREAM = true issues non-temporal loads (the streaming cache policy), which keep
+// them from displacing other lines: 62.0 -> 58.6-60.3 us per call at the batch-32 bench
+// shape. When rows alias blocks (a shared prefix, MX_PA_SHARED_BLOCKS) the rows of a
+// group read the same blocks at about the same time and STREAM = false keeps those
+// re-reads in L2 / MALL: 402 -> 325 us per layer on the 128-row shared-prefix batch.
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+template <bool STREAM>
 __device__ __forceinline__ half8v load_kv8(const _Float16* p) {
-    return __builtin_bit_cast(half8v, __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p)));
+    if constexpr (STREAM)
+        return __builtin_bit_cast(half8v, __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p)));
+    else
+        return load_half8(p);
 }
+template <bool STREAM>
 __device__ __forceinline__ half4v load_kv4(const _Float16* p) {
-    return __builtin_bit_cast(half4v, __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(p)));
+    if constexpr (STREAM)
+        return __builtin_bit_cast(half4v, __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(p)));
+    else
+        return __builtin_bit_cast(half4v, *reinterpret_cast<const u32x2v*>(p));
 }
 
 // Tiles of row b (bounded by the table width) and its effective length.
@@ -180,12 +191,14 @@ struct VFragT;
 template <>
 struct VFragT<128> {
     using type = half8v;
-    static __device__ __forceinline__ type load(const _Float16* p) { return load_kv8(p); }
+    template <bool STREAM>
+    static __device__ __forceinline__ type load(const _Float16* p) { return load_kv8<STREAM>(p); }
 };
 template <>
 struct VFragT<64> {
     using type = half4v;
-    static __device__ __forceinline__ type load(const _Float16* p) { return load_kv4(p); }
+    template <bool STREAM>
+    static __device__ __forceinline__ type load(const _Float16* p) { return load_kv4<STREAM>(p); }
 };
 
 template <int KK, typename VF>
@@ -211,7 +224,7 @@ constexpr int kDepth = MX_PA_DEPTH;
 #define MX_PA_MIN_WAVES 3
 #endif
 
-template <int D, int BS, int G>
+template <int D, int BS, int G, bool STREAM>
 __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
     constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
@@ -317,9 +330,9 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
             const _Float16* kt = kbase + base;
             const _Float16* vt = vbase + base;
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_kv8(kt + koff + 32 * kk);
+            for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_kv8<STREAM>(kt + koff + 32 * kk);
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) tr.v[jj] = VFragT<D>::load(vt + voff + jj * D);
+            for (int jj = 0; jj < 4; ++jj) tr.v[jj] = VFragT<D>::template load<STREAM>(vt + voff + jj * D);
         };
 
         auto compute_tile = [&](int j, const Regs& tr) {
@@ -550,7 +563,7 @@ static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_si
 
 // Waves of this kernel instance that fit on the current device at once
 // (occupancy x CUs), cached per device; 0 if the runtime cannot say.
-template <int D, int BS, int G>
+template <int D, int BS, int G, bool STREAM>
 static int resident_waves() {
     static int cache[64] = {0};
     int dev = 0;
@@ -558,7 +571,7 @@ static int resident_waves() {
     if (cache[dev] == 0) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_kernel<D, BS, G>, kWaves * 64, 0) !=
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_kernel<D, BS, G, STREAM>, kWaves * 64, 0) !=
                 hipSuccess)
             return 0;
         cache[dev] = cus * per_cu * kWaves;
@@ -566,28 +579,28 @@ static int resident_waves() {
     return cache[dev];
 }
 
-template <int D, int BS, int G>
+template <int D, int BS, int G, bool STREAM>
 static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     // More workers than resident waves would leave a second, partial round; use
     // one round unless ranges would then exceed kMaxRangeTiles.
-    const int cap = resident_waves<D, BS, G>();
+    const int cap = resident_waves<D, BS, G, STREAM>();
     if (cap > 0 && prm.workers > cap) prm.workers = (int)(floor_workers > cap ? floor_workers : cap);
     const int blocks = (int)ceil_div(prm.workers, kWaves);
-    hipLaunchKernelGGL((decode_split_kernel<D, BS, G>), dim3(blocks), dim3(kWaves * 64), 0, st, prm);
+    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM>), dim3(blocks), dim3(kWaves * 64), 0, st, prm);
     hipLaunchKernelGGL((decode_merge_kernel<D, BS, G>), dim3(prm.Hkv, B), dim3(256), 0, st, prm);
 }
 
-template <int D, int BS>
+template <int D, int BS, bool STREAM>
 static bool dispatch_g(int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
     switch (G) {
-        case 1: launch<D, BS, 1>(prm, B, st, fw); return true;
-        case 2: launch<D, BS, 2>(prm, B, st, fw); return true;
-        case 3: launch<D, BS, 3>(prm, B, st, fw); return true;
-        case 4: launch<D, BS, 4>(prm, B, st, fw); return true;
-        case 5: launch<D, BS, 5>(prm, B, st, fw); return true;
-        case 6: launch<D, BS, 6>(prm, B, st, fw); return true;
-        case 7: launch<D, BS, 7>(prm, B, st, fw); return true;
-        case 8: launch<D, BS, 8>(prm, B, st, fw); return true;
+        case 1: launch<D, BS, 1, STREAM>(prm, B, st, fw); return true;
+        case 2: launch<D, BS, 2, STREAM>(prm, B, st, fw); return true;
+        case 3: launch<D, BS, 3, STREAM>(prm, B, st, fw); return true;
+        case 4: launch<D, BS, 4, STREAM>(prm, B, st, fw); return true;
+        case 5: launch<D, BS, 5, STREAM>(prm, B, st, fw); return true;
+        case 6: launch<D, BS, 6, STREAM>(prm, B, st, fw); return true;
+        case 7: launch<D, BS, 7, STREAM>(prm, B, st, fw); return true;
+        case 8: launch<D, BS, 8, STREAM>(prm, B, st, fw); return true;
         default: return false;
     }
 }
@@ -614,7 +627,7 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
                                     const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
                                     int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out,
                                     int64_t o_sb, int64_t o_sh, void* workspace, size_t workspace_bytes,
-                                    int32_t chunk_tokens, void* stream) {
+                                    int32_t chunk_tokens, uint32_t flags, void* stream) {
     if (B < 0) return fail(MX_ERR_INVALID, "mx_paged_attn_decode: B must be >= 0");
     if (B == 0) return MX_OK;
     if (!q || !k || !v || !block_tables || !seq_lens || !out)
@@ -629,6 +642,8 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     if (max_blocks < 1 || num_pool_blocks < 1)
         return fail(MX_ERR_INVALID, "mx_paged_attn_decode: max_blocks and num_pool_blocks must be >= 1");
     if (B > 65535 || Hkv > 65535) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: B or Hkv too large");
+    if (flags & ~(uint32_t)MX_PA_SHARED_BLOCKS)
+        return fail(MX_ERR_INVALID, "mx_paged_attn_decode: unknown flags 0x%x", flags);
     if (chunk_tokens < 0 || chunk_tokens % pa::kTile != 0 || chunk_tokens > pa::kMaxChunkTokens)
         return fail(MX_ERR_INVALID, "mx_paged_attn_decode: chunk_tokens must be 0 or a multiple of 16 <= %d",
                     pa::kMaxChunkTokens);
@@ -673,10 +688,17 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     // Fewest workers that keep every range within one vector of block ids.
     const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, pa::kTile),
                                 pa::kMaxRangeTiles);
-    if (D == 128 && block_size == 16) ok = pa::dispatch_g<128, 16>(G, prm, B, st, fw);
-    else if (D == 128 && block_size == 32) ok = pa::dispatch_g<128, 32>(G, prm, B, st, fw);
-    else if (D == 64 && block_size == 16) ok = pa::dispatch_g<64, 16>(G, prm, B, st, fw);
-    else ok = pa::dispatch_g<64, 32>(G, prm, B, st, fw);
+    if (flags & MX_PA_SHARED_BLOCKS) {
+        if (D == 128 && block_size == 16) ok = pa::dispatch_g<128, 16, false>(G, prm, B, st, fw);
+        else if (D == 128 && block_size == 32) ok = pa::dispatch_g<128, 32, false>(G, prm, B, st, fw);
+        else if (D == 64 && block_size == 16) ok = pa::dispatch_g<64, 16, false>(G, prm, B, st, fw);
+        else ok = pa::dispatch_g<64, 32, false>(G, prm, B, st, fw);
+    } else {
+        if (D == 128 && block_size == 16) ok = pa::dispatch_g<128, 16, true>(G, prm, B, st, fw);
+        else if (D == 128 && block_size == 32) ok = pa::dispatch_g<128, 32, true>(G, prm, B, st, fw);
+        else if (D == 64 && block_size == 16) ok = pa::dispatch_g<64, 16, true>(G, prm, B, st, fw);
+        else ok = pa::dispatch_g<64, 32, true>(G, prm, B, st, fw);
+    }
     if (!ok) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: unsupported configuration");
     return check_launch("mx_paged_attn_decode");
 }

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -29,6 +29,7 @@ _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _sz = ctypes.c_size_t
+_u32 = ctypes.c_uint32
 
 # name -> (restype, argtypes); mirrors include/mxdecode.h
 SIGNATURES = {
@@ -48,7 +49,7 @@ SIGNATURES = {
     "mx_paged_attn_decode": (
         ctypes.c_int,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32,
-         ctypes.c_float, _p, _i64, _i64, _p, _sz, _i32, _p],
+         ctypes.c_float, _p, _i64, _i64, _p, _sz, _i32, _u32, _p],
     ),
     "mx_kv_append": (
         ctypes.c_int,

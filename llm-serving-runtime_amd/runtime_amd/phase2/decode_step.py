@@ -138,6 +138,9 @@ class Int8DecodeModel:
         # QKV projection + RoPE + append as one launch where it applies (uses_fused_qkv);
         # False keeps the two-launch path (split partials or fp16 rows, then the RoPE kernel).
         self.fuse_qkv_rope = True
+        # Set when block tables may alias block ids across rows (a shared prefix): the
+        # attention kernel then keeps the default cache policy for K/V.
+        self.shared_kv_blocks = False
         self._buffers: dict[int, _Buffers] = {}
         self.layers: list[_Layer] = []
         if not init:
@@ -294,7 +297,7 @@ class Int8DecodeModel:
                                 s.kv_heads, err=buf.err, lens_out=lens_out)
             ev = self._tick(timers, "attn")
             _paged_decode(buf.q.view(bsz, s.heads, 1, s.head_dim), k_layer, v_layer, block_tables, buf.attn_lens,
-                          s.head_dim ** -0.5, s.group, out=buf.attn)
+                          s.head_dim ** -0.5, s.group, out=buf.attn, shared_blocks=self.shared_kv_blocks)
             self._tock(timers, "attn", ev)
             if sp["o"] > 1:
                 self._partials(buf.attn.view(bsz, -1), layer.o, buf.part, timers, "o")

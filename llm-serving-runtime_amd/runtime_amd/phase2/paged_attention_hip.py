@@ -16,7 +16,10 @@ Differences from the reference that a caller can observe:
 * ``seq_len == 0`` rows produce zeros (the reference divides by zero,
   ``:238``); ``paged_attention_decode`` still rejects ``seq_len <= 0`` (``:789-790``);
 * the returned tensor is freshly allocated, never an alias of a cached buffer
-  (the reference's fp32 path aliases its scratch, ``:108-115,600``).
+  (the reference's fp32 path aliases its scratch, ``:108-115,600``);
+* ``PagedDecodeBatchMetadata.shared_blocks`` (default ``False``) says that rows may
+  alias block ids (a shared prefix); the kernel then reads K/V with the default cache
+  policy instead of streaming loads. The result is the same either way.
 """
 
 from __future__ import annotations
@@ -37,6 +40,7 @@ if TYPE_CHECKING:
     from .paged_kv_kernel import GpuKVBlockPool
 
 _CHUNK_TOKENS = int(os.getenv("MX_PAGED_ATTN_CHUNK_TOKENS", "0"))
+MX_PA_SHARED_BLOCKS = 1
 
 _decode_batch_metadata: contextvars.ContextVar["PagedDecodeBatchMetadata | None"] = contextvars.ContextVar(
     "paged_decode_batch_metadata", default=None
@@ -51,6 +55,7 @@ class PagedDecodeBatchMetadata:
     layer_idx: int
     block_tables: torch.Tensor  # [B, max_blocks] int32
     seq_lens: torch.Tensor  # [B] int32, KV length to attend over (includes current token)
+    shared_blocks: bool = False  # rows may alias block ids (MX_PA_SHARED_BLOCKS)
 
 
 PagedDecodeContext = PagedDecodeBatchMetadata
@@ -122,8 +127,8 @@ def workspace_error_flag(device: torch.device | None = None) -> int:
 
 
 def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor,
-            seq_lens: torch.Tensor, scaling: float, num_kv_groups: int, out: torch.Tensor | None = None
-            ) -> torch.Tensor:
+            seq_lens: torch.Tensor, scaling: float, num_kv_groups: int, out: torch.Tensor | None = None,
+            shared_blocks: bool = False) -> torch.Tensor:
     bsz, hq, q_len, d = query.shape
     if q_len != 1:
         raise ValueError("paged decode expects q_len=1")
@@ -162,7 +167,8 @@ def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, b
             query.data_ptr(), query.stride(0), query.stride(1), k_layer.data_ptr(), v_layer.data_ptr(),
             k_layer.stride(0), k_layer.stride(1), block_tables.data_ptr(), block_tables.stride(0), max_blocks,
             seq_lens.data_ptr(), bsz, hq, hkv, d, bs, nb, float(scaling), out.data_ptr(), out.stride(0),
-            out.stride(1), ws.data_ptr(), nbytes, _CHUNK_TOKENS, _hip.stream_handle(query.device),
+            out.stride(1), ws.data_ptr(), nbytes, _CHUNK_TOKENS, MX_PA_SHARED_BLOCKS if shared_blocks else 0,
+            _hip.stream_handle(query.device),
         ),
         "mx_paged_attn_decode",
     )
@@ -179,7 +185,8 @@ def paged_attention_decode_batched(query: torch.Tensor, metadata: PagedDecodeBat
     pool._ensure_pools()
     k_layer = pool.k_layer_view(metadata.layer_idx)
     v_layer = pool.v_layer_view(metadata.layer_idx)
-    return _decode(query, k_layer, v_layer, metadata.block_tables, metadata.seq_lens, scaling, num_kv_groups)
+    return _decode(query, k_layer, v_layer, metadata.block_tables, metadata.seq_lens, scaling, num_kv_groups,
+                   shared_blocks=metadata.shared_blocks)
 
 
 def paged_attention_decode(query: torch.Tensor, pool: "GpuKVBlockPool", layer_idx: int, block_ids: list[int],

@@ -85,14 +85,14 @@ def test_invalid_arguments_return_status_codes():
     _status(lib.mx_w8a16_quantize(None, 4, 4, fake, fake, None), _hip.MX_ERR_NULL)
     args = dict(q=fake, q_sb=256, q_sh=64, k=fake, v=fake, kv_sblk=2048, kv_shead=1024, bt=fake, bt_sb=4, mb=4,
                 sl=fake, B=1, Hq=8, Hkv=2, D=64, bs=16, npool=8, scale=0.125, out=fake, o_sb=512, o_sh=64,
-                ws=None, wsb=0, ct=0, st=None)
+                ws=None, wsb=0, ct=0, flags=0, st=None)
 
     def call(**over):
         a = dict(args, **over)
         return lib.mx_paged_attn_decode(a["q"], a["q_sb"], a["q_sh"], a["k"], a["v"], a["kv_sblk"], a["kv_shead"],
                                         a["bt"], a["bt_sb"], a["mb"], a["sl"], a["B"], a["Hq"], a["Hkv"], a["D"],
                                         a["bs"], a["npool"], a["scale"], a["out"], a["o_sb"], a["o_sh"], a["ws"],
-                                        a["wsb"], a["ct"], a["st"])
+                                        a["wsb"], a["ct"], a["flags"], a["st"])
 
     assert call(B=0) == _hip.MX_OK
     _status(call(q=None), _hip.MX_ERR_NULL)
@@ -102,6 +102,7 @@ def test_invalid_arguments_return_status_codes():
     _status(call(bs=8), _hip.MX_ERR_UNSUPPORTED)
     _status(call(ct=40), _hip.MX_ERR_INVALID)
     _status(call(ct=2048), _hip.MX_ERR_INVALID)  # split granularity is at most 64 tiles
+    _status(call(flags=2), _hip.MX_ERR_INVALID)  # only MX_PA_SHARED_BLOCKS is defined
     _status(call(), _hip.MX_ERR_WORKSPACE)
     _status(call(q_sh=60), _hip.MX_ERR_ALIGNMENT)
     with pytest.raises(ValueError):

@@ -173,7 +173,7 @@ def test_config2_full_shape_and_repeatability():
     assert workspace_error_flag() == 0
 
 
-def _abi_decode(q, k, v, tables, lens, scale, grp, chunk_tokens, num_pool_blocks=None):
+def _abi_decode(q, k, v, tables, lens, scale, grp, chunk_tokens, num_pool_blocks=None, flags=0):
     lib = _hip.load()
     bsz, hq, _, d = q.shape
     nb, hkv, bs, _ = k.shape
@@ -185,7 +185,7 @@ def _abi_decode(q, k, v, tables, lens, scale, grp, chunk_tokens, num_pool_blocks
         q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
         tables.data_ptr(), tables.stride(0), mb, lens.data_ptr(), bsz, hq, hkv, d, bs,
         num_pool_blocks if num_pool_blocks is not None else nb, scale, out.data_ptr(), out.stride(0), out.stride(1),
-        ws.data_ptr(), nbytes, chunk_tokens, _hip.stream_handle(q.device)), "decode")
+        ws.data_ptr(), nbytes, chunk_tokens, flags, _hip.stream_handle(q.device)), "decode")
     torch.cuda.synchronize()
     err = int(ws[lib.mx_paged_attn_error_offset(bsz, hq, hkv, d, mb, bs, chunk_tokens):][:4].view(torch.int32).item())
     return out, err
@@ -203,6 +203,22 @@ def test_split_chunk_size_invariance():
         outs.append(out.float())
     for o in outs[1:]:
         assert (o - outs[0]).abs().max().item() < 2e-3
+
+
+@pytest.mark.parametrize("d,bs", [(128, 16), (128, 32), (64, 16), (64, 32)])
+def test_shared_blocks_flag_is_bit_identical(d, bs):
+    """MX_PA_SHARED_BLOCKS changes only the cache policy of the K/V loads: same bits, with
+    rows that alias each other's blocks."""
+    q, k, v, tables, lens = _random_case(31 + d + bs, 4, 2, 4, d, bs, [300, 700, 64, 1000])
+    tables = tables.clone()
+    tables[1, :4] = tables[0, :4]  # rows 0, 1 and 3 share their first blocks
+    tables[3, :4] = tables[0, :4]
+    scale = d**-0.5
+    plain, err0 = _abi_decode(q, k, v, tables, lens, scale, 4, 0)
+    shared, err1 = _abi_decode(q, k, v, tables, lens, scale, 4, 0, flags=1)
+    assert err0 == 0 and err1 == 0
+    assert torch.equal(plain, shared)
+    _check(shared, oracle_out(q, k, v, tables, lens, scale, 4))
 
 
 @pytest.mark.parametrize("hkv,grp,d,bs", [(2, 7, 64, 16), (4, 1, 128, 16), (2, 8, 128, 16), (3, 2, 64, 32),

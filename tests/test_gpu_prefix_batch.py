@@ -2,8 +2,8 @@
 
 * Alias safety of the attention kernel: rows whose tables alias their group's prefix
   blocks give bit-identical output to the same rows with the prefix copied into private
-  blocks (the reference's copy-on-hit, ``runtime/phase2/worker_server.py:1372-1375``), and
-  both match the fp32 oracle within atol/rtol 1e-2.
+  blocks (the reference's copy-on-hit, ``runtime/phase2/worker_server.py:1372-1375``),
+  under either K/V cache policy, and match the fp32 oracle within atol/rtol 1e-2.
 * The native decode step over a :class:`PrefixBatch`: rows of a group share a prompt
   prefix and its K/V blocks; half-way through, two requests finish and two new ones join
   their slots (freed blocks reused, tables and lengths rewritten in place while the step
@@ -55,9 +55,11 @@ def test_aliased_prefix_blocks_equal_copied_blocks():
             v[dst] = v[r.blocks[j]]
             copied[b, j] = dst
     scale = d**-0.5
-    out_alias = _decode(q, k, v, tables.to(DEV), lens.to(DEV), scale, grp)
+    out_alias = _decode(q, k, v, tables.to(DEV), lens.to(DEV), scale, grp, shared_blocks=True)
     out_copy = _decode(q, k, v, copied.to(DEV), lens.to(DEV), scale, grp)
     assert torch.equal(out_alias, out_copy)
+    # The streaming cache policy reads the aliased blocks to the same result.
+    assert torch.equal(_decode(q, k, v, tables.to(DEV), lens.to(DEV), scale, grp), out_alias)
     want = oracle_pa.decode_rows_fp32(q.cpu(), k.cpu(), v.cpu(), tables, lens.tolist(), scale, grp)
     np.testing.assert_allclose(out_alias.float().cpu().numpy(), want.numpy(), atol=1e-2, rtol=1e-2)
 
@@ -81,6 +83,7 @@ def test_native_step_shared_prefix_join_finish():
     ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
     torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
     native = Int8DecodeModel.from_hf(hf, device=DEV, max_positions=1024)
+    native.shared_kv_blocks = True
     s = native.shape
     batch, groups, prefix = 16, 2, 64
     g = torch.Generator().manual_seed(6)
