@@ -201,35 +201,40 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 // staging; their accumulators are summed in LDS (part 0 first) before the one partial of
 // the split is written. The host requires KT % (KS * KW) == 0, so every group takes the
 // same number of steps and meets every barrier.
-// Waves per SIMD the plain 4-wave, MT <= 2 instances must fit: left free the compiler uses
-// 226 VGPRs (2 waves per SIMD), so a 768-workgroup launch (qkv at M=32) ran in 1.5 rounds;
-// at 3 it takes 166 VGPRs without spills and one round (qkv 12.5 -> 10.3 us on MI355X).
+// Waves per SIMD the NPW = 1, MT <= 2 instances without k parts must fit: left free the
+// compiler uses 226 VGPRs (2 waves per SIMD), so a 768-workgroup launch (qkv at M=32) ran in
+// 1.5 rounds; at 3 it takes 166 VGPRs without spills and one round (qkv 12.5 -> 10.3 us on
+// MI355X). The gate||up SwiGLU instance (7 waves, one workgroup per CU) fits either way, yet
+// its 166-VGPR schedule streams faster: 26.5-28.0 -> 24.3-24.4 us at M=32 in the decode step.
+// The k-part instances (o, down) measured the same at 166 and 226 and stay unbounded.
 #ifndef MX_GEMM_MIN_WAVES
 #define MX_GEMM_MIN_WAVES 3
 #endif
-template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false, int KW = 1>
-__global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && KW == 1) ? MX_GEMM_MIN_WAVES : 1) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
+template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false, int KW = 1, int MW = 1>
+__global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 && MW == 1) ? MX_GEMM_MIN_WAVES : 1) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
                                                                const uint16_t* __restrict__ bias,
                                                                uint16_t* __restrict__ y, int64_t ys, int KT, int NT,
                                                                float* __restrict__ partial) {
-    constexpr int ROWS = MT * 16;
+    constexpr int ROWS = MW * MT * 16;  // x rows staged per k-tile (MW waves along M, MT m-tiles each)
     constexpr int RS = kTileK + 8;  // LDS row stride (halfs): 144 bytes, rows start 4 banks apart
-    constexpr int WN = WAVES / KW;  // waves per k part, each owning NPW n-tiles
-    static_assert(WN * KW == WAVES && (KW == 1 || !GU), "k parts split only partial launches");
+    constexpr int WN = WAVES / (KW * MW);  // waves along N per k part, each owning NPW n-tiles
+    constexpr int WP = WN * MW;            // waves per k part
+    static_assert(WN * KW * MW == WAVES && (KW == 1 || !GU), "k parts split only partial launches");
     constexpr int XCH = ROWS * 8;   // 16-byte chunks of one x k-tile
-    constexpr int XC = (XCH + WN * 64 - 1) / (WN * 64);
+    constexpr int XC = (XCH + WP * 64 - 1) / (WP * 64);
     __shared__ __attribute__((aligned(16))) _Float16 xl[KW][2][ROWS * RS];
 
     const int ks = blockIdx.y, KS = gridDim.y;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kw = wave / WN, wn = wave - kw * WN;
+    const int kw = wave / WP, wm = wave - kw * WP;
+    const int mw = wm / WN, wn = wm - mw * WN;
     const int kt_split = (int)((int64_t)ks * KT / KS);
     const int nj = ((int)((int64_t)(ks + 1) * KT / KS) - kt_split) / KW;
     const int kt_lo = kt_split + kw * nj;
-    const int ltid = tid - kw * WN * 64;  // thread index within the k part
+    const int ltid = tid - kw * WP * 64;  // thread index within the k part
     const int lane = tid & 63;
     const int g = lane >> 4, r = lane & 15;
     const int nt_w = (blockIdx.x * WN + wn) * NPW;
@@ -237,12 +242,12 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && K
     const int nt_c = valid ? nt_w : NT - NPW;     // out-of-range waves load (and drop) the last tiles
     const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt_c * 64;  // tile (nt_c + p, kt): + (kt*NT + p)*64
 
-    // x chunks of this thread: chunk c = ltid + u*WN*64 (wrapped when the tile has
+    // x chunks of this thread: chunk c = ltid + u*WP*64 (wrapped when the tile has
     // fewer chunks than threads; the duplicate writes store identical bytes).
     int xsrc[XC], xdst[XC];
 #pragma unroll
     for (int u = 0; u < XC; ++u) {
-        const int c = (ltid + u * WN * 64) % XCH;
+        const int c = (ltid + u * WP * 64) % XCH;
         const int row = c / 8, col = (c % 8) * 8;
         const int rc = row < M ? row : M - 1;
         xsrc[u] = (int)(rc * xs) + col;
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && K
     auto load = [&](int j, St& st) {
         const int kt = kt_lo + (j < nj ? j : nj - 1);
 #pragma unroll
-        for (int p = 0; p < NPW; ++p) st.w[p] = load_wtile(wbase + ((int64_t)kt * NT + p) * 64 + lane);
+        for (int p = 0; p < NPW; ++p) st.w[p] = load_wtile<MW == 1>(wbase + ((int64_t)kt * NT + p) * 64 + lane);
 #pragma unroll
         for (int u = 0; u < XC; ++u) {
             st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
@@ -298,7 +303,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && K
         half8v a[MT][2];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const _Float16* src = buf + (mt * 16 + r) * RS + 16 * g;
+            const _Float16* src = buf + ((mw * MT + mt) * 16 + r) * RS + 16 * g;
             a[mt][0] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(src));
             a[mt][1] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(src + 8));
         }
@@ -321,33 +326,36 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && K
     const int N = NT * kTileN;
     if (GU) {
         // Every lane takes part in the swap; out-of-range waves just do not store.
-        const int c = nt_c * (kTileN / 2) + (r & 7);  // SwiGLU channel of this lane pair
-        const int64_t n = (int64_t)nt_c * kTileN + r;
-        const float sc = h2f(scale, n);
-        const float bi = bias ? h2f(bias, n) : 0.0f;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int p = 0; p < NPW; ++p) {
+            const int c = (nt_c + p) * (kTileN / 2) + (r & 7);  // SwiGLU channel of this lane pair
+            const int64_t n = (int64_t)(nt_c + p) * kTileN + r;
+            const float sc = h2f(scale, n);
+            const float bi = bias ? h2f(bias, n) : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float v = (float)(_Float16)pin_f32(acc[0][mt][i] * sc + bi);  // this lane's projection
-                const float other = __shfl_xor(v, 8);
-                const int m = mt * 16 + 4 * g + i;
-                if (valid && r < 8 && m < M) {
-                    const _Float16 sg = (_Float16)silu_f32(v);
-                    y[(int64_t)m * ys + c] = f2h_bits((float)sg * other);
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float v = (float)(_Float16)pin_f32(acc[p][mt][i] * sc + bi);  // this lane's projection
+                    const float other = __shfl_xor(v, 8);
+                    const int m = (mw * MT + mt) * 16 + 4 * g + i;
+                    if (valid && r < 8 && m < M) {
+                        const _Float16 sg = (_Float16)silu_f32(v);
+                        y[(int64_t)m * ys + c] = f2h_bits((float)sg * other);
+                    }
                 }
-            }
+        }
         return;
     }
     if constexpr (KW > 1) {
         // Parts 1.. hand their accumulators to part 0 through LDS; every wave reaches this
         // barrier (out-of-range waves too) before any of them leaves.
-        __shared__ float4v red[KW - 1][WN][NPW][MT][64];
+        __shared__ float4v red[KW - 1][WP][NPW][MT][64];
         if (kw > 0) {
 #pragma unroll
             for (int p = 0; p < NPW; ++p)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) red[kw - 1][wn][p][mt][lane] = acc[p][mt];
+                for (int mt = 0; mt < MT; ++mt) red[kw - 1][wm][p][mt][lane] = acc[p][mt];
         }
         __syncthreads();
         if (kw > 0) return;
@@ -356,7 +364,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && K
 #pragma unroll
             for (int p = 0; p < NPW; ++p)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) acc[p][mt] += red[q][wn][p][mt][lane];
+                for (int mt = 0; mt < MT; ++mt) acc[p][mt] += red[q][wm][p][mt][lane];
     }
     if (!valid) return;
 #pragma unroll
@@ -368,7 +376,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !GU && !SW && MT <= 2 && K
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int m = mt * 16 + 4 * g + i;
+                const int m = (mw * MT + mt) * 16 + 4 * g + i;
                 if (m >= M) continue;
                 if (KS == 1) y[(int64_t)m * ys + n] = f2h_bits(pin_f32(acc[p][mt][i] * sc + bi));
                 else partial[((int64_t)ks * M + m) * N + n] = acc[p][mt][i] * sc;
@@ -444,10 +452,34 @@ static int splits_for(int NT, int KT) {
     return ks;
 }
 
+// Chunks of more than 64 rows (6 or 8 m-tiles): 8-wave workgroups of 2 waves along M
+// (each 3 or 4 m-tiles, all of the chunk's rows staged once in LDS) by 4 along N, each
+// wave holding 2 n-tiles, so every x fragment read from LDS feeds two MFMAs. The two
+// m-halves read the same weight tiles (the second read is an L2 hit). With one 4-wave
+// workgroup of 8 m-tiles x 1 n-tile (254 VGPRs + 48 AGPRs, one wave per SIMD) the
+// Llama-3-8B projections at M = 128 ran at 1.2 TB/s (qkv 37.5, o 26.8, gate_up 75.4,
+// down 44.2 us on MI355X). K is split until the grid holds about one workgroup per CU.
+constexpr int kBigWaves = 8, kBigNpw = 2;
+constexpr int kBigTiles = (kBigWaves / 2) * kBigNpw;  // n-tiles per workgroup
+constexpr int kBigGrid = 256;
+static bool big_m_shape(int NT) { return NT % kBigNpw == 0; }
+static int big_splits(int NT, int KT) {
+    const int groups = ceil_div(NT, kBigTiles);
+    int ks = 1;
+    while (ks < kMaxSplits && groups * ks * 2 <= kBigGrid && KT / (2 * ks) >= kMinSplitTiles) ks *= 2;
+    return ks;
+}
+
 static Plan plan_for(int M, int NT, int KT) {
     Plan pl{};
     pl.KS = 1;
     pl.KW = 1;
+    if (mt_for(M) >= 6 && big_m_shape(NT)) {
+        pl.valu = false;
+        pl.MT = mt_for(M);
+        pl.KS = big_splits(NT, KT);
+        return pl;
+    }
     // The VALU GEMV takes M <= 4 unless the n-groups alone fill the chip: there the
     // MFMA kernel's wide workgroups stream faster even with 15 padding rows (gate||up
     // at M = 1: 33.2 us GEMV, 23 us MFMA), while split shapes keep the GEMV, which needs
@@ -505,13 +537,14 @@ static WideShape wide_shape(int NT, bool npw1_only) {
     return WideShape{kMfmaWaves, 1};
 }
 
-template <int MT, int NPW, int WAVES, bool SW, bool GU, int KW = 1>
+template <int MT, int NPW, int WAVES, bool SW, bool GU, int KW = 1, int MW = 1>
 static void launch_shape(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                          uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
-    constexpr int P = NPW == 1 ? mfma_depth(MT) : (NPW == 2 ? 6 : 4);
-    const int groups = ceil_div(NT, (WAVES / KW) * NPW);
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, WAVES, P, SW, GU, KW>), dim3(groups, KS), dim3(WAVES * 64), 0, st, x,
-                       xs, M, w, s, b, y, ys, KT, NT, partial);
+    // Pipeline depth: 6 for the M-split shape spilled (24 VGPRs at 4 m-tiles); 4 fits.
+    constexpr int P = MW > 1 ? 4 : (NPW == 1 ? mfma_depth(MT) : (NPW == 2 ? 6 : 4));
+    const int groups = ceil_div(NT, (WAVES / (KW * MW)) * NPW);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, WAVES, P, SW, GU, KW, MW>), dim3(groups, KS), dim3(WAVES * 64), 0, st,
+                       x, xs, M, w, s, b, y, ys, KT, NT, partial);
 }
 
 // The MFMA kernel alone: KS == 1 writes fp16 y, KS > 1 writes the scaled fp32
@@ -519,6 +552,12 @@ static void launch_shape(const uint16_t* x, int64_t xs, int M, const uint8_t* w,
 template <int MT, bool SW, bool GU = false>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, int KS, int KW, float* partial, hipStream_t st) {
+    if constexpr (MT >= 6 && !SW) {
+        if (big_m_shape(NT)) {
+            launch_shape<MT / 2, kBigNpw, kBigWaves, SW, GU, 1, 2>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);
+            return;
+        }
+    }
     if constexpr (MT <= 4 && !GU && kKParts > 1) {
         if (KS > 1 && KW == kKParts) {
             launch_shape<MT, 1, kMfmaWaves * kKParts, SW, GU, kKParts>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);

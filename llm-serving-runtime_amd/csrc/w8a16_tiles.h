@@ -21,12 +21,15 @@ struct U32x4 {
 // loads take the streaming (non-temporal) cache policy; x, which every workgroup re-reads
 // from L2, keeps the default one. Measured in the decode step at batch 32: lm_head
 // 91.3 -> 82.8 us (6.45 TB/s), qkv 13.1 -> 12.6 us, the step 4.42 -> 4.39 ms.
+// STREAM = false where two waves read each tile (the M-split shape): there the default
+// policy measured faster (M = 128: qkv 26.1 -> 22.4 us, o 25.1 -> 21.4 us).
 #ifndef MX_W8A16_NT_WEIGHTS
 #define MX_W8A16_NT_WEIGHTS 1
 #endif
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+template <bool STREAM = true>
 __device__ __forceinline__ uint4 load_wtile(const uint4* p) {
-    if constexpr (MX_W8A16_NT_WEIGHTS) {
+    if constexpr (MX_W8A16_NT_WEIGHTS && STREAM) {
         const u32x4v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
         return uint4{v.x, v.y, v.z, v.w};
     } else {

@@ -128,9 +128,12 @@ def test_native_step_qwen2_shape():
 
 
 @pytest.mark.timeout(600)
-def test_native_step_more_than_64_rows():
-    """72 rows: the linears and the fused gate||up take rows 64 at a time, without K splits."""
-    _run(om.random_qwen2(seed=3, num_hidden_layers=2, vocab_size=32768), batch=72, lo=16, hi=48, seed=3, graph=True)
+@pytest.mark.parametrize("batch", [72, 128])
+def test_native_step_more_than_64_rows(batch):
+    """72 and 128 rows: one chunk of 6 or 8 m-tiles in the MFMA shape with two waves along M,
+    with K split where the n-groups alone do not fill the chip."""
+    _run(om.random_qwen2(seed=3, num_hidden_layers=2, vocab_size=32768), batch=batch, lo=16, hi=48, seed=3,
+         graph=True)
 
 
 @pytest.mark.timeout(600)
