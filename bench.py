@@ -17,7 +17,9 @@ two HIP events, which gives its average launch duration without host launch
 latency inside the interval (the single lm_head launch is repeated 8 times in its
 graph for the same reason). ``cpu_baseline`` times the CPU oracle on a bounded
 sample (one decoder layer at the same batch and contexts, plus an lm_head
-slice), extrapolated to the full step.
+slice), extrapolated to the full step. ``hbm_copy`` is a timed 1 GiB
+device-to-device copy in the same process: the streaming rate this box reaches,
+beside the nominal 8 TB/s peak that ``roofline.frac`` divides by.
 """
 
 from __future__ import annotations
@@ -259,6 +261,30 @@ def time_family(run, launches: int, reps: int) -> float:
 
 COPY_PROBE_BYTES = 1 << 30
 TRAFFIC_PROFILE = os.path.join(HERE, "profiles", "paged_attn_traffic_llama3_8b_b32.md")
+
+
+def copy_bandwidth(reps: int = 10) -> dict:
+    """The box's streaming rate beside the nominal peak: a 1 GiB device-to-device copy,
+    HIP-event timed over ``reps`` copies; bytes = read + written."""
+    import torch
+
+    src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    t = a.elapsed_time(b) * 1e-3 / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    gbps = 2 * COPY_PROBE_BYTES / t / 1e9
+    return {"gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "what": "1 GiB device-to-device copy (torch copy_), read + written bytes"}
 
 
 def measured_traffic(kernel: str, model: str, batch: int):
@@ -653,6 +679,7 @@ def attention_bench(args) -> int:
                                "U[128,4096], pool 16384 blocks x 32 layers", "bytes_per_call": byts},
         "roofline": {"bound": "hbm", "kernel": "attn", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+        "hbm_copy": copy_bandwidth(),
         "cpu_baseline": {"value": round(byts / t_cpu / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
                          "sample": "one call of the per-row fp32 oracle (oracle.paged_attention.decode_rows_fp32) "
                                    "on the same inputs", "ms_per_call": round(t_cpu * 1e3, 1)},
@@ -806,6 +833,7 @@ def main() -> int:
                                       f"(copy-calibrated), profiles/{os.path.basename(TRAFFIC_PROFILE)}; "
                                       f"{traffic[1]} algorithmic bytes at that run's contexts") if traffic else None},
         "kernels": kernels,
+        "hbm_copy": copy_bandwidth(),
         "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu_baseline:
