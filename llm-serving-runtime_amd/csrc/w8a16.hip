@@ -201,6 +201,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 // staging; their accumulators are summed in LDS (part 0 first) before the one partial of
 // the split is written. The host requires KT % (KS * KW) == 0, so every group takes the
 // same number of steps and meets every barrier.
+//
+// MW > 1: the waves of a k part also split the rows: wave (mw, wn) computes m-tiles
+// mw*MT .. mw*MT + MT - 1 of the MW*MT staged (MW*MT*16 x rows per k-tile) for its NPW
+// n-tiles, so MT counts m-tiles per wave and the MW waves of one wn read the same weight
+// tiles (the repeats hit L2).
 // Waves per SIMD the NPW = 1, MT <= 2 instances without k parts must fit: left free the
 // compiler uses 226 VGPRs (2 waves per SIMD), so a 768-workgroup launch (qkv at M=32) ran in
 // 1.5 rounds; at 3 it takes 166 VGPRs without spills and one round (qkv 12.5 -> 10.3 us on
