@@ -80,7 +80,11 @@ struct Params {
 
 constexpr int kWaves = 4;
 constexpr int kTile = 16;               // tokens per MFMA tile
-constexpr int kMaxRangeTiles = 64;      // a worker's range fits one vector of block ids
+constexpr int kMaxRangeTiles = 64;      // a worker's range fits one vector of block ids (block size >= 16)
+// Tiles whose block ids fit one vector: block sizes 4 and 8 put 4 or 2 blocks in a tile.
+constexpr int max_range_tiles(int block_size) {
+    return block_size >= kTile ? kMaxRangeTiles : kMaxRangeTiles * block_size / kTile;
+}
 constexpr int kDefaultWorkers = 2048;   // 256 CUs x 8 waves on MI355X
 constexpr int kMinDefaultTiles = 4;     // default ranges are at least this long when T allows
 // Default workers per segment on average (the merge reads 16 pieces per memory round trip),
@@ -228,7 +232,9 @@ template <int D, int BS, int G, bool STREAM>
 __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
     constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
-    constexpr int TPB = BS / kTile;  // tiles per KV block
+    constexpr int TPB = BS >= kTile ? BS / kTile : 1;  // tiles per KV block (block sizes 16, 32)
+    constexpr int BPT = BS >= kTile ? 1 : kTile / BS;  // KV blocks per tile (block sizes 4, 8)
+    constexpr int kMaxRange = kMaxRangeTiles / BPT;    // tiles whose block ids fit one vector
     constexpr int P = kDepth;
     using VF = typename VFragT<D>::type;
     using Regs = TileRegs<KK, VF>;
@@ -255,8 +261,12 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
     const int64_t hi = range_lo(worker + 1, T, W);
     int64_t x = range_lo(worker, T, W);
 
-    const int koff = r * D + 8 * g;         // K: token r, dims 8g + 32kk
-    const int voff = 4 * g * D + DPL * r;   // V: token 4g + j, dims DPL*r + e
+    // K: token r, dims 8g + 32kk; V: tokens 4g + j, dims DPL*r + e. With BPT > 1 a tile spans
+    // BPT blocks: lane's K token lies in block slot kslot of the tile and its V tokens (and the
+    // 4 scores it holds) in slot vslot, at the given offsets inside those blocks.
+    const int koff = (BPT == 1 ? r : r % BS) * D + 8 * g;
+    const int voff = (BPT == 1 ? 4 * g : (4 * g) % BS) * D + DPL * r;
+    const int kslot = r / BS, vslot = (4 * g) / BS;
 
     while (x < hi) {
         Seg sg;
@@ -276,8 +286,8 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
         const int kvh = (int)((x - sg.row_start) / nt);
         const int t0 = (int)((x - sg.row_start) % nt);
         const int t1 = (int64_t)(nt - t0) < hi - x ? nt : (int)(t0 + (hi - x));
-        const int nj = t1 - t0;  // <= kMaxRangeTiles because W >= ceil(T_max / 64)
-        if (nj > kMaxRangeTiles) {
+        const int nj = t1 - t0;  // <= kMaxRange because W >= ceil(T_max / kMaxRange)
+        if (nj > kMaxRange) {
             atomicOr(p.err, 4);
             break;
         }
@@ -287,12 +297,22 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
         else row_tiles<BS>(p, b, s_eff);
         const int h0 = kvh * G;
 
-        // Block ids of the piece: lane j holds the id of tile t0 + j; an id outside
-        // the pool becomes -1 (tile skipped, error recorded).
+        // Block ids of the piece: lane j holds the id of tile t0 + j (BPT == 1) or of block
+        // slot j of the piece's tiles (BPT > 1, only the row's blocks below s_eff are read);
+        // an id outside the pool becomes -1 (its tokens skipped, error recorded).
         const int32_t* bt_row = p.bt + (int64_t)b * p.bt_sb;
         int my_pb = 0;
-        if (lane < nj) {
-            my_pb = bt_row[(t0 + lane) / TPB];
+        bool fetch;
+        int bslot;
+        if constexpr (BPT == 1) {
+            fetch = lane < nj;
+            bslot = (t0 + lane) / TPB;
+        } else {
+            bslot = t0 * BPT + lane;
+            fetch = lane < nj * BPT && bslot < (s_eff + BS - 1) / BS;
+        }
+        if (fetch) {
+            my_pb = bt_row[bslot];
             if ((unsigned)my_pb >= (unsigned)p.num_pool_blocks) {  // never read outside the pool
                 atomicOr(p.err, 1);
                 my_pb = -1;
@@ -324,11 +344,20 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
         // predicated, by wave-uniform flags, so waits count exact stages.
         auto load_tile = [&](int j, Regs& tr) {
             const int jc = j < nj ? j : nj - 1;
-            const int pb = __builtin_amdgcn_readlane(my_pb, jc);
-            const int t = t0 + jc;
-            const int64_t base = (int64_t)(pb < 0 ? 0 : pb) * p.kv_sblk + (t % TPB) * kTile * D;
-            const _Float16* kt = kbase + base;
-            const _Float16* vt = vbase + base;
+            const _Float16* kt;
+            const _Float16* vt;
+            if constexpr (BPT == 1) {
+                const int pb = __builtin_amdgcn_readlane(my_pb, jc);
+                const int t = t0 + jc;
+                const int64_t base = (int64_t)(pb < 0 ? 0 : pb) * p.kv_sblk + (t % TPB) * kTile * D;
+                kt = kbase + base;
+                vt = vbase + base;
+            } else {
+                const int pk = __shfl(my_pb, jc * BPT + kslot);
+                const int pv = __shfl(my_pb, jc * BPT + vslot);
+                kt = kbase + (int64_t)(pk < 0 ? 0 : pk) * p.kv_sblk;
+                vt = vbase + (int64_t)(pv < 0 ? 0 : pv) * p.kv_sblk;
+            }
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_kv8<STREAM>(kt + koff + 32 * kk);
 #pragma unroll
@@ -342,9 +371,11 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
             for (int kk = 0; kk < KK; ++kk) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(tr.k[kk], qf[kk], s, 0, 0, 0);
             // s[i] = score of token t*16 + 4g + i for head r.
             const int tok0 = t * kTile + 4 * g;
+            // BPT > 1: this lane's 4 tokens lie in one block (slot vslot); a skipped block masks them.
+            const bool skipped = BPT > 1 && __shfl(my_pb, j * BPT + vslot) < 0;
             float sc[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < s_eff) ? s[i] * p.scale_log2e : kNegInf;
+            for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < s_eff && !skipped) ? s[i] * p.scale_log2e : kNegInf;
             const float mx = xor_max_16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
             // Lazy rescale: the reference point m_run moves only when a score exceeds it
             // by more than kLazyLog2, so p = exp2(s - m_run) <= 2^kLazyLog2 (exact range
@@ -372,10 +403,10 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
             VF v[4];
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) v[jj] = tr.v[jj];
-            if (t * kTile + kTile > s_eff) {
+            if (t * kTile + kTile > s_eff || skipped) {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
-                    if (tok0 + jj >= s_eff) v[jj] = VF{};
+                    if (tok0 + jj >= s_eff || skipped) v[jj] = VF{};
             }
 #pragma unroll
             for (int e = 0; e < DPL; ++e) {
@@ -392,7 +423,7 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
 #pragma unroll
                 for (int s = 0; s < P; ++s) {
                     const int j = j0 + s;
-                    if (j < nj && __builtin_amdgcn_readlane(my_pb, j) >= 0) compute_tile(j, st[s]);
+                    if (j < nj && (BPT > 1 || __builtin_amdgcn_readlane(my_pb, j) >= 0)) compute_tile(j, st[s]);
                     load_tile(j + P, st[s]);
                 }
             }
@@ -523,8 +554,8 @@ struct Layout {
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Number of workers. T_max (every row at the table width) bounds the real tile
-// count, so W >= ceil(T_max / 64) keeps each range within one vector of block
-// ids. chunk_tokens > 0 asks for ranges of about that many tokens at T_max;
+// count, so W >= ceil(T_max / max_range_tiles) keeps each range within one vector
+// of block ids. chunk_tokens > 0 asks for ranges of about that many tokens at T_max;
 // 0 picks kDefaultWorkers (one round of resident waves on the chip), fewer
 // when that would make ranges shorter than kMinDefaultTiles tiles or cut a
 // segment into more than kPiecesPerSegment pieces on average (but at least
@@ -532,7 +563,7 @@ static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 static int resolve_workers(int chunk_tokens, int B, int Hkv, int max_blocks, int block_size) {
     const int64_t row_tiles_max = ceil_div((int64_t)max_blocks * block_size, kTile);
     const int64_t t_max = (int64_t)B * Hkv * row_tiles_max;
-    const int64_t floor_w = ceil_div(t_max, kMaxRangeTiles);
+    const int64_t floor_w = ceil_div(t_max, max_range_tiles(block_size));
     int64_t w;
     if (chunk_tokens > 0) {
         w = ceil_div(t_max, chunk_tokens / kTile);
@@ -582,7 +613,7 @@ static int resident_waves() {
 template <int D, int BS, int G, bool STREAM>
 static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     // More workers than resident waves would leave a second, partial round; use
-    // one round unless ranges would then exceed kMaxRangeTiles.
+    // one round unless ranges would then exceed max_range_tiles.
     const int cap = resident_waves<D, BS, G, STREAM>();
     if (cap > 0 && prm.workers > cap) prm.workers = (int)(floor_workers > cap ? floor_workers : cap);
     const int blocks = (int)ceil_div(prm.workers, kWaves);
@@ -601,6 +632,21 @@ static bool dispatch_g(int G, const Params& prm, int B, hipStream_t st, int64_t 
         case 6: launch<D, BS, 6, STREAM>(prm, B, st, fw); return true;
         case 7: launch<D, BS, 7, STREAM>(prm, B, st, fw); return true;
         case 8: launch<D, BS, 8, STREAM>(prm, B, st, fw); return true;
+        default: return false;
+    }
+}
+
+template <bool STREAM>
+static bool dispatch_d_bs(int D, int BS, int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
+    switch (D * 100 + BS) {
+        case 12804: return dispatch_g<128, 4, STREAM>(G, prm, B, st, fw);
+        case 12808: return dispatch_g<128, 8, STREAM>(G, prm, B, st, fw);
+        case 12816: return dispatch_g<128, 16, STREAM>(G, prm, B, st, fw);
+        case 12832: return dispatch_g<128, 32, STREAM>(G, prm, B, st, fw);
+        case 6404: return dispatch_g<64, 4, STREAM>(G, prm, B, st, fw);
+        case 6408: return dispatch_g<64, 8, STREAM>(G, prm, B, st, fw);
+        case 6416: return dispatch_g<64, 16, STREAM>(G, prm, B, st, fw);
+        case 6432: return dispatch_g<64, 32, STREAM>(G, prm, B, st, fw);
         default: return false;
     }
 }
@@ -637,8 +683,9 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     const int G = Hq / Hkv;
     if (G > 8) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: GQA group %d > 8 unsupported", G);
     if (D != 64 && D != 128) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: head_dim %d unsupported", D);
-    if (block_size != 16 && block_size != 32)
-        return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: block_size %d unsupported (16 or 32)", block_size);
+    if (block_size != 4 && block_size != 8 && block_size != 16 && block_size != 32)
+        return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: block_size %d unsupported (4, 8, 16 or 32)",
+                    block_size);
     if (max_blocks < 1 || num_pool_blocks < 1)
         return fail(MX_ERR_INVALID, "mx_paged_attn_decode: max_blocks and num_pool_blocks must be >= 1");
     if (B > 65535 || Hkv > 65535) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: B or Hkv too large");
@@ -687,18 +734,11 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     bool ok = false;
     // Fewest workers that keep every range within one vector of block ids.
     const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, pa::kTile),
-                                pa::kMaxRangeTiles);
-    if (flags & MX_PA_SHARED_BLOCKS) {
-        if (D == 128 && block_size == 16) ok = pa::dispatch_g<128, 16, false>(G, prm, B, st, fw);
-        else if (D == 128 && block_size == 32) ok = pa::dispatch_g<128, 32, false>(G, prm, B, st, fw);
-        else if (D == 64 && block_size == 16) ok = pa::dispatch_g<64, 16, false>(G, prm, B, st, fw);
-        else ok = pa::dispatch_g<64, 32, false>(G, prm, B, st, fw);
-    } else {
-        if (D == 128 && block_size == 16) ok = pa::dispatch_g<128, 16, true>(G, prm, B, st, fw);
-        else if (D == 128 && block_size == 32) ok = pa::dispatch_g<128, 32, true>(G, prm, B, st, fw);
-        else if (D == 64 && block_size == 16) ok = pa::dispatch_g<64, 16, true>(G, prm, B, st, fw);
-        else ok = pa::dispatch_g<64, 32, true>(G, prm, B, st, fw);
-    }
+                                pa::max_range_tiles(block_size));
+    if (flags & MX_PA_SHARED_BLOCKS)
+        ok = pa::dispatch_d_bs<false>(D, block_size, G, prm, B, st, fw);
+    else
+        ok = pa::dispatch_d_bs<true>(D, block_size, G, prm, B, st, fw);
     if (!ok) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: unsupported configuration");
     return check_launch("mx_paged_attn_decode");
 }

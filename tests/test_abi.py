@@ -99,7 +99,7 @@ def test_invalid_arguments_return_status_codes():
     _status(call(Hq=7), _hip.MX_ERR_INVALID)
     _status(call(Hq=36, Hkv=2), _hip.MX_ERR_UNSUPPORTED)  # G = 18
     _status(call(D=96), _hip.MX_ERR_UNSUPPORTED)
-    _status(call(bs=8), _hip.MX_ERR_UNSUPPORTED)
+    _status(call(bs=12), _hip.MX_ERR_UNSUPPORTED)
     _status(call(ct=40), _hip.MX_ERR_INVALID)
     _status(call(ct=2048), _hip.MX_ERR_INVALID)  # split granularity is at most 64 tiles
     _status(call(flags=2), _hip.MX_ERR_INVALID)  # only MX_PA_SHARED_BLOCKS is defined

@@ -164,6 +164,17 @@ def _config2(seed=0):
     return q, k, v, tables.cuda(), lens.to(torch.int32).cuda(), grp, d**-0.5
 
 
+@pytest.mark.parametrize("seq_len", [7, 100])
+def test_reference_block_size_4_shapes(seq_len):
+    """tests/test_paged_attention_kernel_parity.py:80-100 of the reference run its short case at block size 4
+    (Hkv 2, G 2, 7 tokens; there D 32 in fp32 on the CPU path). The same shapes at D 64 in fp16 (the kernel's
+    smallest head dim): a 16-token tile spans 4 blocks, each lane reads its own block."""
+    hkv, grp, d, bs = 2, 2, 64, 4
+    q, k, v, tables, sl = _random_case(40 + seq_len, 1, hkv, grp, d, bs, [seq_len])
+    scale = d**-0.5
+    _check(_decode(q, k, v, tables, sl, scale, grp), oracle_out(q, k, v, tables, sl, scale, grp))
+
+
 def test_config2_full_shape_and_repeatability():
     q, k, v, tables, lens, grp, scale = _config2()
     got = _decode(q, k, v, tables, lens, scale, grp)
@@ -205,7 +216,7 @@ def test_split_chunk_size_invariance():
         assert (o - outs[0]).abs().max().item() < 2e-3
 
 
-@pytest.mark.parametrize("d,bs", [(128, 16), (128, 32), (64, 16), (64, 32)])
+@pytest.mark.parametrize("d,bs", [(128, 16), (128, 32), (64, 16), (64, 32), (128, 4), (64, 8)])
 def test_shared_blocks_flag_is_bit_identical(d, bs):
     """MX_PA_SHARED_BLOCKS changes only the cache policy of the K/V loads: same bits, with
     rows that alias each other's blocks."""
@@ -222,7 +233,8 @@ def test_shared_blocks_flag_is_bit_identical(d, bs):
 
 
 @pytest.mark.parametrize("hkv,grp,d,bs", [(2, 7, 64, 16), (4, 1, 128, 16), (2, 8, 128, 16), (3, 2, 64, 32),
-                                          (8, 4, 128, 32), (1, 3, 64, 16), (2, 5, 128, 16), (1, 6, 64, 16)])
+                                          (8, 4, 128, 32), (1, 3, 64, 16), (2, 5, 128, 16), (1, 6, 64, 16),
+                                          (2, 2, 64, 4), (4, 4, 128, 4), (2, 7, 64, 8), (8, 4, 128, 8)])
 def test_gqa_dims_and_block_sizes(hkv, grp, d, bs):
     lens = [1, 15, 16, 17, 300, 1000]
     q, k, v, tables, sl = _random_case(11 + grp + d + bs, len(lens), hkv, grp, d, bs, lens)

@@ -2,7 +2,7 @@
 
 Each case draws its shape from a fixed seed, so a failure names a reproducible case:
 
-* paged attention (through the C ABI): D 64/128, block 16/32, GQA 1..8, 1..24 rows of
+* paged attention (through the C ABI): D 64/128, block 4/8/16/32, GQA 1..8, 1..24 rows of
   0..2048 tokens, split granularity 0/16/64/256 tokens, tables narrower than some rows,
   rows that alias other rows' blocks (with and without ``MX_PA_SHARED_BLOCKS``) and
   strided query/output views; bar atol/rtol 1e-2 against ``decode_rows_fp32``;
@@ -34,7 +34,7 @@ MX_PA_SHARED_BLOCKS = 1
 def _attention_case(seed: int):
     rng = np.random.default_rng(5000 + seed)
     d = int(rng.choice([64, 128]))
-    bs = int(rng.choice([16, 32]))
+    bs = int(rng.choice([4, 8, 16, 16, 32]))
     grp = int(rng.integers(1, 9))
     hkv = int(rng.choice([1, 2, 4, 8]))
     bsz = int(rng.integers(1, 25))
