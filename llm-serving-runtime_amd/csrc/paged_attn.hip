@@ -469,80 +469,73 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
 
 // Log-sum-exp merge of the partials of one (kv-head, sequence); zeros for an empty row.
 // Workers seg_w[s] .. seg_w[s + 1] cut segment s, each with a partial at slot w + s.
+// Thread t owns 4 consecutive dims of one head (16-byte partial loads; m and l are shared
+// by the head's threads).
+template <int D, int G>
+constexpr int merge_threads() {
+    return ((G * D / 4 + 63) / 64) * 64;
+}
 template <int D, int BS, int G>
 __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
+    constexpr int Q = D / 4;  // 4-dim groups per head
     const int kvh = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x;
+    const bool active = tid < G * Q;
+    const int h = active ? tid / Q : 0, d = active ? (tid % Q) * 4 : 0;
     const int64_t s = (int64_t)b * p.Hkv + kvh;
     int s_eff;
     const int nt = row_tiles<BS>(p, b, s_eff);
     const int w0 = p.seg_w[2 * s], w1 = p.seg_w[2 * s + 1];
-    _Float16* out_row = p.out + (int64_t)b * p.o_sb + (int64_t)(kvh * G) * p.o_sh;
+    _Float16* out = p.out + (int64_t)b * p.o_sb + (int64_t)(kvh * G + h) * p.o_sh + d;
     if (nt == 0) {
-        for (int idx = tid; idx < G * D; idx += 256) out_row[(int64_t)(idx / D) * p.o_sh + idx % D] = (_Float16)0.0f;
+        if (active) *reinterpret_cast<half4v*>(out) = half4v{};
         return;
     }
     if (w0 == w1) return;  // one worker held the whole segment and wrote the output
-    // One online pass over the pieces, U at a time, for all EPT output elements
-    // of this thread together: every load of a batch is issued before the first
-    // is used (indices clamped, values masked), so a batch costs one memory
-    // round trip and a segment cut by at most U workers needs one batch.
+    // One online pass over the pieces, U at a time: every load of a batch is issued before
+    // the first is used (indices clamped, values masked), so a segment cut by at most U
+    // workers needs one memory round trip.
     constexpr int U = 16;
-    constexpr int EPT = (G * D + 255) / 256;
     const int np = w1 - w0 + 1;
     const float kNegInf = -__builtin_huge_valf();
-    float mg[EPT], l[EPT], a[EPT];
-    const float* mlp[EPT];
-    const float* accp[EPT];
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        const int idx = tid + e * 256 < G * D ? tid + e * 256 : G * D - 1;
-        const int h = idx / D, d = idx % D;
-        mlp[e] = p.part_ml + (((int64_t)w0 + s) * G + h) * 2;
-        accp[e] = p.part_acc + (((int64_t)w0 + s) * G + h) * D + d;
-        mg[e] = kNegInf;
-        l[e] = 0.0f;
-        a[e] = 0.0f;
-    }
+    const float* mlp = p.part_ml + (((int64_t)w0 + s) * G + h) * 2;
+    const float* accp = p.part_acc + (((int64_t)w0 + s) * G + h) * D + d;
+    float mg = kNegInf, l = 0.0f;
+    float4v a = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int i0 = 0; i0 < np; i0 += U) {
-        float mv[EPT][U], lv[EPT][U], av[EPT][U];
+        float mv[U], lv[U];
+        float4v av[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t i = i0 + u < np ? i0 + u : np - 1;
+            mv[u] = mlp[i * G * 2];
+            lv[u] = mlp[i * G * 2 + 1];
+            av[u] = *reinterpret_cast<const float4v*>(accp + i * G * D);
+        }
+        float mc = kNegInf;
 #pragma unroll
-            for (int e = 0; e < EPT; ++e) {
-                mv[e][u] = mlp[e][i * G * 2];
-                lv[e][u] = mlp[e][i * G * 2 + 1];
-                av[e][u] = accp[e][i * G * D];
+        for (int u = 0; u < U; ++u)
+            if (i0 + u < np) mc = fmaxf(mc, mv[u]);
+        const float mn = fmaxf(mg, mc);
+        if (mn == kNegInf) continue;  // only skipped tiles so far
+        const float r = exp2f(mg - mn);
+        l *= r;
+        a *= r;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (i0 + u < np) {
+                const float f = exp2f(mv[u] - mn);
+                l += f * lv[u];
+                a += f * av[u];
             }
         }
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-            float mc = kNegInf;
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (i0 + u < np) mc = fmaxf(mc, mv[e][u]);
-            const float mn = fmaxf(mg[e], mc);
-            if (mn == kNegInf) continue;  // only skipped tiles so far
-            const float r = exp2f(mg[e] - mn);
-            l[e] *= r;
-            a[e] *= r;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (i0 + u < np) {
-                    const float f = exp2f(mv[e][u] - mn);
-                    l[e] += f * lv[e][u];
-                    a[e] += f * av[e][u];
-                }
-            }
-            mg[e] = mn;
-        }
+        mg = mn;
     }
+    if (active) {
+        half4v o;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        const int idx = tid + e * 256;
-        if (idx < G * D)
-            out_row[(int64_t)(idx / D) * p.o_sh + idx % D] = (_Float16)(l[e] > 0.0f ? a[e] / l[e] : 0.0f);
+        for (int e = 0; e < 4; ++e) o[e] = (_Float16)(l > 0.0f ? a[e] / l : 0.0f);
+        *reinterpret_cast<half4v*>(out) = o;
     }
 }
 
@@ -618,7 +611,7 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     if (cap > 0 && prm.workers > cap) prm.workers = (int)(floor_workers > cap ? floor_workers : cap);
     const int blocks = (int)ceil_div(prm.workers, kWaves);
     hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM>), dim3(blocks), dim3(kWaves * 64), 0, st, prm);
-    hipLaunchKernelGGL((decode_merge_kernel<D, BS, G>), dim3(prm.Hkv, B), dim3(256), 0, st, prm);
+    hipLaunchKernelGGL((decode_merge_kernel<D, BS, G>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0, st, prm);
 }
 
 template <int D, int BS, bool STREAM>
