@@ -134,8 +134,8 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  * _paged_attn_decode_split_kernel (:245-336), _paged_attn_decode_direct_kernel
  * (:338-412) and _paged_attn_combine_kernel (:414-457).
  *
- * q:   fp16 [B, Hq, D] with strides (q_sb, q_sh, 1)      (the [B,Hq,1,D] query)
- * k,v: fp16 per-layer pool views [num_blocks, Hkv, block_size, D] with strides
+ * q:   fp16 (or bf16, MX_PA_BF16) [B, Hq, D] with strides (q_sb, q_sh, 1) (the [B,Hq,1,D] query)
+ * k,v: fp16 (bf16) per-layer pool views [num_blocks, Hkv, block_size, D] with strides
  *      (kv_sblk, kv_shead, D, 1) (GpuKVBlockPool.k_layer_view,
  *      runtime/phase2/paged_kv_kernel.py:124-134)
  * block_tables: int32 [B, max_blocks] with row stride bt_sb; entries past a
@@ -144,7 +144,7 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  *      (paged_attention_triton.py:43-50); the kernel reads
  *      min(ceil(seq_len / block_size), max_blocks) blocks; seq_len <= 0 gives
  *      a zero output row
- * out: fp16 [B, Hq, D] with strides (o_sb, o_sh, 1)
+ * out: fp16 (bf16) [B, Hq, D] with strides (o_sb, o_sh, 1)
  * num_pool_blocks: block ids outside [0, num_pool_blocks) are skipped and
  *      recorded in the workspace error word (see mx_paged_attn_error_offset)
  * chunk_tokens: split granularity. All (sequence, kv-head) tiles of 16 tokens
@@ -158,7 +158,12 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  *      the value the workspace was sized for. A
  *      second, small kernel on the same stream merges the ranges of a
  *      sequence that more than one wave touched.
- * flags: 0 or MX_PA_SHARED_BLOCKS. Without it K and V are read with the
+ * flags: an OR of MX_PA_SHARED_BLOCKS and MX_PA_BF16 (or 0).
+ *      MX_PA_BF16: q, K, V and out hold bf16 instead of fp16 (the same layouts;
+ *      scores, softmax and accumulation stay fp32, probabilities enter P.V in
+ *      bf16). The reference kernel takes the pool's dtype
+ *      (paged_attention_triton.py:500,533-535).
+ *      MX_PA_SHARED_BLOCKS: without it K and V are read with the
  *      streaming (non-temporal) cache policy, right when each block id occurs
  *      in one row of block_tables. Set it when rows alias blocks (a shared
  *      prefix): the default policy then keeps a group's repeated reads of the
@@ -171,6 +176,7 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  * a workspace. out rows must be 16-byte aligned (o_sb, o_sh multiples of 8).
  * ------------------------------------------------------------------------- */
 #define MX_PA_SHARED_BLOCKS 1u
+#define MX_PA_BF16 2u
 
 size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                      int32_t block_size, int32_t chunk_tokens);

@@ -124,6 +124,39 @@ __device__ __forceinline__ half4v load_kv4(const _Float16* p) {
         return __builtin_bit_cast(half4v, *reinterpret_cast<const u32x2v*>(p));
 }
 
+// Element type of q, K, V and the output: fp16 (BF16 = false) or bf16 (MX_PA_BF16). Registers
+// and memory hold the 16-bit patterns in half vectors either way; only the MFMA forms and the
+// fp32 conversions differ. Probabilities enter P.V rounded to the element type, as the
+// reference's SDPA path casts its softmax to the query dtype (paged_attention_triton.py:816).
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef short s16x4v __attribute__((ext_vector_type(4)));
+template <bool BF16>
+struct Elt;
+template <>
+struct Elt<false> {
+    static __device__ __forceinline__ float4v mma32(half8v a, half8v b, float4v c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float4v mma16(half4v a, half4v b, float4v c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ _Float16 round(float x) { return (_Float16)x; }
+    static __device__ __forceinline__ float widen(_Float16 x) { return (float)x; }
+};
+template <>
+struct Elt<true> {
+    static __device__ __forceinline__ float4v mma32(half8v a, half8v b, float4v c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b),
+                                                       c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float4v mma16(half4v a, half4v b, float4v c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4v, a), __builtin_bit_cast(s16x4v, b),
+                                                         c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ _Float16 round(float x) { return __builtin_bit_cast(_Float16, (__bf16)x); }
+    static __device__ __forceinline__ float widen(_Float16 x) { return (float)__builtin_bit_cast(__bf16, x); }
+};
+
 // Tiles of row b (bounded by the table width) and its effective length.
 template <int BS>
 __device__ __forceinline__ int row_tiles(const Params& p, int b, int& s_eff) {
@@ -229,7 +262,7 @@ constexpr int kDepth = MX_PA_DEPTH;
 #define MX_PA_MIN_WAVES 3
 #endif
 
-template <int D, int BS, int G, bool STREAM>
+template <int D, int BS, int G, bool STREAM, bool BF16>
 __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
     constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
@@ -369,7 +402,7 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
             const int t = t0 + j;
             float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(tr.k[kk], qf[kk], s, 0, 0, 0);
+            for (int kk = 0; kk < KK; ++kk) s = Elt<BF16>::mma32(tr.k[kk], qf[kk], s);
             // s[i] = score of token t*16 + 4g + i for head r.
             const int tok0 = t * kTile + 4 * g;
             // BPT > 1: this lane's 4 tokens lie in one block (slot vslot); a skipped block masks them.
@@ -395,8 +428,8 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
             float psum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                pv[i] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - m_run);
-                psum += (float)pv[i];
+                pv[i] = Elt<BF16>::round(__builtin_amdgcn_exp2f(sc[i] - m_run));
+                psum += Elt<BF16>::widen(pv[i]);
             }
             l_run += psum;
             // V rows past the sequence end are zeroed: p is 0 there, but stale pool
@@ -412,7 +445,7 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
 #pragma unroll
             for (int e = 0; e < DPL; ++e) {
                 const half4v a = {v[0][e], v[1][e], v[2][e], v[3][e]};
-                acc[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pv, acc[e], 0, 0, 0);
+                acc[e] = Elt<BF16>::mma16(a, pv, acc[e]);
             }
         };
 
@@ -447,7 +480,7 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
                 for (int i = 0; i < 4; ++i) {
                     VF o;
 #pragma unroll
-                    for (int e = 0; e < DPL; ++e) o[e] = (_Float16)(acc[e][i] * inv);
+                    for (int e = 0; e < DPL; ++e) o[e] = Elt<BF16>::round(acc[e][i] * inv);
                     *reinterpret_cast<VF*>(orow + (4 * g + i) * DPL) = o;
                 }
             } else {
@@ -476,7 +509,7 @@ template <int D, int G>
 constexpr int merge_threads() {
     return ((G * D / 4 + 63) / 64) * 64;
 }
-template <int D, int BS, int G>
+template <int D, int BS, int G, bool BF16>
 __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     constexpr int Q = D / 4;  // 4-dim groups per head
     const int kvh = blockIdx.x, b = blockIdx.y;
@@ -535,7 +568,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     if (active) {
         half4v o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (_Float16)(l > 0.0f ? a[e] / l : 0.0f);
+        for (int e = 0; e < 4; ++e) o[e] = Elt<BF16>::round(l > 0.0f ? a[e] / l : 0.0f);
         *reinterpret_cast<half4v*>(out) = o;
     }
 }
@@ -588,7 +621,7 @@ static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_si
 
 // Waves of this kernel instance that fit on the current device at once
 // (occupancy x CUs), cached per device; 0 if the runtime cannot say.
-template <int D, int BS, int G, bool STREAM>
+template <int D, int BS, int G, bool STREAM, bool BF16>
 static int resident_waves() {
     static int cache[64] = {0};
     int dev = 0;
@@ -596,7 +629,7 @@ static int resident_waves() {
     if (cache[dev] == 0) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_kernel<D, BS, G, STREAM>, kWaves * 64, 0) !=
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_kernel<D, BS, G, STREAM, BF16>, kWaves * 64, 0) !=
                 hipSuccess)
             return 0;
         cache[dev] = cus * per_cu * kWaves;
@@ -604,43 +637,44 @@ static int resident_waves() {
     return cache[dev];
 }
 
-template <int D, int BS, int G, bool STREAM>
+template <int D, int BS, int G, bool STREAM, bool BF16>
 static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     // More workers than resident waves would leave a second, partial round; use
     // one round unless ranges would then exceed max_range_tiles.
-    const int cap = resident_waves<D, BS, G, STREAM>();
+    const int cap = resident_waves<D, BS, G, STREAM, BF16>();
     if (cap > 0 && prm.workers > cap) prm.workers = (int)(floor_workers > cap ? floor_workers : cap);
     const int blocks = (int)ceil_div(prm.workers, kWaves);
-    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM>), dim3(blocks), dim3(kWaves * 64), 0, st, prm);
-    hipLaunchKernelGGL((decode_merge_kernel<D, BS, G>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0, st, prm);
+    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16>), dim3(blocks), dim3(kWaves * 64), 0, st, prm);
+    hipLaunchKernelGGL((decode_merge_kernel<D, BS, G, BF16>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0, st,
+                       prm);
 }
 
-template <int D, int BS, bool STREAM>
+template <int D, int BS, bool STREAM, bool BF16>
 static bool dispatch_g(int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
     switch (G) {
-        case 1: launch<D, BS, 1, STREAM>(prm, B, st, fw); return true;
-        case 2: launch<D, BS, 2, STREAM>(prm, B, st, fw); return true;
-        case 3: launch<D, BS, 3, STREAM>(prm, B, st, fw); return true;
-        case 4: launch<D, BS, 4, STREAM>(prm, B, st, fw); return true;
-        case 5: launch<D, BS, 5, STREAM>(prm, B, st, fw); return true;
-        case 6: launch<D, BS, 6, STREAM>(prm, B, st, fw); return true;
-        case 7: launch<D, BS, 7, STREAM>(prm, B, st, fw); return true;
-        case 8: launch<D, BS, 8, STREAM>(prm, B, st, fw); return true;
+        case 1: launch<D, BS, 1, STREAM, BF16>(prm, B, st, fw); return true;
+        case 2: launch<D, BS, 2, STREAM, BF16>(prm, B, st, fw); return true;
+        case 3: launch<D, BS, 3, STREAM, BF16>(prm, B, st, fw); return true;
+        case 4: launch<D, BS, 4, STREAM, BF16>(prm, B, st, fw); return true;
+        case 5: launch<D, BS, 5, STREAM, BF16>(prm, B, st, fw); return true;
+        case 6: launch<D, BS, 6, STREAM, BF16>(prm, B, st, fw); return true;
+        case 7: launch<D, BS, 7, STREAM, BF16>(prm, B, st, fw); return true;
+        case 8: launch<D, BS, 8, STREAM, BF16>(prm, B, st, fw); return true;
         default: return false;
     }
 }
 
-template <bool STREAM>
+template <bool STREAM, bool BF16>
 static bool dispatch_d_bs(int D, int BS, int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
     switch (D * 100 + BS) {
-        case 12804: return dispatch_g<128, 4, STREAM>(G, prm, B, st, fw);
-        case 12808: return dispatch_g<128, 8, STREAM>(G, prm, B, st, fw);
-        case 12816: return dispatch_g<128, 16, STREAM>(G, prm, B, st, fw);
-        case 12832: return dispatch_g<128, 32, STREAM>(G, prm, B, st, fw);
-        case 6404: return dispatch_g<64, 4, STREAM>(G, prm, B, st, fw);
-        case 6408: return dispatch_g<64, 8, STREAM>(G, prm, B, st, fw);
-        case 6416: return dispatch_g<64, 16, STREAM>(G, prm, B, st, fw);
-        case 6432: return dispatch_g<64, 32, STREAM>(G, prm, B, st, fw);
+        case 12804: return dispatch_g<128, 4, STREAM, BF16>(G, prm, B, st, fw);
+        case 12808: return dispatch_g<128, 8, STREAM, BF16>(G, prm, B, st, fw);
+        case 12816: return dispatch_g<128, 16, STREAM, BF16>(G, prm, B, st, fw);
+        case 12832: return dispatch_g<128, 32, STREAM, BF16>(G, prm, B, st, fw);
+        case 6404: return dispatch_g<64, 4, STREAM, BF16>(G, prm, B, st, fw);
+        case 6408: return dispatch_g<64, 8, STREAM, BF16>(G, prm, B, st, fw);
+        case 6416: return dispatch_g<64, 16, STREAM, BF16>(G, prm, B, st, fw);
+        case 6432: return dispatch_g<64, 32, STREAM, BF16>(G, prm, B, st, fw);
         default: return false;
     }
 }
@@ -683,7 +717,7 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     if (max_blocks < 1 || num_pool_blocks < 1)
         return fail(MX_ERR_INVALID, "mx_paged_attn_decode: max_blocks and num_pool_blocks must be >= 1");
     if (B > 65535 || Hkv > 65535) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: B or Hkv too large");
-    if (flags & ~(uint32_t)MX_PA_SHARED_BLOCKS)
+    if (flags & ~(uint32_t)(MX_PA_SHARED_BLOCKS | MX_PA_BF16))
         return fail(MX_ERR_INVALID, "mx_paged_attn_decode: unknown flags 0x%x", flags);
     if (chunk_tokens < 0 || chunk_tokens % pa::kTile != 0 || chunk_tokens > pa::kMaxChunkTokens)
         return fail(MX_ERR_INVALID, "mx_paged_attn_decode: chunk_tokens must be 0 or a multiple of 16 <= %d",
@@ -729,10 +763,13 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     // Fewest workers that keep every range within one vector of block ids.
     const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, pa::kTile),
                                 pa::max_range_tiles(block_size));
-    if (flags & MX_PA_SHARED_BLOCKS)
-        ok = pa::dispatch_d_bs<false>(D, block_size, G, prm, B, st, fw);
+    const bool shared = flags & MX_PA_SHARED_BLOCKS, bf16 = flags & MX_PA_BF16;
+    if (bf16)
+        ok = shared ? pa::dispatch_d_bs<false, true>(D, block_size, G, prm, B, st, fw)
+                    : pa::dispatch_d_bs<true, true>(D, block_size, G, prm, B, st, fw);
     else
-        ok = pa::dispatch_d_bs<true>(D, block_size, G, prm, B, st, fw);
+        ok = shared ? pa::dispatch_d_bs<false, false>(D, block_size, G, prm, B, st, fw)
+                    : pa::dispatch_d_bs<true, false>(D, block_size, G, prm, B, st, fw);
     if (!ok) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: unsupported configuration");
     return check_launch("mx_paged_attn_decode");
 }

@@ -91,8 +91,8 @@ def kv_append(k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.
     dev = k_layer.device
     if key_states.shape != value_states.shape or key_states.dim() != 4:
         raise ValueError("key_states and value_states must both be [B, Hkv, T, D]")
-    if key_states.dtype != k_layer.dtype or k_layer.dtype != torch.float16:
-        raise ValueError("kv_append supports fp16 states and pools")
+    if key_states.dtype != k_layer.dtype or k_layer.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("kv_append supports fp16 or bf16 states and pools of the same dtype")
     b, hkv, t, d = key_states.shape
     nb, hkv_p, bs, d_p = k_layer.shape
     if (hkv, d) != (hkv_p, d_p) or k_layer.stride() != v_layer.stride():

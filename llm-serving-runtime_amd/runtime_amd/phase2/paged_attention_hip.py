@@ -11,8 +11,8 @@ Differences from the reference that a caller can observe:
 
 * device tensors only: a CPU query raises ``ValueError`` instead of running a
   torch fallback (``:761-775``);
-* fp16 queries/pools only, ``head_dim`` in {64, 128}, ``block_size`` in
-  {4, 8, 16, 32}, GQA group 1..8 (``ValueError`` otherwise);
+* fp16 or bf16 queries and pools (one dtype), ``head_dim`` in {64, 128}, ``block_size``
+  in {4, 8, 16, 32}, GQA group 1..8 (``ValueError`` otherwise);
 * ``seq_len == 0`` rows produce zeros (the reference divides by zero,
   ``:238``); ``paged_attention_decode`` still rejects ``seq_len <= 0`` (``:789-790``);
 * the returned tensor is freshly allocated, never an alias of a cached buffer
@@ -41,6 +41,8 @@ if TYPE_CHECKING:
 
 _CHUNK_TOKENS = int(os.getenv("MX_PAGED_ATTN_CHUNK_TOKENS", "0"))
 MX_PA_SHARED_BLOCKS = 1
+MX_PA_BF16 = 2
+_DTYPE_FLAGS = {torch.float16: 0, torch.bfloat16: MX_PA_BF16}
 
 _decode_batch_metadata: contextvars.ContextVar["PagedDecodeBatchMetadata | None"] = contextvars.ContextVar(
     "paged_decode_batch_metadata", default=None
@@ -132,8 +134,9 @@ def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, b
     bsz, hq, q_len, d = query.shape
     if q_len != 1:
         raise ValueError("paged decode expects q_len=1")
-    if query.dtype != torch.float16 or k_layer.dtype != torch.float16 or v_layer.dtype != torch.float16:
-        raise ValueError(f"HIP paged decode supports fp16 query and pool, got {query.dtype}/{k_layer.dtype}")
+    if query.dtype not in _DTYPE_FLAGS or k_layer.dtype != query.dtype or v_layer.dtype != query.dtype:
+        raise ValueError(f"HIP paged decode supports fp16 or bf16 query and pool of one dtype, got "
+                         f"{query.dtype}/{k_layer.dtype}/{v_layer.dtype}")
     nb, hkv, bs, dk = k_layer.shape
     if tuple(v_layer.shape) != tuple(k_layer.shape) or v_layer.stride() != k_layer.stride():
         raise ValueError("K and V layer views must have the same shape and strides")
@@ -167,7 +170,8 @@ def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, b
             query.data_ptr(), query.stride(0), query.stride(1), k_layer.data_ptr(), v_layer.data_ptr(),
             k_layer.stride(0), k_layer.stride(1), block_tables.data_ptr(), block_tables.stride(0), max_blocks,
             seq_lens.data_ptr(), bsz, hq, hkv, d, bs, nb, float(scaling), out.data_ptr(), out.stride(0),
-            out.stride(1), ws.data_ptr(), nbytes, _CHUNK_TOKENS, MX_PA_SHARED_BLOCKS if shared_blocks else 0,
+            out.stride(1), ws.data_ptr(), nbytes, _CHUNK_TOKENS,
+            _DTYPE_FLAGS[query.dtype] | (MX_PA_SHARED_BLOCKS if shared_blocks else 0),
             _hip.stream_handle(query.device),
         ),
         "mx_paged_attn_decode",

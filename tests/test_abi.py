@@ -102,7 +102,7 @@ def test_invalid_arguments_return_status_codes():
     _status(call(bs=12), _hip.MX_ERR_UNSUPPORTED)
     _status(call(ct=40), _hip.MX_ERR_INVALID)
     _status(call(ct=2048), _hip.MX_ERR_INVALID)  # split granularity is at most 64 tiles
-    _status(call(flags=2), _hip.MX_ERR_INVALID)  # only MX_PA_SHARED_BLOCKS is defined
+    _status(call(flags=4), _hip.MX_ERR_INVALID)  # only MX_PA_SHARED_BLOCKS and MX_PA_BF16 are defined
     _status(call(), _hip.MX_ERR_WORKSPACE)
     _status(call(q_sh=60), _hip.MX_ERR_ALIGNMENT)
     with pytest.raises(ValueError):

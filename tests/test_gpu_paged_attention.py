@@ -175,6 +175,44 @@ def test_reference_block_size_4_shapes(seq_len):
     _check(_decode(q, k, v, tables, sl, scale, grp), oracle_out(q, k, v, tables, sl, scale, grp))
 
 
+# bf16 has 8 significant bits: rounding the output alone moves it by up to 2^-9 relative and the
+# probabilities enter P.V rounded to bf16 (2^-9 relative each), so the bar is atol = rtol = 2e-2.
+BF16_TOL = 2e-2
+
+
+@pytest.mark.parametrize("hkv,grp,d,bs,lens", [(2, 4, 64, 16, [128, 768, 1, 0]), (8, 4, 128, 16, [300, 2049, 16]),
+                                               (2, 7, 64, 32, [100, 513]), (4, 2, 128, 4, [7, 100, 37])])
+def test_bf16_pool_and_query(hkv, grp, d, bs, lens):
+    """bf16 q and pool (MX_PA_BF16): K/V written through GpuKVBlockPool.write_tokens (the bf16
+    append), decoded through paged_attention_decode_batched, against the fp32 oracle on the same
+    bf16 values."""
+    bsz = len(lens)
+    need = [math.ceil(max(s, 0) / bs) for s in lens]
+    nb = sum(need) + 3
+    g = torch.Generator().manual_seed(sum(lens) + d)
+    perm = torch.randperm(nb, generator=g)
+    pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=bs, num_layers=1, num_kv_heads=hkv, head_dim=d,
+                          dtype=torch.bfloat16, device="cuda")
+    tables = torch.zeros(bsz, max(max(need), 1), dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = perm[at:at + n].to(torch.int32)
+        at += n
+        if lens[b] > 0:
+            kv = torch.randn(2, 1, hkv, lens[b], d, generator=g).to(torch.bfloat16).cuda()
+            pool.write_tokens(0, tables[b, :n].tolist(), 0, kv[0], kv[1])
+    q = torch.randn(bsz, hkv * grp, 1, d, generator=g).to(torch.bfloat16).cuda()
+    meta = PagedDecodeBatchMetadata(pool=pool, layer_idx=0, block_tables=tables.cuda(),
+                                    seq_lens=torch.tensor(lens, dtype=torch.int32, device="cuda"))
+    scale = d**-0.5
+    out = paged_attention_decode_batched(q, meta, grp, scale)
+    assert out.dtype == torch.bfloat16
+    want = oracle_out(q, pool.k_layer_view(0), pool.v_layer_view(0), tables, lens, scale, grp)
+    np.testing.assert_allclose(out.float().cpu().numpy(), want.numpy(), atol=BF16_TOL, rtol=BF16_TOL)
+    with pytest.raises(ValueError):  # mixed dtypes are refused
+        paged_attention_decode_batched(q.half(), meta, grp, scale)
+
+
 def test_config2_full_shape_and_repeatability():
     q, k, v, tables, lens, grp, scale = _config2()
     got = _decode(q, k, v, tables, lens, scale, grp)

@@ -4,8 +4,9 @@ Each case draws its shape from a fixed seed, so a failure names a reproducible c
 
 * paged attention (through the C ABI): D 64/128, block 4/8/16/32, GQA 1..8, 1..24 rows of
   0..2048 tokens, split granularity 0/16/64/256 tokens, tables narrower than some rows,
-  rows that alias other rows' blocks (with and without ``MX_PA_SHARED_BLOCKS``) and
-  strided query/output views; bar atol/rtol 1e-2 against ``decode_rows_fp32``;
+  rows that alias other rows' blocks (with and without ``MX_PA_SHARED_BLOCKS``),
+  strided query/output views and bf16 (``MX_PA_BF16``); bar atol/rtol 1e-2 (2e-2 in bf16)
+  against ``decode_rows_fp32``;
 * int8 linear: N = 16..6400, K = 64..4096, M = 1..300 (chunks of 128 rows past that),
   strided x, with and without bias; bar atol/rtol 1e-2 against ``linear_ref_fp32``, and
   where K is split the partials summed bias-first in split order equal the output bit
@@ -29,6 +30,8 @@ pytestmark = pytest.mark.gpu
 ATOL = 1e-2
 RTOL = 1e-2
 MX_PA_SHARED_BLOCKS = 1
+MX_PA_BF16 = 2
+BF16_TOL = 2e-2  # 8 significant bits: output and probabilities rounded to bf16 (2^-9 relative each)
 
 
 def _attention_case(seed: int):
@@ -47,7 +50,8 @@ def _attention_case(seed: int):
         width = max(1, width - int(rng.integers(1, 4)))  # some rows run past the table
     chunk = int(rng.choice([0, 0, 16, 64, 256]))
     return dict(d=d, bs=bs, grp=grp, hkv=hkv, lens=[int(s) for s in lens], need=need, width=width, chunk=chunk,
-                alias=bool(rng.random() < 0.4), strided=bool(rng.random() < 0.3), rng=rng)
+                alias=bool(rng.random() < 0.4), strided=bool(rng.random() < 0.3), bf16=bool(rng.random() < 0.3),
+                rng=rng)
 
 
 @pytest.mark.parametrize("seed", range(48))
@@ -70,15 +74,16 @@ def test_attention_randomized(seed):
             m = min(share, c["need"][b], width)
             tables[b, :m] = tables[0, :m]
     g = torch.Generator().manual_seed(seed)
-    k = torch.randn(nb, hkv, bs, d, generator=g).to(torch.float16).cuda()
-    v = torch.randn(nb, hkv, bs, d, generator=g).to(torch.float16).cuda()
+    dt = torch.bfloat16 if c["bf16"] else torch.float16
+    k = torch.randn(nb, hkv, bs, d, generator=g).to(dt).cuda()
+    v = torch.randn(nb, hkv, bs, d, generator=g).to(dt).cuda()
     if c["strided"]:
-        qbig = torch.randn(bsz, hq + 3, 1, d + 8, generator=g).to(torch.float16).cuda()
+        qbig = torch.randn(bsz, hq + 3, 1, d + 8, generator=g).to(dt).cuda()
         q = qbig[:, 2:2 + hq, :, 8:]
-        out_big = torch.full((bsz, hq + 1, 1, d + 16), float("nan"), dtype=torch.float16, device="cuda")
+        out_big = torch.full((bsz, hq + 1, 1, d + 16), float("nan"), dtype=dt, device="cuda")
         out = out_big[:, 1:, :, 16:]
     else:
-        q = torch.randn(bsz, hq, 1, d, generator=g).to(torch.float16).cuda()
+        q = torch.randn(bsz, hq, 1, d, generator=g).to(dt).cuda()
         out = torch.empty_like(q)
     tables_d = torch.from_numpy(tables).cuda()
     lens_d = torch.tensor(lens, dtype=torch.int32, device="cuda")
@@ -86,9 +91,9 @@ def test_attention_randomized(seed):
     lib = _hip.load()
     nbytes = lib.mx_paged_attn_workspace_bytes(bsz, hq, hkv, d, width, bs, c["chunk"])
     ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
-    flags = MX_PA_SHARED_BLOCKS if c["alias"] and seed % 2 == 0 else 0
+    flags = (MX_PA_SHARED_BLOCKS if c["alias"] and seed % 2 == 0 else 0) | (MX_PA_BF16 if c["bf16"] else 0)
     print(f"[attn] seed {seed}: B {bsz} Hq {hq} Hkv {hkv} D {d} bs {bs} width {width} chunk {c['chunk']} "
-          f"alias {c['alias']} strided {c['strided']} flags {flags} lens {lens}", flush=True)
+          f"alias {c['alias']} strided {c['strided']} bf16 {c['bf16']} flags {flags} lens {lens}", flush=True)
     _hip.check(lib.mx_paged_attn_decode(
         q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
         tables_d.data_ptr(), tables_d.stride(0), width, lens_d.data_ptr(), bsz, hq, hkv, d, bs, nb, scale,
@@ -98,7 +103,8 @@ def test_attention_randomized(seed):
     err = int(ws[lib.mx_paged_attn_error_offset(bsz, hq, hkv, d, width, bs, c["chunk"]):][:4].view(torch.int32).item())
     assert err == 0
     want = oracle_pa.decode_rows_fp32(q.cpu(), k.cpu(), v.cpu(), tables_d.cpu(), lens, scale, grp)
-    np.testing.assert_allclose(out.float().cpu().numpy(), want.numpy(), atol=ATOL, rtol=RTOL)
+    tol = BF16_TOL if c["bf16"] else ATOL
+    np.testing.assert_allclose(out.float().cpu().numpy(), want.numpy(), atol=tol, rtol=tol)
     if c["strided"]:  # nothing outside the output view was written
         assert torch.isnan(out_big[:, :1]).all() and torch.isnan(out_big[:, 1:, :, :16]).all()
 
