@@ -141,3 +141,74 @@ def test_greedy_qwen2_two_layers_all_rows():
 @pytest.mark.timeout(900)
 def test_greedy_qwen2_config3():
     _check(_case(layers=24, batch=16, lo=512, hi=2048, seed=0))
+
+
+@pytest.mark.timeout(600)
+def test_greedy_bf16_model_through_the_hook():
+    """An unquantized HF Qwen2 (2 layers, config-3 widths, 32768-token vocabulary) in bf16: the
+    block_paged hook, the cache adapters and a bf16 pool (MX_PA_BF16 decode, bf16 K/V append).
+    Oracle: the same weights in fp32 on the CPU, teacher-forced on the device's tokens;
+    yardstick: torch's own bf16 path (eager attention) on the GPU. Per row, the rules of the
+    int8 cases (logits within max(1e-2, 1.25 x torch bf16's error), mismatches only at near
+    ties). bf16 logits are ~8x coarser than fp16 ones (~4e-2 here), so near ties are too: the
+    aggregate bound is the larger of 2 % of the steps and 2 x (torch bf16's own argmax
+    disagreements with the oracle on the same prefixes) + 2, not the fp16 cases' 2 %."""
+    from runtime_amd.phase2 import block_paged_attention as bpa
+    from runtime_amd.phase2.hf_decode import enable_block_paged_attention, greedy_decode
+    from runtime_amd.phase2.paged_attention_hip import workspace_error_flag
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    device = torch.device("cuda:0")
+    steps, batch = 16, 6
+    model = om.random_qwen2(seed=11, num_hidden_layers=2, vocab_size=32768)
+    cfg = model.config
+    ref = copy.deepcopy(model).eval()
+    yard = copy.deepcopy(model).to(device=device, dtype=torch.bfloat16).eval()
+    model.to(device=device, dtype=torch.bfloat16)
+    enable_block_paged_attention(model)
+    g = torch.Generator().manual_seed(11)
+    lens = torch.randint(40, 160, (batch,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g) for n in lens]
+    need = [math.ceil((n + steps) / BLOCK_SIZE) for n in lens]
+    perm = torch.randperm(2 * sum(need), generator=g).tolist()
+    rows, at = [], 0
+    for n in need:
+        rows.append(perm[at:at + n])
+        at += n
+    pool = GpuKVBlockPool(num_blocks=2 * sum(need), block_size_tokens=BLOCK_SIZE, num_layers=2,
+                          num_kv_heads=cfg.num_key_value_heads, head_dim=cfg.hidden_size // cfg.num_attention_heads,
+                          dtype=torch.bfloat16, device=device)
+    calls = {"n": 0}
+    hip_decode = bpa.paged_attention_decode_batched
+
+    def counting(*args, **kwargs):
+        calls["n"] += 1
+        return hip_decode(*args, **kwargs)
+
+    bpa.paged_attention_decode_batched = counting
+    try:
+        tokens, logits = greedy_decode(model, pool, prompts, rows, steps, keep_logits=True)
+        torch.cuda.synchronize()
+    finally:
+        bpa.paged_attention_decode_batched = hip_decode
+    assert calls["n"] == steps * 2, "decode attention did not go through the HIP kernel"
+    assert workspace_error_flag(device) == 0
+    tokens = tokens.cpu()
+    results = []
+    for b in range(batch):
+        ref_logits = om.teacher_forced_logits(ref, prompts[b], tokens[b])
+        ids = torch.cat([prompts[b], tokens[b][:-1]]).view(1, -1).to(device)
+        with torch.no_grad():
+            tb = yard(input_ids=ids, use_cache=False, logits_to_keep=steps + 1).logits[0].float().cpu()
+        err = float((logits[b].float().cpu() - ref_logits).abs().max())
+        errb = float((tb - ref_logits).abs().max())
+        allowed = max(LOGIT_ATOL, YARDSTICK_SLACK * errb)
+        agree = om.greedy_agreement(ref_logits, tokens[b], tie_tol=2 * allowed)
+        yard_miss = int((tb.argmax(dim=-1) != ref_logits.argmax(dim=-1)).sum())
+        print(f"[bf16] row {b} prompt {lens[b]}: max|dL| hip {err:.3e} torch bf16 {errb:.3e}, "
+              f"mismatches {agree['mismatches']}/{agree['steps']} (torch bf16 {yard_miss})", flush=True)
+        assert err <= allowed, f"row {b}: logits off by {err:.3e} (torch bf16: {errb:.3e})"
+        assert agree["ties_ok"], f"row {b}: a mismatch outside the near-tie band {agree}"
+        results.append((agree["mismatches"], agree["steps"], yard_miss))
+    ties, total, yard = (sum(r[i] for r in results) for i in range(3))
+    assert ties <= max(MAX_TIE_FRACTION * total, 2 * yard + 2), f"{ties} near ties in {total} steps (torch bf16 {yard})"
