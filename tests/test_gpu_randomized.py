@@ -3,8 +3,9 @@
 Each case draws its shape from a fixed seed, so a failure names a reproducible case:
 
 * paged attention (through the C ABI): D 64/128, block 4/8/16/32, GQA 1..8, 1..24 rows of
-  0..2048 tokens, split granularity 0/16/64/256 tokens, tables narrower than some rows,
-  rows that alias other rows' blocks (with and without ``MX_PA_SHARED_BLOCKS``),
+  0..2048 tokens or 65..100 rows of 0..300 tokens, split granularity 0/16/64/256 tokens,
+  tables narrower than some rows, rows that alias other rows' blocks (with and without
+  ``MX_PA_SHARED_BLOCKS``),
   strided query/output views and bf16 (``MX_PA_BF16``); bar atol/rtol 1e-2 (2e-2 in bf16)
   against ``decode_rows_fp32``;
 * int8 linear: N = 16..6400, K = 64..4096, M = 1..300 (chunks of 128 rows past that),
@@ -40,8 +41,12 @@ def _attention_case(seed: int):
     bs = int(rng.choice([4, 8, 16, 16, 32]))
     grp = int(rng.integers(1, 9))
     hkv = int(rng.choice([1, 2, 4, 8]))
-    bsz = int(rng.integers(1, 25))
-    lens = rng.integers(0, 2049, size=bsz)
+    if rng.random() < 0.2:  # more than 64 rows: the kernel's multi-pass row search
+        bsz = int(rng.integers(65, 101))
+        lens = rng.integers(0, 300, size=bsz)
+    else:
+        bsz = int(rng.integers(1, 25))
+        lens = rng.integers(0, 2049, size=bsz)
     lens[rng.random(bsz) < 0.15] = 0
     lens[rng.random(bsz) < 0.15] = bs * rng.integers(1, 8)  # exact block multiples
     need = [math.ceil(int(s) / bs) for s in lens]
