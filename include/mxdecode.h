@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 9
+#define MX_ABI_VERSION 10
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -119,8 +119,10 @@ int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t M, int64_t 
  * 8t + [0, 8) (scale and bias reordered the same way), quantized and packed
  * as usual. Replaces transformers' act_fn(gate_proj(x)) * up_proj(x) (reached
  * from worker_server.py:771-775) with one launch and half the output bytes.
- * Rows are processed 128 at a time; the shape must not split K
- * (mx_w8a16_splits(min(M, 128), 2I, K) == 1, true for every M when it holds at M = 128). */
+ * Rows are processed 128 at a time, each chunk with mx_w8a16_linear's plan
+ * (the VALU GEMV at M <= 4 on shapes that split, else the MFMA kernel); a chunk
+ * whose MFMA launch would split K is refused (MX_ERR_UNSUPPORTED): the call
+ * needs mx_w8a16_splits(c, 2I, K) == 1 for every chunk size c of M. */
 int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                            const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I, int64_t y_stride,
                            void* stream);
@@ -215,11 +217,15 @@ size_t mx_paged_attn_error_offset(int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
  * start_pos[b] + t, i.e. block block_tables[b, pos / block_size] at offset
  * pos % block_size. Replaces write_tokens_batch (paged_kv_kernel.py:176-227;
  * the reference loops over tokens on the host and checks bounds with host
- * syncs, :217-227). D % 8 == 0; rows 16-byte aligned. */
+ * syncs, :217-227). D % 8 == 0; rows 16-byte aligned. used_blocks (nullable,
+ * uint8 [num_pool_blocks]) gets 1 at every physical block a token was written
+ * to: the block-usage accounting of the reference's _touch_blocks (:229-231)
+ * kept on the device, read only when the caller asks. */
 int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_t new_sb, int64_t new_sh, int64_t new_st,
                  int32_t B, int32_t T, int32_t Hkv, int32_t D, const int32_t* block_tables, int64_t bt_sb,
                  int32_t max_blocks, const int32_t* start_pos, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk,
-                 int64_t kv_shead, int32_t block_size, int32_t num_pool_blocks, int32_t* err, void* stream);
+                 int64_t kv_shead, int32_t block_size, int32_t num_pool_blocks, int32_t* err, uint8_t* used_blocks,
+                 void* stream);
 
 /* From one fused QKV projection row per sequence (fp16 [B, (Hq + 2*Hkv) * D],
  * row stride qkv_stride; heads in the order q, k, v): rotate q and k with

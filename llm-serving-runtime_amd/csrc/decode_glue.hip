@@ -65,6 +65,7 @@ struct AppendParams {
     int64_t sblk, shead;
     int bs, num_pool_blocks;
     int32_t* err;
+    uint8_t* used;  // optional [num_pool_blocks] map: 1 where a token was written
 };
 
 // One thread per 8-element chunk of one (row, token, kv-head); K and V share the slot.
@@ -87,6 +88,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendParams p, int
     const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)t * p.st + c * 8;
     st16(p.k_pool + dst + c * 8, ld16(p.k_new + src));
     st16(p.v_pool + dst + c * 8, ld16(p.v_new + src));
+    // Block-usage accounting (GpuKVBlockPool.allocated_block_count) without a host sync.
+    if (p.used && c == 0 && h == 0) p.used[p.bt[(int64_t)b * p.bt_sb + (p.start[b] + t) / p.bs]] = 1;
 }
 
 struct RopeAppendParams {
@@ -461,7 +464,7 @@ extern "C" int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_
                             int64_t new_st, int32_t B, int32_t T, int32_t Hkv, int32_t D, const int32_t* block_tables,
                             int64_t bt_sb, int32_t max_blocks, const int32_t* start_pos, uint16_t* k_pool,
                             uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead, int32_t block_size,
-                            int32_t num_pool_blocks, int32_t* err, void* stream) {
+                            int32_t num_pool_blocks, int32_t* err, uint8_t* used_blocks, void* stream) {
     clear_error();
     if (B < 0 || T < 0) return fail(MX_ERR_INVALID, "mx_kv_append: B and T must be >= 0 (B=%d T=%d)", B, T);
     if (B == 0 || T == 0) return MX_OK;
@@ -475,7 +478,8 @@ extern "C" int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_
         !glue::a16(v_new) || !glue::a16(k_pool) || !glue::a16(v_pool))
         return fail(MX_ERR_ALIGNMENT, "mx_kv_append: states and pool need 16-byte aligned rows");
     glue::AppendParams p{k_new, v_new, new_sb, new_sh, new_st, T, Hkv, D, block_tables, bt_sb, max_blocks,
-                         start_pos, k_pool, v_pool, kv_sblk, kv_shead, block_size, num_pool_blocks, err};
+                         start_pos, k_pool, v_pool, kv_sblk, kv_shead, block_size, num_pool_blocks, err,
+                         used_blocks};
     const int64_t total = (int64_t)B * T * Hkv * (D / 8);
     hipLaunchKernelGGL(glue::kv_append_kernel, dim3((unsigned)ceil_div(total, glue::kThreads)), dim3(glue::kThreads),
                        0, as_stream(stream), p, total);

@@ -429,6 +429,9 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 pv[i] = Elt<BF16>::round(__builtin_amdgcn_exp2f(sc[i] - m_run));
+                // BPT > 1: every block of a tile may be outside the pool while m_run is still
+                // -inf; exp2(-inf - -inf) is NaN, so masked scores give p = 0 explicitly.
+                if constexpr (BPT > 1) pv[i] = sc[i] == kNegInf ? (_Float16)0.0f : pv[i];
                 psum += Elt<BF16>::widen(pv[i]);
             }
             l_run += psum;

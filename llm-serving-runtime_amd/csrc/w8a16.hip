@@ -97,7 +97,12 @@ struct Stage {
 };
 
 // GEMV on the VALU for small M (v_dot2_f32_f16 against exact fp16 weights).
-template <int M, int WAVES, int P>
+// GU: the gate||up projection with SwiGLU in the epilogue (interleaved rows, as the MFMA
+// kernel's GU): the pair of rows r and r + 8 of an n-tile are gate and up channel
+// 8*nt + r; y is [M, N/2] and receives fp16(fp16(silu(g)) * u) with g and u rounded to
+// fp16 exactly as this kernel's plain epilogue rounds them. This covers gate||up shapes
+// whose MFMA launch would split K (the Qwen2-0.5B MLP) at M <= 4.
+template <int M, int WAVES, int P, bool GU = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* __restrict__ x, int64_t xs,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
@@ -150,6 +155,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
         for (int m = 0; m < M; ++m) red[wave][m][r] = acc[m];
     }
     __syncthreads();
+    // M * kTileN <= 64 threads: all in wave 0, so the GU lane swap below stays in one wave.
     if (threadIdx.x < M * kTileN) {
         const int m = threadIdx.x / kTileN, rr = threadIdx.x % kTileN;
         float s = 0.0f;
@@ -158,7 +164,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
         const int64_t n = (int64_t)nt * kTileN + rr;
         float v = s * h2f(scale, n);
         if (bias) v += h2f(bias, n);
-        y[m * ys + n] = f2h_bits(v);
+        if constexpr (!GU) {
+            y[m * ys + n] = f2h_bits(v);
+        } else {
+            const float vh = (float)(_Float16)pin_f32(v);  // this lane's projection as fp16
+            const float other = __shfl_xor(vh, 8);         // lane rr ^ 8: the matching up channel
+            if (rr < 8) {
+                const _Float16 sg = (_Float16)silu_f32(vh);
+                y[m * ys + (int64_t)nt * (kTileN / 2) + rr] = f2h_bits((float)sg * other);
+            }
+        }
     }
 }
 
@@ -513,11 +528,22 @@ static size_t workspace_for(int M, int NT, int KT) {
     return pl.KS > 1 ? (size_t)pl.KS * M * NT * kTileN * sizeof(float) : 0;
 }
 
-template <int M>
+template <int M, bool GU = false>
 static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_valu_kernel<M, kGemvWaves, gemv_depth(M)>), dim3(NT), dim3(kGemvWaves * 64), 0, st, x,
-                       xs, w, s, b, y, ys, KT);
+    hipLaunchKernelGGL((gemv_valu_kernel<M, kGemvWaves, gemv_depth(M), GU>), dim3(NT), dim3(kGemvWaves * 64), 0, st,
+                       x, xs, w, s, b, y, ys, KT);
+}
+
+template <bool GU = false>
+static void launch_gemv_m(int M, const uint16_t* x, int64_t xs, const uint8_t* w, const uint16_t* s,
+                          const uint16_t* b, uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
+    switch (M) {
+        case 1: launch_gemv<1, GU>(x, xs, w, s, b, y, ys, NT, KT, st); break;
+        case 2: launch_gemv<2, GU>(x, xs, w, s, b, y, ys, NT, KT, st); break;
+        case 3: launch_gemv<3, GU>(x, xs, w, s, b, y, ys, NT, KT, st); break;
+        default: launch_gemv<4, GU>(x, xs, w, s, b, y, ys, NT, KT, st); break;
+    }
 }
 
 // Workgroup shape of an unsplit launch at M <= 64: about one workgroup per CU,
@@ -676,12 +702,7 @@ extern "C" int mx_w8a16_linear(const uint16_t* x, int64_t M, int64_t K, int64_t 
         // Split-K needs the caller's workspace; without enough of it run unsplit.
         if (pl.KS > 1 && (!workspace || workspace_bytes < w8a16::workspace_for(mc, NT, KT))) pl.KS = pl.KW = 1;
         if (pl.valu) {
-            switch (mc) {
-                case 1: w8a16::launch_gemv<1>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
-                case 2: w8a16::launch_gemv<2>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
-                case 3: w8a16::launch_gemv<3>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
-                default: w8a16::launch_gemv<4>(xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st); break;
-            }
+            w8a16::launch_gemv_m(mc, xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st);
         } else {
             w8a16::launch_mfma_mt(pl.MT, xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, pl.KS, pl.KW, partial,
                                   st);
@@ -795,16 +816,27 @@ extern "C" int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, i
     const int NT = (int)(2 * I / w8a16::kTileN), KT = (int)(K / w8a16::kTileK);
     if ((int64_t)NT * w8a16::kTileN != 2 * I || K * 64 > 0x7fffffff)
         return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: bad shape");
-    if (w8a16::splits_for(NT, KT) != 1)
-        return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: shape splits K (mx_w8a16_splits(M, 2I, K) = %d)",
-                    w8a16::splits_for(NT, KT));
+    // Rows in chunks of at most kMaxRows, as mx_w8a16_linear, each with that entry's plan: the
+    // VALU GEMV (M <= 4 on shapes that split) or an unsplit MFMA launch. A chunk whose MFMA
+    // launch would split K cannot take the epilogue (mx_w8a16_splits(chunk, 2I, K) > 1).
+    for (int64_t m0 = 0; m0 < M; m0 += w8a16::kMaxRows) {
+        const int mc = (int)(M - m0 < w8a16::kMaxRows ? M - m0 : w8a16::kMaxRows);
+        const w8a16::Plan pl = w8a16::plan_for(mc, NT, KT);
+        if (!pl.valu && pl.KS != 1)
+            return fail(MX_ERR_UNSUPPORTED, "mx_w8a16_gateup_swiglu: shape splits K at %d rows "
+                                            "(mx_w8a16_splits(%d, 2I, K) = %d)", mc, mc, pl.KS);
+    }
     hipStream_t st = as_stream(stream);
-    // Rows in chunks of at most kMaxRows (the MFMA kernel's largest m-tile count), as mx_w8a16_linear.
     for (int64_t m0 = 0; m0 < M; m0 += w8a16::kMaxRows) {
         const int mc = (int)(M - m0 < w8a16::kMaxRows ? M - m0 : w8a16::kMaxRows);
         const uint16_t* xc = x + m0 * x_stride;
         uint16_t* yc = y + m0 * y_stride;
-        switch (w8a16::mt_for(mc)) {
+        const w8a16::Plan pl = w8a16::plan_for(mc, NT, KT);
+        if (pl.valu) {
+            w8a16::launch_gemv_m<true>(mc, xc, x_stride, packed, scale, bias, yc, y_stride, NT, KT, st);
+            continue;
+        }
+        switch (pl.MT) {
             case 1: w8a16::launch_mfma<1, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
             case 2: w8a16::launch_mfma<2, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;
             case 3: w8a16::launch_mfma<3, false, true>(xc, x_stride, mc, packed, scale, bias, yc, y_stride, NT, KT, 1, 1, nullptr, st); break;

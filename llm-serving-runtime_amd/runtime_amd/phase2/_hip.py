@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -54,7 +54,7 @@ SIGNATURES = {
     "mx_kv_append": (
         ctypes.c_int,
         [_p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _i64, _i32, _p, _p, _p, _i64, _i64, _i32, _i32, _p,
-         _p],
+         _p, _p],
     ),
     "mx_qkv_rope_append": (
         ctypes.c_int,

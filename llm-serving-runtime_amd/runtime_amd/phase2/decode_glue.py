@@ -80,12 +80,14 @@ def rope_table(max_pos: int, head_dim: int, theta: float, device: torch.device |
 
 
 def kv_append(k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor, start_pos: torch.Tensor,
-              key_states: torch.Tensor, value_states: torch.Tensor, err: torch.Tensor | None = None) -> None:
+              key_states: torch.Tensor, value_states: torch.Tensor, err: torch.Tensor | None = None,
+              used_blocks: torch.Tensor | None = None) -> None:
     """Write ``key/value_states [B, Hkv, T, D]`` at positions ``start_pos[b] + t`` of each row.
 
     ``k_layer``/``v_layer`` are per-layer pool views ``[num_blocks, Hkv, bs, D]``.
     Slots outside the table or the pool are skipped and flagged in ``err``
-    (an int32 device word, OR-ed with 1) when given.
+    (an int32 device word, OR-ed with 1) when given. ``used_blocks`` (uint8
+    ``[num_blocks]``, optional) gets 1 at every block a token was written to.
     """
     _hip.require_device_tensor(key_states, "key_states")
     dev = k_layer.device
@@ -106,12 +108,16 @@ def kv_append(k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.
     if tables.dim() != 2 or tables.shape[0] != b:
         raise ValueError("block_tables must be [B, max_blocks]")
     starts = _i32(start_pos.reshape(-1), dev)
+    if used_blocks is not None and (used_blocks.dtype != torch.uint8 or used_blocks.numel() < nb
+                                    or not used_blocks.is_contiguous() or used_blocks.device != dev):
+        raise ValueError("used_blocks must be a contiguous uint8 device tensor of num_blocks entries")
     lib = _hip.load()
     _hip.check(lib.mx_kv_append(
         key_states.data_ptr(), value_states.data_ptr(), key_states.stride(0), key_states.stride(1),
         key_states.stride(2), b, t, hkv, d, tables.data_ptr(), tables.stride(0), int(tables.shape[1]),
         starts.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), bs, nb,
-        err.data_ptr() if err is not None else None, _hip.stream_handle(dev)), "mx_kv_append")
+        err.data_ptr() if err is not None else None, used_blocks.data_ptr() if used_blocks is not None else None,
+        _hip.stream_handle(dev)), "mx_kv_append")
 
 
 def qkv_rope_append(qkv: torch.Tensor, rope: torch.Tensor, positions: torch.Tensor, q_out: torch.Tensor,

@@ -37,10 +37,10 @@ Llama / Qwen2 style (pre-norm, rotate-half RoPE, GQA, SwiGLU, untied int8
 lm_head); :meth:`Int8DecodeModel.from_hf` loads the weights of an HF
 ``LlamaForCausalLM`` / ``Qwen2ForCausalLM``. The gate||up weight is stored
 with gate and up rows interleaved in groups of 8 (``gateup_interleave``);
-where the fused epilogue does not apply, ``mx_swiglu_interleaved`` forms the
-product from the projection's split-K partials (a gate||up GEMM that splits K,
-e.g. Qwen2-0.5B at batch 16) or from its fp16 output (the VALU GEMV, which
-takes batches of at most 4 rows on shapes that split).
+where the fused epilogue does not apply (a gate||up GEMM that splits K, e.g.
+Qwen2-0.5B at batch 16), ``mx_swiglu_interleaved`` forms the product from the
+projection's split-K partials. At batches of at most 4 rows on such shapes the
+VALU GEMV takes the projection, with the SwiGLU product in its own epilogue.
 """
 
 from __future__ import annotations
@@ -52,7 +52,7 @@ import torch
 
 from .decode_glue import (QKV_ROPE_MAX_ROWS, add_rmsnorm, add_rmsnorm_splits, argmax_rows, qkv_linear_rope_append,
                           qkv_rope_append, qkv_rope_append_splits, rope_table, swiglu_interleaved)
-from .int8_linear import (gateup_interleave, int8_gateup_swiglu, int8_linear,
+from .int8_linear import (gateup_fusable, gateup_interleave, int8_gateup_swiglu, int8_linear,
                           int8_linear_partials, linear_splits, pack_weight, quantize_weight)
 from .paged_attention_hip import _decode as _paged_decode
 
@@ -109,6 +109,7 @@ class _Buffers:
     logits: torch.Tensor  # [B, vocab]
     part: torch.Tensor    # fp32 split partials of the current split projection
     splits: dict          # projection name -> K splits at this batch size
+    gate_up_fused: bool   # gate||up with the SwiGLU epilogue in one launch (int8_gateup_swiglu)
     attn_lens: torch.Tensor  # int32 [B]
     next: torch.Tensor    # int64 [B], greedy tokens
     err: torch.Tensor     # int32 [1], OR of the append kernels' error bits
@@ -178,6 +179,13 @@ class Int8DecodeModel:
         head_dim = int(getattr(cfg, "head_dim", None) or cfg.hidden_size // heads)
         rope = getattr(cfg, "rope_parameters", None) or {}
         theta = float(rope.get("rope_theta", getattr(cfg, "rope_theta", 10000.0)))
+        # The (cos, sin) table is transformers' default rotary embedding; a scaled variant
+        # (llama3, yarn, linear, dynamic, ...) would load and decode with wrong phases.
+        scaling = getattr(cfg, "rope_scaling", None) or {}
+        for spec in (rope, scaling):
+            kind = spec.get("rope_type", spec.get("type", "default")) if isinstance(spec, dict) else "default"
+            if kind not in (None, "default"):
+                raise ValueError(f"from_hf supports the default rotary embedding only, got rope_type={kind!r}")
         attn0 = model.model.layers[0].self_attn
         shape = DecoderShape(hidden=int(cfg.hidden_size), layers=int(cfg.num_hidden_layers), heads=heads,
                              kv_heads=int(cfg.num_key_value_heads), head_dim=head_dim,
@@ -238,14 +246,15 @@ class Int8DecodeModel:
                       "gate_up": (2 * s.intermediate, s.hidden), "down": (s.hidden, s.intermediate),
                       "lm_head": (s.vocab, s.hidden)}
             splits = {k: linear_splits(batch, n, kk) for k, (n, kk) in shapes.items()}
-            # The fused gate||up runs rows 128 at a time and needs an unsplit chunk.
-            splits["gate_up_chunk"] = linear_splits(min(batch, 128), *shapes["gate_up"])
+            # The fused gate||up (SwiGLU epilogue) runs rows 128 at a time and needs no chunk split.
+            gate_up_fused = gateup_fusable(batch, *shapes["gate_up"])
             part_elems = max([splits[k] * batch * shapes[k][0] for k in shapes if splits[k] > 1] + [4])
             buf = _Buffers(h=e(batch, s.hidden), x=e(batch, s.hidden), qkv=e(batch, s.qkv_out),
                            q=e(batch, s.heads * s.head_dim), attn=e(batch, s.heads, 1, s.head_dim),
                            o=e(batch, s.hidden), gu=e(batch, 2 * s.intermediate), act=e(batch, s.intermediate),
                            mlp=e(batch, s.hidden), logits=e(batch, s.vocab),
                            part=torch.empty(part_elems, dtype=torch.float32, device=dev), splits=splits,
+                           gate_up_fused=gate_up_fused,
                            attn_lens=torch.zeros(batch, dtype=torch.int32, device=dev),
                            next=torch.zeros(batch, dtype=torch.int64, device=dev),
                            err=torch.zeros(1, dtype=torch.int32, device=dev))
@@ -333,7 +342,7 @@ class Int8DecodeModel:
         """act = silu(gate) * up from the interleaved gate||up weight."""
         packed, scale, n, bias = w
         ev = self._tick(timers, "gate_up")
-        if buf.splits["gate_up_chunk"] == 1:
+        if buf.gate_up_fused:
             int8_gateup_swiglu(buf.x, packed, scale, bias, n // 2, out=buf.act)
         elif buf.splits["gate_up"] > 1:  # split over K: the SwiGLU consumer sums the partials
             int8_linear_partials(buf.x, packed, scale, n, buf.part)

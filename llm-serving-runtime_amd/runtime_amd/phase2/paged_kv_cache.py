@@ -360,16 +360,28 @@ class BlockPagedBatchCache(Cache):
         return dense, slots
 
     def write_back_dense(self, dense: "BlockPagedBatchCache", slots: list[int]) -> None:
-        """Copy lengths and tables of a dense decode back into the persistent slots."""
-        lens = dense.seq_lens.tolist()
-        for i, slot in enumerate(slots):
-            self.sync_block_ids_row(slot, list(dense.block_ids_rows[i]))
-            self._set_row_length(slot, lens[i])
+        """Copy lengths and tables of a dense decode back into the persistent slots.
 
-    def extract_cache(self, index: int) -> BlockPagedCache:
+        The lengths move device to device (one ``index_copy_`` per length tensor, no host
+        read; the reference reads each row's length back per layer, ``:389-396``), and a
+        table row is re-uploaded only when its block ids changed.
+        """
+        index = torch.tensor(slots, dtype=torch.long).to(self.seq_lens.device)
+        lens = dense.seq_lens.to(self.seq_lens.dtype)
+        self.seq_lens.index_copy_(0, index, lens)
+        for layer in self.layers:
+            layer._row_seq_lens.index_copy_(0, index, lens)
+        for i, slot in enumerate(slots):
+            if self.block_ids_rows[slot] != dense.block_ids_rows[i]:
+                self.sync_block_ids_row(slot, list(dense.block_ids_rows[i]))
+
+    def extract_cache(self, index: int, seq_len: int | None = None) -> BlockPagedCache:
+        """A batch-1 cache over slot ``index``. ``seq_len``, when the caller knows it (a decode
+        step adds one token per row), saves reading the length back from the device."""
         cache = BlockPagedCache(self._config, self.pool)
         cache.set_block_ids(self.block_ids_rows[index])
-        seq_len = int(self.seq_lens[index].item())
+        if seq_len is None:
+            seq_len = int(self.seq_lens[index].item())
         for layer in cache.layers:
             layer.set_seq_length(seq_len)
         return cache

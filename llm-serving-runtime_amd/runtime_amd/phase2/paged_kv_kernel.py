@@ -23,8 +23,16 @@ MI355X-first differences:
   whole slab on every growth (``:86-115``). Here the first use allocates all
   ``num_blocks`` at once (288 GB of HBM per GPU makes that the cheap choice),
   so tensor addresses never change after ``_ensure_pools`` and a captured HIP
-  graph stays valid. Block usage accounting (``allocated_block_count`` /
-  ``peak_allocated_block_count``) is unchanged.
+  graph stays valid.
+* ``write_tokens_batch`` on a device pool makes no host round trip. The
+  reference checks the table bounds with ``.item()`` and records the written
+  blocks with ``unique().tolist()`` on every call (``:221,229-231``), four
+  syncs per layer per step. Here the one ``mx_kv_append`` launch skips a slot
+  outside the table or the pool and sets the pool's device error word, and
+  marks the blocks it writes in a device byte map. The ``IndexError`` the
+  reference raises is raised by :meth:`check_write_errors` (one sync, called
+  once per decode step by the decode loop), and ``allocated_block_count`` /
+  ``peak_allocated_block_count`` read the byte map when asked.
 """
 
 from __future__ import annotations
@@ -59,16 +67,40 @@ class GpuKVBlockPool:
         self._v_pool: torch.Tensor | None = None
         self._used_blocks: set[int] = set()
         self._peak_allocated_blocks = 0
+        self._used_map: torch.Tensor | None = None    # uint8 [num_blocks]: blocks written on the device
+        self._write_err: torch.Tensor | None = None   # int32 [1]: kv append error bits since the last check
 
     @property
     def block_size_tokens(self) -> int:
         return self.shape.block_size_tokens
 
+    def _sync_used_map(self) -> None:
+        """Fold the device byte map of written blocks into the host set (one host sync)."""
+        if self._used_map is None:
+            return
+        ids = torch.nonzero(self._used_map).flatten().tolist()
+        if ids:
+            self._used_blocks.update(int(i) for i in ids)
+            self._peak_allocated_blocks = max(self._peak_allocated_blocks, len(self._used_blocks))
+
     def allocated_block_count(self) -> int:
+        self._sync_used_map()
         return len(self._used_blocks)
 
     def peak_allocated_block_count(self) -> int:
+        self._sync_used_map()
         return self._peak_allocated_blocks
+
+    def check_write_errors(self) -> None:
+        """Raise ``IndexError`` if a device KV write met a slot outside its block table or the
+        pool since the last check (the reference's ``:221-222`` check, deferred to one host
+        sync); the error word is cleared."""
+        if self._write_err is None:
+            return
+        bits = int(self._write_err.item())
+        if bits:
+            self._write_err.zero_()
+            raise IndexError("block table underrun or physical block id out of range during batched write")
 
     def bytes_per_block(self) -> int:
         s = self.shape
@@ -79,7 +111,7 @@ class GpuKVBlockPool:
         return block_count * self.bytes_per_block()
 
     def peak_allocated_bytes(self) -> int:
-        return self.bytes_for_blocks(self._peak_allocated_blocks)
+        return self.bytes_for_blocks(self.peak_allocated_block_count())
 
     def _ensure_pools(self) -> None:
         if self._k_pool is not None:
@@ -88,6 +120,9 @@ class GpuKVBlockPool:
         shape = (s.num_layers, s.num_blocks, s.num_kv_heads, s.block_size_tokens, s.head_dim)
         self._k_pool = torch.zeros(shape, dtype=self.dtype, device=self.device)
         self._v_pool = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        if self.device.type == "cuda":
+            self._used_map = torch.zeros(s.num_blocks, dtype=torch.uint8, device=self.device)
+            self._write_err = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     def _touch_block(self, physical: int) -> None:
         if physical < 0 or physical >= self.shape.num_blocks:
@@ -134,12 +169,12 @@ class GpuKVBlockPool:
         """KV write: tables ``[B, max_blocks]``, starts ``[B]``, states ``[B, Hkv, kv_len, D]``.
 
         Same semantics as the reference (``:176-227``). On a device pool it is
-        one ``mx_kv_append`` launch (no per-token loop); outside graph capture
-        the table bounds are checked on the host first and raise ``IndexError``
-        as in the reference (``:221-222``), at the cost of one host sync.
-        During capture the kernel skips out-of-range slots instead. A pool on
-        the CPU (used by host-side tests of the cache bookkeeping) takes an
-        indexed torch store.
+        one ``mx_kv_append`` launch (no per-token loop) and no host sync: a slot
+        outside the table or the pool is skipped and recorded in the pool's
+        error word, which :meth:`check_write_errors` turns into the reference's
+        ``IndexError`` (``:221-222``); written blocks are marked in a device map
+        for the usage accounting. A pool on the CPU (host-side tests of the
+        cache bookkeeping) checks on the host and takes an indexed torch store.
         """
         if key_states.shape != value_states.shape:
             raise ValueError("key_states and value_states must match shape")
@@ -152,28 +187,25 @@ class GpuKVBlockPool:
         self._ensure_pools()
         assert self._k_pool is not None and self._v_pool is not None
         device = self.device
-        on_device = device.type == "cuda"
-        capturing = bool(on_device and torch.cuda.is_current_stream_capturing())
         bs = self.block_size_tokens
-        if not capturing:
-            tables = block_tables.to(device=device, dtype=torch.int64)
-            pos = start_positions.to(device=device, dtype=torch.int64).view(-1, 1) + torch.arange(
-                kv_len, device=device, dtype=torch.int64).view(1, -1)  # [B, T]
-            logical = torch.div(pos, bs, rounding_mode="floor")
-            if int(logical.max().item()) >= tables.shape[1] or int(pos.min().item()) < 0:
-                raise IndexError("block table underrun during batched write")
-            physical = torch.gather(tables, 1, logical)  # [B, T]
-            if int(physical.min().item()) < 0 or int(physical.max().item()) >= self.shape.num_blocks:
-                raise IndexError("physical block id out of range during batched write")
-            self._touch_blocks(physical)
         k_layer = self._k_pool[layer_idx]
         v_layer = self._v_pool[layer_idx]
-        if on_device:
+        if device.type == "cuda":
             from .decode_glue import kv_append
 
             kv_append(k_layer, v_layer, block_tables, start_positions, key_states.to(self.dtype),
-                      value_states.to(self.dtype))
+                      value_states.to(self.dtype), err=self._write_err, used_blocks=self._used_map)
             return
+        tables = block_tables.to(device=device, dtype=torch.int64)
+        pos = start_positions.to(device=device, dtype=torch.int64).view(-1, 1) + torch.arange(
+            kv_len, device=device, dtype=torch.int64).view(1, -1)  # [B, T]
+        logical = torch.div(pos, bs, rounding_mode="floor")
+        if int(logical.max().item()) >= tables.shape[1] or int(pos.min().item()) < 0:
+            raise IndexError("block table underrun during batched write")
+        physical = torch.gather(tables, 1, logical)  # [B, T]
+        if int(physical.min().item()) < 0 or int(physical.max().item()) >= self.shape.num_blocks:
+            raise IndexError("physical block id out of range during batched write")
+        self._touch_blocks(physical)
         offset = (pos % bs).reshape(-1)
         phys = physical.reshape(-1)
         # pool[physical, layer, :, offset, :] = states[b, :, t, :]
@@ -242,5 +274,7 @@ class GpuKVBlockPool:
     def reset(self) -> None:
         self._k_pool = None
         self._v_pool = None
+        self._used_map = None
+        self._write_err = None
         self._used_blocks.clear()
         self._peak_allocated_blocks = 0

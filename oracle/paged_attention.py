@@ -27,6 +27,9 @@ blocks and id 0 is a real block, so a reader bounds by ``ceil(S / bs)``, and
 never by the table width alone. Like the reference's batched kernel
 (``:194-196``) the number of blocks read is ``min(ceil(S/bs), max_blocks)``.
 
+* :func:`decode_rows_fp32_valid` - the same with table entries outside the pool
+  skipped (the build's contract for such ids; the reference has no check).
+
 Parity pinning (tests/test_oracle_attention.py): torch's own
 ``scaled_dot_product_attention`` on gathered, GQA-expanded K/V (a library
 routine); closed forms (S = 1 -> V[0]; identical keys -> mean of V;
@@ -116,6 +119,40 @@ def decode_rows_fp32(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.
         q = query[b, :, 0, :].float()
         scores = torch.einsum("hd,htd->ht", q, k[kv_idx]) * scaling
         p = torch.softmax(scores, dim=-1)
+        out[b, :, 0, :] = torch.einsum("ht,htd->hd", p, v[kv_idx])
+    return out
+
+
+def decode_rows_fp32_valid(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                           block_tables: torch.Tensor, seq_lens, scaling: float, num_kv_groups: int,
+                           num_pool_blocks: int) -> torch.Tensor:
+    """:func:`decode_rows_fp32` over the tokens whose physical block lies in ``[0, num_pool_blocks)``.
+
+    The build's contract for a table entry outside the pool (the reference would index out of
+    its slab, ``paged_kv_kernel.py:217-227``): that block's tokens are skipped, the softmax runs
+    over the remaining tokens, and a row with none left is zeros. ``k_layer``/``v_layer`` only
+    need to hold the in-pool blocks' rows (ids outside the pool are never indexed).
+    """
+    bsz, hq, _, d = query.shape
+    max_blocks = int(block_tables.shape[1])
+    bs = k_layer.shape[2]
+    out = torch.zeros(bsz, hq, 1, d, dtype=torch.float32)
+    kv_idx = torch.arange(hq) // num_kv_groups
+    for b in range(bsz):
+        s = int(seq_lens[b])
+        nblk = min(math.ceil(max(s, 0) / bs), max_blocks)
+        keys, vals = [], []
+        for j in range(nblk):
+            phys = int(block_tables[b, j])
+            take = min(bs, s - j * bs)
+            if 0 <= phys < num_pool_blocks:
+                keys.append(k_layer[phys, :, :take].float())
+                vals.append(v_layer[phys, :, :take].float())
+        if not keys:
+            continue
+        k, v = torch.cat(keys, dim=1), torch.cat(vals, dim=1)
+        q = query[b, :, 0, :].float()
+        p = torch.softmax(torch.einsum("hd,htd->ht", q, k[kv_idx]) * scaling, dim=-1)
         out[b, :, 0, :] = torch.einsum("ht,htd->hd", p, v[kv_idx])
     return out
 

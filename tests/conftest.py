@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import os
 import sys
+import warnings
 
 import pytest
 
@@ -12,6 +13,16 @@ PKG_ROOT = os.path.join(REPO, "llm-serving-runtime_amd")
 for p in (REPO, PKG_ROOT):
     if p not in sys.path:
         sys.path.insert(0, p)
+
+
+class ParityReport(UserWarning):
+    """Figures a passing parity test reports (token flips, margins, errors). Emitted as a
+    warning so that pytest's warnings summary carries them in a ``-q`` run's log."""
+
+
+def report(msg: str) -> None:
+    print(msg, flush=True)
+    warnings.warn(msg, ParityReport, stacklevel=2)
 
 
 def pytest_configure(config):

@@ -127,6 +127,17 @@ def test_native_step_qwen2_shape():
     _run(om.random_qwen2(seed=1, num_hidden_layers=2), batch=16, lo=64, hi=256, seed=1, graph=False)
 
 
+@pytest.mark.parametrize("batch", [1, 4])
+def test_native_step_qwen2_shape_small_batches(batch):
+    """1 and 4 rows on the Qwen2-0.5B dims: every projection on the VALU GEMV, gate||up
+    (whose MFMA launch would split K) with the SwiGLU product in the GEMV's epilogue."""
+    from runtime_amd.phase2.int8_linear import gateup_fusable, linear_splits
+
+    assert linear_splits(5, 2 * 4864, 896) > 1 and gateup_fusable(batch, 2 * 4864, 896)
+    _run(om.random_qwen2(seed=4, num_hidden_layers=2, vocab_size=32768), batch=batch, lo=30, hi=200, seed=4,
+         graph=batch == 4)
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("batch", [72, 128])
 def test_native_step_more_than_64_rows(batch):

@@ -239,10 +239,13 @@ def test_swiglu_linear_equals_silu_mul_then_linear(m, n, k):
 
 
 @pytest.mark.parametrize("m,inter,k", [(32, 14336, 4096), (7, 4864, 896), (64, 1024, 256), (128, 1024, 256),
-                                        (70, 4864, 896), (100, 14336, 4096)])
+                                        (70, 4864, 896), (100, 14336, 4096), (1, 4864, 896), (3, 4864, 896),
+                                        (4, 4864, 896), (1, 14336, 4096), (4, 14336, 4096)])
 def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     """gate||up with interleaved rows and the SwiGLU product in the epilogue equals the plain
-    [gate | up] projection followed by mx_silu_mul, bit for bit."""
+    [gate | up] projection followed by mx_silu_mul, bit for bit. At M <= 4 on the Qwen2-0.5B
+    MLP (a shape whose MFMA launch splits K) the VALU GEMV takes both, with the product in
+    the GEMV's own epilogue; the Llama MLP at M <= 4 runs the unsplit MFMA kernel."""
     from runtime_amd.phase2.decode_glue import silu_mul
     from runtime_amd.phase2.int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu,
                                                 linear_splits)

@@ -347,3 +347,67 @@ def test_stale_nan_past_sequence_end(d):
         assert err == 0
         assert torch.isfinite(out.float()).all(), f"chunk_tokens={ct}"
         _check(out, base, f"chunk_tokens={ct}")
+
+
+@pytest.mark.parametrize("d,bs", [(128, 16), (64, 8), (128, 4), (64, 32)])
+def test_block_ids_outside_the_pool(d, bs):
+    """Table entries outside [0, num_pool_blocks) are skipped, never dereferenced: the error word
+    gets bit 1, the output stays finite, a row with no block left is zeros, and every other row is
+    the oracle over its in-pool blocks (oracle.paged_attention.decode_rows_fp32_valid). Covers a
+    row's first block(s) out (the running max is still -inf when the first in-pool tile arrives),
+    a block in the middle, the last block, and at block sizes 4 and 8 a whole 16-token tile of out
+    blocks at the start of a piece (chunk_tokens 16 cuts every row into one-tile pieces)."""
+    lens = [40, 64, 100, 37, 300, 77]
+    grp = 4
+    q, k, v, tables, sl = _random_case(61 + d + bs, len(lens), 2, grp, d, bs, lens)
+    n_valid = int(k.shape[0])
+    t = tables.clone()
+    nblk = [math.ceil(s / bs) for s in lens]
+    t[0, :nblk[0]] = n_valid + 5                      # every block out: zeros
+    t[1, :max(1, 16 // bs)] = -1                     # the first tile's blocks out
+    t[2, nblk[2] // 2] = n_valid                     # a block in the middle
+    t[3, nblk[3] - 1] = 1 << 30                      # the last (partial) block
+    t[4, 1:1 + max(1, 32 // bs)] = n_valid + 1       # two tiles' worth in the second piece
+    scale = d**-0.5
+    want = oracle_pa.decode_rows_fp32_valid(q.cpu(), k.cpu(), v.cpu(), t.cpu(), lens, scale, grp, n_valid)
+    for ct in (0, 16):
+        out, err = _abi_decode(q, k, v, t, sl, scale, grp, ct, num_pool_blocks=n_valid)
+        assert err & 1, f"chunk_tokens={ct}: out-of-pool ids not flagged"
+        assert torch.isfinite(out.float()).all(), f"chunk_tokens={ct}: non-finite output"
+        assert torch.count_nonzero(out[0]) == 0
+        _check(out, want, f"chunk_tokens={ct}")
+
+
+def _config5_attention_case(seed=0):
+    """BASELINE config 5's attention shape: 128 rows in 16 groups of 8, each group's rows longer than
+    1024 tokens aliasing the group's 1024-token prefix blocks; contexts U[1, 8192]; Llama-3-8B heads
+    (Hq 32, Hkv 8, D 128), block 16, a 40960-block pool with seeded block ids."""
+    from runtime_amd.phase2.prefix_batch import PrefixBatch
+
+    nb, bs, hkv, grp, d = 40960, 16, 8, 4, 128
+    pb = PrefixBatch(batch=128, groups=16, prefix_tokens=1024, lo=1, hi=8192, block_size=bs, num_blocks=nb,
+                     headroom=1, seed=seed)
+    lens = pb.lens + 1  # the attention length counts the current token
+    gd = torch.Generator(device="cuda").manual_seed(seed)
+    k = torch.randn(nb, hkv, bs, d, generator=gd, device="cuda", dtype=torch.float16)
+    v = torch.randn(nb, hkv, bs, d, generator=gd, device="cuda", dtype=torch.float16)
+    q = torch.randn(128, hkv * grp, 1, d, generator=gd, device="cuda", dtype=torch.float16)
+    return pb, q, k, v, pb.tables.cuda(), lens.to(torch.int32).cuda(), grp, d**-0.5
+
+
+@pytest.mark.timeout(600)
+def test_config5_shared_prefix_full_shape():
+    """Config 5 at its stated size under both K/V cache policies (streaming loads, and the default
+    policy that MX_PA_SHARED_BLOCKS selects for aliased blocks): bit-identical to each other and
+    within atol/rtol 1e-2 of the fp32 per-row oracle."""
+    pb, q, k, v, tables, lens, grp, scale = _config5_attention_case()
+    shared_rows = sum(r.shared > 0 for r in pb.rows)
+    lens_h = lens.cpu().tolist()
+    print(f"[config5] rows 128, sharing {shared_rows}, contexts {min(lens_h)}..{max(lens_h)}, "
+          f"logical tokens {sum(lens_h)}, unique {pb.unique_tokens(1)}", flush=True)
+    assert shared_rows >= 100 and max(lens_h) > 7000 and min(lens_h) < 1024
+    shared, err1 = _abi_decode(q, k, v, tables, lens, scale, grp, 0, flags=1)
+    stream, err0 = _abi_decode(q, k, v, tables, lens, scale, grp, 0)
+    assert err0 == 0 and err1 == 0
+    assert torch.equal(shared, stream)
+    _check(shared, oracle_out(q, k, v, tables, lens_h, scale, grp))

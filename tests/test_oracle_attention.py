@@ -194,3 +194,29 @@ def test_checks_catch_planted_mistakes():
     good = paged_attention.merge_partials(m, l, acc)
     naive = acc.sum(-2) / l.sum(-1, keepdim=True)
     assert not torch.allclose(good, naive)
+
+
+def test_valid_block_variant_pins():
+    """decode_rows_fp32_valid: every id in the pool -> decode_rows_fp32; the trailing blocks of a
+    row outside the pool -> the row truncated to its in-pool prefix; no block in the pool -> zeros;
+    a block in the middle outside the pool -> SDPA over the remaining tokens (library routine)."""
+    bs, d, hkv, grp = 8, 32, 2, 3
+    lens = [40, 40, 40, 40]
+    q, k, v, tables = _case(9, 4, hkv, grp, d, bs, lens, num_blocks=64)
+    scale = d**-0.5
+    full = paged_attention.decode_rows_fp32(q, k, v, tables, lens, scale, grp)
+    assert torch.equal(paged_attention.decode_rows_fp32_valid(q, k, v, tables, lens, scale, grp, 64), full)
+    t = tables.clone()
+    t[0, 3:5] = 99         # row 0: blocks 3, 4 outside -> the first 24 tokens
+    t[1, :5] = -1          # row 1: nothing left -> zeros
+    t[2, 2] = 64           # row 2: middle block outside
+    got = paged_attention.decode_rows_fp32_valid(q, k, v, t, lens, scale, grp, 64)
+    trunc = paged_attention.decode_rows_fp32(q[:1], k, v, tables[:1], [24], scale, grp)
+    assert torch.allclose(got[0], trunc[0], atol=1e-6)
+    assert torch.count_nonzero(got[1]) == 0
+    keep = [j for j in range(5) if j != 2]
+    keys = torch.cat([k[int(tables[2, j])] for j in keep], dim=1).repeat_interleave(grp, dim=0).unsqueeze(0)
+    vals = torch.cat([v[int(tables[2, j])] for j in keep], dim=1).repeat_interleave(grp, dim=0).unsqueeze(0)
+    want2 = F.scaled_dot_product_attention(q[2:3].float(), keys.float(), vals.float(), scale=scale)
+    assert torch.allclose(got[2], want2[0], atol=2e-6, rtol=1e-5)
+    assert torch.equal(got[3], full[3])

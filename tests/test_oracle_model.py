@@ -82,3 +82,48 @@ def test_config3_shape_constants():
             cfg["intermediate_size"], cfg["vocab_size"]) == (896, 24, 14, 2, 4864, 151936)
     assert cfg["hidden_size"] // cfg["num_attention_heads"] == 64
     assert np.isclose(cfg["rope_theta"], 1e6)
+
+
+def test_prefix_cache_continuation_equals_full_forward(tiny_pair):
+    """Continuing from prefix_cache gives the full forward's teacher-forced logits and prompt K/V; the
+    cache itself is not consumed (a second continuation from it agrees too)."""
+    _, ref = tiny_pair
+    g = torch.Generator().manual_seed(1)
+    prefix = torch.randint(0, TINY["vocab_size"], (32,), generator=g)
+    past = om.prefix_cache(ref, prefix)
+    assert past[1] == 32
+    for n_suffix in (1, 9):
+        prompt = torch.cat([prefix, torch.randint(0, TINY["vocab_size"], (n_suffix,), generator=g)])
+        tokens, _ = om.greedy_reference(ref, prompt, steps=6)
+        full = om.teacher_forced_logits(ref, prompt, tokens)
+        cont = om.teacher_forced_logits(ref, prompt, tokens, past=past)
+        torch.testing.assert_close(cont, full, atol=1e-4, rtol=1e-4)
+        kv_full, last_full = om.prefill_kv(ref, prompt)
+        kv_cont, last_cont = om.prefill_kv(ref, prompt, past=past)
+        torch.testing.assert_close(last_cont, last_full, atol=1e-4, rtol=1e-4)
+        for (kf, vf), (kc, vc) in zip(kv_full, kv_cont):
+            assert kc.shape == kf.shape == (TINY["num_key_value_heads"], prompt.numel(), 32)
+            torch.testing.assert_close(kc, kf, atol=1e-5, rtol=1e-5)
+            torch.testing.assert_close(vc, vf, atol=1e-5, rtol=1e-5)
+    # A wrong prefix length (the cache continued one token too early) is caught.
+    prompt = torch.cat([prefix, torch.randint(0, TINY["vocab_size"], (4,), generator=g)])
+    tokens, _ = om.greedy_reference(ref, prompt, steps=3)
+    bad = om.teacher_forced_logits(ref, prompt, tokens, past=(past[0], 31))
+    assert (bad - om.teacher_forced_logits(ref, prompt, tokens)).abs().max() > 1e-2
+
+
+def test_margin_controlled_init_pins():
+    """margin_controlled_: the greedy successor of token u is perm[u] with a wide margin, on a small
+    model whose plain-init margins include near ties; the permutation is seeded."""
+    plain = om.random_qwen2(seed=4, **dict(TINY, num_hidden_layers=3, vocab_size=4096))
+    sharp = om.random_qwen2(seed=4, **dict(TINY, num_hidden_layers=3, vocab_size=4096))
+    perm = om.margin_controlled_(sharp, seed=1)
+    assert torch.equal(perm, om.margin_controlled_(om.random_qwen2(seed=4, **dict(TINY, vocab_size=4096)), seed=1))
+    prompt = torch.randint(0, 4096, (50,), generator=torch.Generator().manual_seed(2))
+    tokens, logits = om.greedy_reference(sharp, prompt, steps=24)
+    prev = torch.cat([prompt[-1:], tokens[:-1]])
+    assert torch.equal(tokens, perm[prev])
+    top2 = logits.topk(2, dim=-1).values
+    _, plain_logits = om.greedy_reference(plain, prompt, steps=24)
+    plain_top2 = plain_logits.topk(2, dim=-1).values
+    assert float((top2[:, 0] - top2[:, 1]).min()) > 10 * float((plain_top2[:, 0] - plain_top2[:, 1]).min())
