@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 10
+#define MX_ABI_VERSION 11
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -189,6 +189,27 @@ int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const ui
                          int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out, int64_t o_sb,
                          int64_t o_sh, void* workspace, size_t workspace_bytes, int32_t chunk_tokens, uint32_t flags,
                          void* stream);
+
+/* mx_paged_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP-graph capture, serving loops and
+ * harnesses that forbid hipMalloc). No counterpart in the reference: its
+ * decode path allocates scratch per shape (paged_attention_triton.py:90-115).
+ * The split partials live in a static device array of
+ * MX_PA_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
+ * until the process ends; shapes whose workspace (mx_paged_attn_workspace_bytes)
+ * exceeds it are refused with MX_ERR_WORKSPACE. The call allocates nothing.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (concurrent streams) race, so serialise them. err (nullable) is a
+ * caller-owned int32 device word OR-ed with the error bits (bit 0: a block id
+ * outside the pool was skipped); without it the bits are dropped. Other
+ * arguments, results and status codes are those of mx_paged_attn_decode. */
+#define MX_PA_NOALLOC_SCRATCH_BYTES (32u << 20)
+int mx_paged_attn_decode_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k, const uint16_t* v,
+                                 int64_t kv_sblk, int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb,
+                                 int32_t max_blocks, const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv,
+                                 int32_t D, int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out,
+                                 int64_t o_sb, int64_t o_sh, int32_t chunk_tokens, uint32_t flags, int32_t* err,
+                                 void* stream);
 
 /* Byte offset of the int32 error word inside a paged-attention workspace
  * (nonzero after a call that met an out-of-range block id). Reading it needs a

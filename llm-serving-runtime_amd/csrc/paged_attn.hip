@@ -51,6 +51,8 @@
 // writes back and invalidates the XCD's L2 (measured 2.6x slower at the bench
 // shape), and write-through atomic partials with a ticket counter still lost
 // (1.3x).
+#include <mutex>
+
 #include "common.h"
 
 namespace mx {
@@ -698,46 +700,36 @@ extern "C" size_t mx_paged_attn_error_offset(int32_t B, int32_t Hq, int32_t Hkv,
     return pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens).err;
 }
 
-extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k,
-                                    const uint16_t* v, int64_t kv_sblk, int64_t kv_shead,
-                                    const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
-                                    const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
-                                    int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out,
-                                    int64_t o_sb, int64_t o_sh, void* workspace, size_t workspace_bytes,
-                                    int32_t chunk_tokens, uint32_t flags, void* stream) {
-    if (B < 0) return fail(MX_ERR_INVALID, "mx_paged_attn_decode: B must be >= 0");
-    if (B == 0) return MX_OK;
-    if (!q || !k || !v || !block_tables || !seq_lens || !out)
-        return fail(MX_ERR_NULL, "mx_paged_attn_decode: null pointer");
+namespace mx {
+namespace pa {
+
+// Argument checks shared by the two decode entry points; fills the launch parameters except
+// the workspace pointers.
+static int check_args(const char* what, const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k,
+                      const uint16_t* v, int64_t kv_sblk, int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb,
+                      int32_t max_blocks, const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                      int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out, int64_t o_sb,
+                      int64_t o_sh, int32_t chunk_tokens, uint32_t flags, Params& prm) {
+    if (!q || !k || !v || !block_tables || !seq_lens || !out) return fail(MX_ERR_NULL, "%s: null pointer", what);
     if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
-        return fail(MX_ERR_INVALID, "mx_paged_attn_decode: Hq (%d) must be a positive multiple of Hkv (%d)", Hq, Hkv);
+        return fail(MX_ERR_INVALID, "%s: Hq (%d) must be a positive multiple of Hkv (%d)", what, Hq, Hkv);
     const int G = Hq / Hkv;
-    if (G > 8) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: GQA group %d > 8 unsupported", G);
-    if (D != 64 && D != 128) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: head_dim %d unsupported", D);
+    if (G > 8) return fail(MX_ERR_UNSUPPORTED, "%s: GQA group %d > 8 unsupported", what, G);
+    if (D != 64 && D != 128) return fail(MX_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", what, D);
     if (block_size != 4 && block_size != 8 && block_size != 16 && block_size != 32)
-        return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: block_size %d unsupported (4, 8, 16 or 32)",
-                    block_size);
+        return fail(MX_ERR_UNSUPPORTED, "%s: block_size %d unsupported (4, 8, 16 or 32)", what, block_size);
     if (max_blocks < 1 || num_pool_blocks < 1)
-        return fail(MX_ERR_INVALID, "mx_paged_attn_decode: max_blocks and num_pool_blocks must be >= 1");
-    if (B > 65535 || Hkv > 65535) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: B or Hkv too large");
-    if (flags & ~(uint32_t)(MX_PA_SHARED_BLOCKS | MX_PA_BF16))
-        return fail(MX_ERR_INVALID, "mx_paged_attn_decode: unknown flags 0x%x", flags);
-    if (chunk_tokens < 0 || chunk_tokens % pa::kTile != 0 || chunk_tokens > pa::kMaxChunkTokens)
-        return fail(MX_ERR_INVALID, "mx_paged_attn_decode: chunk_tokens must be 0 or a multiple of 16 <= %d",
-                    pa::kMaxChunkTokens);
-    if ((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, pa::kTile) > ((int64_t)1 << 31))
-        return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: more than 2^31 tiles");
+        return fail(MX_ERR_INVALID, "%s: max_blocks and num_pool_blocks must be >= 1", what);
+    if (B > 65535 || Hkv > 65535) return fail(MX_ERR_UNSUPPORTED, "%s: B or Hkv too large", what);
+    if (flags & ~(uint32_t)(MX_PA_SHARED_BLOCKS | MX_PA_BF16)) return fail(MX_ERR_INVALID, "%s: unknown flags 0x%x", what, flags);
+    if (chunk_tokens < 0 || chunk_tokens % kTile != 0 || chunk_tokens > kMaxChunkTokens)
+        return fail(MX_ERR_INVALID, "%s: chunk_tokens must be 0 or a multiple of 16 <= %d", what, kMaxChunkTokens);
+    if ((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, kTile) > ((int64_t)1 << 31))
+        return fail(MX_ERR_UNSUPPORTED, "%s: more than 2^31 tiles", what);
     if (!aligned(q, 16) || q_sb % 8 || q_sh % 8 || !aligned(k, 16) || !aligned(v, 16) || kv_sblk % 8 ||
         kv_shead % 8 || !aligned(out, 16) || o_sb % 8 || o_sh % 8)
-        return fail(MX_ERR_ALIGNMENT, "mx_paged_attn_decode: q/K/V/out rows must be 16-byte aligned");
-    const pa::Layout L = pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens);
-    if (!workspace || workspace_bytes < L.total)
-        return fail(MX_ERR_WORKSPACE, "mx_paged_attn_decode: workspace needs %zu bytes, got %zu", L.total,
-                    workspace_bytes);
-    if (!aligned(workspace, 256)) return fail(MX_ERR_ALIGNMENT, "mx_paged_attn_decode: workspace must be 256-byte aligned");
-
-    char* ws = static_cast<char*>(workspace);
-    pa::Params prm{};
+        return fail(MX_ERR_ALIGNMENT, "%s: q/K/V/out rows must be 16-byte aligned", what);
+    prm = Params{};
     prm.q = reinterpret_cast<const _Float16*>(q);
     prm.q_sb = q_sb;
     prm.q_sh = q_sh;
@@ -756,23 +748,108 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     prm.out = reinterpret_cast<_Float16*>(out);
     prm.o_sb = o_sb;
     prm.o_sh = o_sh;
-    prm.err = reinterpret_cast<int*>(ws + L.err);
+    return MX_OK;
+}
+
+// Points the launch at a workspace laid out by `L` (err may redirect the error word) and launches.
+static int launch_decode(const char* what, Params prm, const Layout& L, char* ws, int32_t* err, int32_t B, int32_t Hq,
+                         int32_t Hkv, int32_t D, int32_t max_blocks, int32_t block_size, uint32_t flags, void* stream) {
+    const int G = Hq / Hkv;
+    prm.err = err ? err : reinterpret_cast<int*>(ws + L.err);
     prm.part_ml = reinterpret_cast<float*>(ws + L.ml);
     prm.part_acc = reinterpret_cast<float*>(ws + L.acc);
     prm.seg_w = reinterpret_cast<int*>(ws + L.segw);
     prm.workers = L.workers;
     hipStream_t st = as_stream(stream);
-    bool ok = false;
     // Fewest workers that keep every range within one vector of block ids.
-    const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, pa::kTile),
-                                pa::max_range_tiles(block_size));
+    const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, kTile),
+                                max_range_tiles(block_size));
     const bool shared = flags & MX_PA_SHARED_BLOCKS, bf16 = flags & MX_PA_BF16;
+    bool ok;
     if (bf16)
-        ok = shared ? pa::dispatch_d_bs<false, true>(D, block_size, G, prm, B, st, fw)
-                    : pa::dispatch_d_bs<true, true>(D, block_size, G, prm, B, st, fw);
+        ok = shared ? dispatch_d_bs<false, true>(D, block_size, G, prm, B, st, fw)
+                    : dispatch_d_bs<true, true>(D, block_size, G, prm, B, st, fw);
     else
-        ok = shared ? pa::dispatch_d_bs<false, false>(D, block_size, G, prm, B, st, fw)
-                    : pa::dispatch_d_bs<true, false>(D, block_size, G, prm, B, st, fw);
-    if (!ok) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode: unsupported configuration");
-    return check_launch("mx_paged_attn_decode");
+        ok = shared ? dispatch_d_bs<false, false>(D, block_size, G, prm, B, st, fw)
+                    : dispatch_d_bs<true, false>(D, block_size, G, prm, B, st, fw);
+    if (!ok) return fail(MX_ERR_UNSUPPORTED, "%s: unsupported configuration", what);
+    return check_launch(what);
+}
+
+// Scratch of mx_paged_attn_decode_noalloc: a file-scope device array, one copy per GPU, held
+// until the process ends. Host code never passes the array's name to a kernel (on the host it
+// is a stand-in, not a device address): each device's address comes from hipGetSymbolAddress,
+// taken once per device with that device current, and only that pointer is used.
+static __device__ __align__(256) char scratch[MX_PA_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_of_current_device(char** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MX_ERR_LAUNCH, "mx_paged_attn_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(MX_ERR_UNSUPPORTED, "mx_paged_attn_decode_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(MX_ERR_LAUNCH, "mx_paged_attn_decode_noalloc: hipGetSymbolAddress(scratch): %s",
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = static_cast<char*>(g_scratch_ptr[dev]);
+    return MX_OK;
+}
+
+}  // namespace pa
+}  // namespace mx
+
+extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k,
+                                    const uint16_t* v, int64_t kv_sblk, int64_t kv_shead,
+                                    const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
+                                    const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                                    int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out,
+                                    int64_t o_sb, int64_t o_sh, void* workspace, size_t workspace_bytes,
+                                    int32_t chunk_tokens, uint32_t flags, void* stream) {
+    const char* what = "mx_paged_attn_decode";
+    if (B < 0) return fail(MX_ERR_INVALID, "%s: B must be >= 0", what);
+    if (B == 0) return MX_OK;
+    pa::Params prm;
+    int rc = pa::check_args(what, q, q_sb, q_sh, k, v, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, seq_lens, B,
+                            Hq, Hkv, D, block_size, num_pool_blocks, scale, out, o_sb, o_sh, chunk_tokens, flags, prm);
+    if (rc != MX_OK) return rc;
+    const pa::Layout L = pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens);
+    if (!workspace || workspace_bytes < L.total)
+        return fail(MX_ERR_WORKSPACE, "%s: workspace needs %zu bytes, got %zu", what, L.total, workspace_bytes);
+    if (!aligned(workspace, 256)) return fail(MX_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", what);
+    return pa::launch_decode(what, prm, L, static_cast<char*>(workspace), nullptr, B, Hq, Hkv, D, max_blocks,
+                             block_size, flags, stream);
+}
+
+extern "C" int mx_paged_attn_decode_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k,
+                                            const uint16_t* v, int64_t kv_sblk, int64_t kv_shead,
+                                            const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
+                                            const int32_t* seq_lens, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                                            int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out,
+                                            int64_t o_sb, int64_t o_sh, int32_t chunk_tokens, uint32_t flags,
+                                            int32_t* err, void* stream) {
+    const char* what = "mx_paged_attn_decode_noalloc";
+    if (B < 0) return fail(MX_ERR_INVALID, "%s: B must be >= 0", what);
+    if (B == 0) return MX_OK;
+    pa::Params prm;
+    int rc = pa::check_args(what, q, q_sb, q_sh, k, v, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, seq_lens, B,
+                            Hq, Hkv, D, block_size, num_pool_blocks, scale, out, o_sb, o_sh, chunk_tokens, flags, prm);
+    if (rc != MX_OK) return rc;
+    if (err && !aligned(err, 4)) return fail(MX_ERR_ALIGNMENT, "%s: err must be 4-byte aligned", what);
+    const pa::Layout L = pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens);
+    if (L.total > (size_t)MX_PA_NOALLOC_SCRATCH_BYTES)
+        return fail(MX_ERR_WORKSPACE, "%s: this shape needs %zu bytes of scratch, more than the %zu the library holds "
+                                      "per GPU; use mx_paged_attn_decode with a workspace",
+                    what, L.total, (size_t)MX_PA_NOALLOC_SCRATCH_BYTES);
+    char* ws = nullptr;
+    rc = pa::scratch_of_current_device(&ws);
+    if (rc != MX_OK) return rc;
+    return pa::launch_decode(what, prm, L, ws, err, B, Hq, Hkv, D, max_blocks, block_size, flags, stream);
 }
