@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 11
+#define MX_ABI_VERSION 12
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -210,6 +210,20 @@ int mx_paged_attn_decode_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_sh, 
                                  int32_t D, int32_t block_size, int32_t num_pool_blocks, float scale, uint16_t* out,
                                  int64_t o_sb, int64_t o_sh, int32_t chunk_tokens, uint32_t flags, int32_t* err,
                                  void* stream);
+
+/* Calibration probe (no reference counterpart; used by bench.py): the K/V reads
+ * of mx_paged_attn_decode over the same block tables and lengths, without the
+ * math, so its duration is what the gather alone costs on this GPU. mode 0:
+ * the decode kernel's own partition and load pattern (default worker count);
+ * mode 1: equal ranges of 16-token tiles per workgroup of Hkv waves, wave h
+ * reading head h of each tile's block, so a workgroup requests a whole block's
+ * Hkv runs (contiguous in the pool) at once. Block size 16, fp16 or bf16 runs
+ * (D 64 or 128), Hkv <= 16. Nothing is written except, with negligible odds, a
+ * checksum to sink[1] (sink: 2 int32 of device memory). */
+int mx_kv_gather_probe(const uint16_t* k, const uint16_t* v, int64_t kv_sblk, int64_t kv_shead,
+                       const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, const int32_t* seq_lens,
+                       int32_t B, int32_t Hkv, int32_t D, int32_t block_size, int32_t num_pool_blocks, int32_t mode,
+                       int32_t* sink, void* stream);
 
 /* Byte offset of the int32 error word inside a paged-attention workspace
  * (nonzero after a call that met an out-of-range block id). Reading it needs a

@@ -52,6 +52,7 @@
 // shape), and write-through atomic partials with a ticket counter still lost
 // (1.3x).
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -264,7 +265,10 @@ constexpr int kDepth = MX_PA_DEPTH;
 #define MX_PA_MIN_WAVES 3
 #endif
 
-template <int D, int BS, int G, bool STREAM, bool BF16>
+// PROBE = true: the calibration instance of mx_kv_gather_probe. The same partition and the same
+// K/V loads, with the math replaced by an xor of the loaded words (nothing is written unless
+// that checksum hits a magic value), so its duration is the gather alone.
+template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false>
 __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
     constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
@@ -357,7 +361,7 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
 
         // B operand: query head r (zero past G), dims 32*kk + 8*g + [0, 8).
         half8v qf[KK];
-        if (r < G) {
+        if (r < G && !PROBE) {
             const _Float16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h0 + r) * p.q_sh + 8 * g;
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) qf[kk] = load_half8(qp + 32 * kk);
@@ -454,6 +458,34 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
             }
         };
 
+        if constexpr (PROBE) {
+            Regs st[P];
+            uint32_t sum = 0;
+#pragma unroll
+            for (int s = 0; s < P; ++s) load_tile(s, st[s]);
+            for (int j0 = 0; j0 < nj; j0 += P) {
+#pragma unroll
+                for (int s = 0; s < P; ++s) {
+                    if (j0 + s < nj) {
+                        const Regs& tr = st[s];
+#pragma unroll
+                        for (int kk = 0; kk < KK; ++kk) {
+                            const uint4 w = __builtin_bit_cast(uint4, tr.k[kk]);
+                            sum ^= w.x ^ w.y ^ w.z ^ w.w;
+                        }
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) {
+                            const auto w = __builtin_bit_cast(typename std::conditional<D == 128, uint4, uint2>::type,
+                                                              tr.v[jj]);
+                            sum ^= w.x ^ w.y;
+                        }
+                    }
+                    load_tile(j0 + s + P, st[s]);
+                }
+            }
+            if (sum == 0x9e3779b9u) p.err[1] = (int)sum;  // keeps the loads; practically never taken
+            continue;
+        }
         {
             Regs st[P];
 #pragma unroll
@@ -684,6 +716,67 @@ static bool dispatch_d_bs(int D, int BS, int G, const Params& prm, int B, hipStr
     }
 }
 
+// Whole-block gather (mx_kv_gather_probe mode 1): the tiles of every row, flattened row-major,
+// cut into equal ranges, one per workgroup of Hkv waves; wave h reads the K and V runs of head h
+// of each tile's block, so a workgroup requests a block's Hkv runs (contiguous in the pool)
+// together. Two tiles in flight per wave, streaming loads, xor checksum as in PROBE.
+template <int D>
+__global__ __launch_bounds__(1024) void kv_block_probe_kernel(Params p) {
+    constexpr int RUN16 = D * kTile * 2 / 16;  // 16-byte chunks in one (tile, head) run: 256 at D 128
+    constexpr int U = RUN16 / 64;              // chunks per lane per run
+    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+    int64_t T = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {  // tiles of all rows (kv-head 0 only)
+        int s_eff, n = 0;
+        if (b0 + lane < p.B) n = row_tiles<kTile>(p, b0 + lane, s_eff);
+        T += wave_sum_i(n);
+    }
+    const int W = T < (int64_t)gridDim.x ? (int)T : (int)gridDim.x;
+    if ((int)blockIdx.x >= W) return;
+    int64_t x = range_lo(blockIdx.x, T, W);
+    const int64_t hi = range_lo(blockIdx.x + 1, T, W);
+    uint32_t sum = 0;
+    while (x < hi) {
+        // Row of tile x: locate with Hkv = 1 (tiles counted once per row).
+        Params q1 = p;
+        q1.Hkv = 1;
+        const Seg sg = locate<kTile>(q1, x, lane);
+        const int t0 = (int)(x - sg.row_start);
+        const int nj = (int)((int64_t)(sg.ntiles - t0) < hi - x ? sg.ntiles - t0 : hi - x);
+        const int32_t* bt_row = p.bt + (int64_t)sg.b * p.bt_sb;
+        uint4 r[2][2 * U];
+        auto load = [&](int j, uint4* d) {
+            const int jc = j < nj ? j : nj - 1;
+            const int t = t0 + jc;
+            int pb = bt_row[t];  // block size 16: tile t is block t of the row
+            pb = (unsigned)pb < (unsigned)p.num_pool_blocks ? pb : 0;
+            const uint4* kp = reinterpret_cast<const uint4*>(p.k + (int64_t)pb * p.kv_sblk + (int64_t)h * p.kv_shead);
+            const uint4* vp = reinterpret_cast<const uint4*>(p.v + (int64_t)pb * p.kv_sblk + (int64_t)h * p.kv_shead);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const u32x4v a = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(kp + u * 64 + lane));
+                const u32x4v c = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(vp + u * 64 + lane));
+                d[u] = uint4{a.x, a.y, a.z, a.w};
+                d[U + u] = uint4{c.x, c.y, c.z, c.w};
+            }
+        };
+        load(0, r[0]);
+        load(1, r[1]);
+        for (int j0 = 0; j0 < nj; j0 += 2) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                if (j0 + s < nj) {
+#pragma unroll
+                    for (int u = 0; u < 2 * U; ++u) sum ^= r[s][u].x ^ r[s][u].y ^ r[s][u].z ^ r[s][u].w;
+                }
+                load(j0 + s + 2, r[s]);
+            }
+        }
+        x += nj;
+    }
+    if (sum == 0x9e3779b9u) p.err[1] = (int)sum;
+}
+
 }  // namespace pa
 }  // namespace mx
 
@@ -852,4 +945,52 @@ extern "C" int mx_paged_attn_decode_noalloc(const uint16_t* q, int64_t q_sb, int
     rc = pa::scratch_of_current_device(&ws);
     if (rc != MX_OK) return rc;
     return pa::launch_decode(what, prm, L, ws, err, B, Hq, Hkv, D, max_blocks, block_size, flags, stream);
+}
+
+extern "C" int mx_kv_gather_probe(const uint16_t* k, const uint16_t* v, int64_t kv_sblk, int64_t kv_shead,
+                                  const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
+                                  const int32_t* seq_lens, int32_t B, int32_t Hkv, int32_t D, int32_t block_size,
+                                  int32_t num_pool_blocks, int32_t mode, int32_t* sink, void* stream) {
+    const char* what = "mx_kv_gather_probe";
+    if (B < 0) return fail(MX_ERR_INVALID, "%s: B must be >= 0", what);
+    if (B == 0) return MX_OK;
+    if (!k || !v || !block_tables || !seq_lens || !sink) return fail(MX_ERR_NULL, "%s: null pointer", what);
+    if (D != 64 && D != 128) return fail(MX_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", what, D);
+    if (block_size != 16 || Hkv < 1 || Hkv > 16 || max_blocks < 1 || num_pool_blocks < 1)
+        return fail(MX_ERR_UNSUPPORTED, "%s: needs block_size 16, 1 <= Hkv <= 16", what);
+    if (mode != 0 && mode != 1) return fail(MX_ERR_INVALID, "%s: mode must be 0 or 1", what);
+    if (!aligned(k, 16) || !aligned(v, 16) || kv_sblk % 8 || kv_shead % 8 || !aligned(sink, 8))
+        return fail(MX_ERR_ALIGNMENT, "%s: K/V runs must be 16-byte aligned", what);
+    pa::Params prm{};
+    prm.k = reinterpret_cast<const _Float16*>(k);
+    prm.v = reinterpret_cast<const _Float16*>(v);
+    prm.kv_sblk = kv_sblk;
+    prm.kv_shead = kv_shead;
+    prm.bt = block_tables;
+    prm.bt_sb = bt_sb;
+    prm.max_blocks = max_blocks;
+    prm.seq_lens = seq_lens;
+    prm.B = B;
+    prm.Hkv = Hkv;
+    prm.num_pool_blocks = num_pool_blocks;
+    prm.err = sink;
+    hipStream_t st = as_stream(stream);
+    if (mode == 0) {
+        // The decode kernel's default partition: one round of 2048 waves (or the range floor).
+        prm.workers = pa::resolve_workers(0, B, Hkv, max_blocks, block_size);
+        const int blocks = (int)ceil_div(prm.workers, pa::kWaves);
+        if (D == 128)
+            hipLaunchKernelGGL((pa::decode_split_kernel<128, 16, 1, true, false, true>), dim3(blocks),
+                               dim3(pa::kWaves * 64), 0, st, prm);
+        else
+            hipLaunchKernelGGL((pa::decode_split_kernel<64, 16, 1, true, false, true>), dim3(blocks),
+                               dim3(pa::kWaves * 64), 0, st, prm);
+    } else {
+        const int groups = pa::kDefaultWorkers / Hkv;
+        if (D == 128)
+            hipLaunchKernelGGL((pa::kv_block_probe_kernel<128>), dim3(groups), dim3(64 * Hkv), 0, st, prm);
+        else
+            hipLaunchKernelGGL((pa::kv_block_probe_kernel<64>), dim3(groups), dim3(64 * Hkv), 0, st, prm);
+    }
+    return check_launch(what);
 }

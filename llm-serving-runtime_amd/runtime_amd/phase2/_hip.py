@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -55,6 +55,9 @@ SIGNATURES = {
         ctypes.c_int,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32,
          ctypes.c_float, _p, _i64, _i64, _i32, _u32, _p, _p],
+    ),
+    "mx_kv_gather_probe": (
+        ctypes.c_int, [_p, _p, _i64, _i64, _p, _i64, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p],
     ),
     "mx_kv_append": (
         ctypes.c_int,

@@ -55,6 +55,7 @@ from .decode_glue import (QKV_ROPE_MAX_ROWS, add_rmsnorm, add_rmsnorm_splits, ar
 from .int8_linear import (gateup_fusable, gateup_interleave, int8_gateup_swiglu, int8_linear,
                           int8_linear_partials, linear_splits, pack_weight, quantize_weight)
 from .paged_attention_hip import _decode as _paged_decode
+from .roofline import linear_hbm_bytes
 
 
 @dataclass(frozen=True)
@@ -220,16 +221,13 @@ class Int8DecodeModel:
     # --- byte accounting (algorithmic HBM bytes of one step) -------------------
     def linear_bytes(self, batch: int) -> dict[str, int]:
         s = self.shape
-
-        def lb(n, k, bias=False, out=None):
-            return n * k + 2 * n + 2 * batch * k + 2 * batch * (n if out is None else out) + (2 * n if bias else 0)
-
         return {
-            "qkv": lb(s.qkv_out, s.hidden, s.qkv_bias),
-            "o": lb(s.hidden, s.heads * s.head_dim),
-            "gate_up": lb(2 * s.intermediate, s.hidden, out=s.intermediate),  # writes silu(g) * u only
-            "down": lb(s.hidden, s.intermediate),
-            "lm_head": lb(s.vocab, s.hidden),
+            "qkv": linear_hbm_bytes(batch, s.qkv_out, s.hidden, s.qkv_bias),
+            "o": linear_hbm_bytes(batch, s.hidden, s.heads * s.head_dim),
+            # gate||up writes silu(g) * u only
+            "gate_up": linear_hbm_bytes(batch, 2 * s.intermediate, s.hidden, out_cols=s.intermediate),
+            "down": linear_hbm_bytes(batch, s.hidden, s.intermediate),
+            "lm_head": linear_hbm_bytes(batch, s.vocab, s.hidden),
         }
 
     def buffers(self, batch: int) -> _Buffers:

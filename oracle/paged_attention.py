@@ -193,17 +193,3 @@ def decode_rows_split(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch
             accs.append(torch.einsum("ht,htd->hd", p, vc))
         out[b, :, 0, :] = merge_partials(torch.stack(ms, -1), torch.stack(ls, -1), torch.stack(accs, -2))
     return out
-
-
-def attention_bytes(seq_lens, num_kv_heads: int, head_dim: int, num_heads: int, block_size: int,
-                    elem_bytes: int = 2) -> int:
-    """Algorithmic HBM bytes of one batched decode-attention call.
-
-    K and V of every attended token are counted once per kv-head (GQA query
-    heads share them), plus q, out, the block ids actually read and seq_lens.
-    """
-    lens = [max(int(s), 0) for s in seq_lens]
-    kv = sum(lens) * num_kv_heads * head_dim * 2 * elem_bytes
-    qo = 2 * len(lens) * num_heads * head_dim * elem_bytes
-    meta = sum(math.ceil(s / block_size) for s in lens) * 4 + len(lens) * 4
-    return kv + qo + meta

@@ -168,7 +168,9 @@ def test_golden_attention_fixture_reproduces():
 
 
 def test_attention_bytes():
-    assert paged_attention.attention_bytes([16, 17], 8, 128, 32, 16) == (33 * 8 * 128 * 4 + 2 * 2 * 32 * 128 * 2
+    from runtime_amd.phase2.roofline import attention_hbm_bytes
+
+    assert attention_hbm_bytes([16, 17], 8, 128, 32, 16) == (33 * 8 * 128 * 4 + 2 * 2 * 32 * 128 * 2
                                                                          + 3 * 4 + 2 * 4)
 
 
