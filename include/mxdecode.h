@@ -119,10 +119,9 @@ int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t M, int64_t 
  * 8t + [0, 8) (scale and bias reordered the same way), quantized and packed
  * as usual. Replaces transformers' act_fn(gate_proj(x)) * up_proj(x) (reached
  * from worker_server.py:771-775) with one launch and half the output bytes.
- * Rows are processed 128 at a time, each chunk with mx_w8a16_linear's plan
- * (the VALU GEMV at M <= 4 on shapes that split, else the MFMA kernel); a chunk
- * whose MFMA launch would split K is refused (MX_ERR_UNSUPPORTED): the call
- * needs mx_w8a16_splits(c, 2I, K) == 1 for every chunk size c of M. */
+ * Rows are processed 128 at a time: the VALU GEMV where mx_w8a16_linear would
+ * take it (M <= 4 on shapes that split), else one MFMA launch that never splits
+ * K, whatever mx_w8a16_splits reports for the plain projection. */
 int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                            const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I, int64_t y_stride,
                            void* stream);

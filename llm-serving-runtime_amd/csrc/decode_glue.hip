@@ -277,12 +277,20 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(NormParams p)
             h[u] = v;
         }
     }
+    // The norm weights are loaded before the row reduction's barrier, so their round trip
+    // overlaps it instead of following it.
+    half8v wv[kNormMaxChunks];
+#pragma unroll
+    for (int u = 0; u < kNormMaxChunks; ++u) {
+        const int c = threadIdx.x + u * kNormThreads;
+        if (c < chunks) wv[u] = as_h8(ld16(p.w + c * 8));
+    }
     const float scale = rsqrtf(block_sum<kNormThreads>(ss, red) / (float)p.H + p.eps);
 #pragma unroll
     for (int u = 0; u < kNormMaxChunks; ++u) {
         const int c = threadIdx.x + u * kNormThreads;
         if (c < chunks) {
-            const half8v g = as_h8(ld16(p.w + c * 8));
+            const half8v g = wv[u];
             half8v o;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {

@@ -265,20 +265,204 @@ constexpr int kDepth = MX_PA_DEPTH;
 #define MX_PA_MIN_WAVES 3
 #endif
 
+// One piece: tiles [t0, t0 + nj) of segment (row b, kv-head kvh) with the row's effective length
+// s_eff. Leaves the online-softmax state of query head r = lane % 16 of the kv-head's group in
+// (m_run, l_run, acc): m_run on the exp2 scale, the same in all 4 lane groups; l_run this lane's
+// partial denominator (sum over the 4 lane groups with xor_sum_16_32); acc[e][i] the
+// unnormalised output of head r at dim (4g + i) * DPL + e, g = lane / 16. PROBE: the loads
+// alone (see decode_split_kernel).
+template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false, int P = kDepth>
+__device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t0, int nj, int s_eff, int lane,
+                                          float& m_run, float& l_run, float4v (&acc)[D / 16]) {
+    constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
+    constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
+    constexpr int TPB = BS >= kTile ? BS / kTile : 1;  // tiles per KV block (block sizes 16, 32)
+    constexpr int BPT = BS >= kTile ? 1 : kTile / BS;  // KV blocks per tile (block sizes 4, 8)
+    using VF = typename VFragT<D>::type;
+    using Regs = TileRegs<KK, VF>;
+    const float kNegInf = -__builtin_huge_valf();
+    const int g = lane >> 4, r = lane & 15;
+    const int h0 = kvh * G;
+    // K: token r, dims 8g + 32kk; V: tokens 4g + j, dims DPL*r + e. With BPT > 1 a tile spans
+    // BPT blocks: lane's K token lies in block slot kslot of the tile and its V tokens (and the
+    // 4 scores it holds) in slot vslot, at the given offsets inside those blocks.
+    const int koff = (BPT == 1 ? r : r % BS) * D + 8 * g;
+    const int voff = (BPT == 1 ? 4 * g : (4 * g) % BS) * D + DPL * r;
+    const int kslot = r / BS, vslot = (4 * g) / BS;
+
+    // Block ids of the piece: lane j holds the id of tile t0 + j (BPT == 1) or of block
+    // slot j of the piece's tiles (BPT > 1, only the row's blocks below s_eff are read);
+    // an id outside the pool becomes -1 (its tokens skipped, error recorded).
+    const int32_t* bt_row = p.bt + (int64_t)b * p.bt_sb;
+    int my_pb = 0;
+    bool fetch;
+    int bslot;
+    if constexpr (BPT == 1) {
+        fetch = lane < nj;
+        bslot = (t0 + lane) / TPB;
+    } else {
+        bslot = t0 * BPT + lane;
+        fetch = lane < nj * BPT && bslot < (s_eff + BS - 1) / BS;
+    }
+    if (fetch) {
+        my_pb = bt_row[bslot];
+        if ((unsigned)my_pb >= (unsigned)p.num_pool_blocks) {  // never read outside the pool
+            atomicOr(p.err, 1);
+            my_pb = -1;
+        }
+    }
+
+    // B operand: query head r (zero past G), dims 32*kk + 8*g + [0, 8).
+    half8v qf[KK];
+    if (r < G && !PROBE) {
+        const _Float16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h0 + r) * p.q_sh + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qf[kk] = load_half8(qp + 32 * kk);
+    } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qf[kk] = (_Float16)0.0f;
+    }
+
+    m_run = kNegInf;
+    l_run = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const _Float16* kbase = p.k + (int64_t)kvh * p.kv_shead;
+    const _Float16* vbase = p.v + (int64_t)kvh * p.kv_shead;
+
+    // Loads are unconditional: past the piece's last tile the index is clamped
+    // (an L2 hit) and a skipped block reads block 0; only the compute below is
+    // predicated, by wave-uniform flags, so waits count exact stages.
+    auto load_tile = [&](int j, Regs& tr) {
+        const int jc = j < nj ? j : nj - 1;
+        const _Float16* kt;
+        const _Float16* vt;
+        if constexpr (BPT == 1) {
+            const int pb = __builtin_amdgcn_readlane(my_pb, jc);
+            const int t = t0 + jc;
+            const int64_t base = (int64_t)(pb < 0 ? 0 : pb) * p.kv_sblk + (t % TPB) * kTile * D;
+            kt = kbase + base;
+            vt = vbase + base;
+        } else {
+            const int pk = __shfl(my_pb, jc * BPT + kslot);
+            const int pv = __shfl(my_pb, jc * BPT + vslot);
+            kt = kbase + (int64_t)(pk < 0 ? 0 : pk) * p.kv_sblk;
+            vt = vbase + (int64_t)(pv < 0 ? 0 : pv) * p.kv_sblk;
+        }
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_kv8<STREAM>(kt + koff + 32 * kk);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) tr.v[jj] = VFragT<D>::template load<STREAM>(vt + voff + jj * D);
+    };
+
+    auto compute_tile = [&](int j, const Regs& tr) {
+        const int t = t0 + j;
+        float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) s = Elt<BF16>::mma32(tr.k[kk], qf[kk], s);
+        // s[i] = score of token t*16 + 4g + i for head r.
+        const int tok0 = t * kTile + 4 * g;
+        // BPT > 1: this lane's 4 tokens lie in one block (slot vslot); a skipped block masks them.
+        const bool skipped = BPT > 1 && __shfl(my_pb, j * BPT + vslot) < 0;
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < s_eff && !skipped) ? s[i] * p.scale_log2e : kNegInf;
+        const float mx = xor_max_16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+        // Lazy rescale: the reference point m_run moves only when a score exceeds it
+        // by more than kLazyLog2, so p = exp2(s - m_run) <= 2^kLazyLog2 (exact range
+        // for fp16, same relative rounding) and acc / l is unchanged. Rescaling all
+        // accumulators at every new maximum cost ~100 instructions on most early tiles.
+        const bool grow = mx > m_run + kLazyLog2;  // always true on the first tile
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = grow ? mx : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+            l_run *= alpha;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
+            m_run = m_new;
+        }
+        half4v pv;
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pv[i] = Elt<BF16>::round(__builtin_amdgcn_exp2f(sc[i] - m_run));
+            // BPT > 1: every block of a tile may be outside the pool while m_run is still
+            // -inf; exp2(-inf - -inf) is NaN, so masked scores give p = 0 explicitly.
+            if constexpr (BPT > 1) pv[i] = sc[i] == kNegInf ? (_Float16)0.0f : pv[i];
+            psum += Elt<BF16>::widen(pv[i]);
+        }
+        l_run += psum;
+        // V rows past the sequence end are zeroed: p is 0 there, but stale pool
+        // memory may hold Inf/NaN, and 0 * NaN would poison the sum.
+        VF v[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) v[jj] = tr.v[jj];
+        if (t * kTile + kTile > s_eff || skipped) {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                if (tok0 + jj >= s_eff || skipped) v[jj] = VF{};
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) {
+            const half4v a = {v[0][e], v[1][e], v[2][e], v[3][e]};
+            acc[e] = Elt<BF16>::mma16(a, pv, acc[e]);
+        }
+    };
+
+    if constexpr (PROBE) {
+        Regs st[P];
+        uint32_t sum = 0;
+#pragma unroll
+        for (int s = 0; s < P; ++s) load_tile(s, st[s]);
+        for (int j0 = 0; j0 < nj; j0 += P) {
+#pragma unroll
+            for (int s = 0; s < P; ++s) {
+                if (j0 + s < nj) {
+                    const Regs& tr = st[s];
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk) {
+                        const uint4 w = __builtin_bit_cast(uint4, tr.k[kk]);
+                        sum ^= w.x ^ w.y ^ w.z ^ w.w;
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const auto w = __builtin_bit_cast(typename std::conditional<D == 128, uint4, uint2>::type,
+                                                          tr.v[jj]);
+                        sum ^= w.x ^ w.y;
+                    }
+                }
+                load_tile(j0 + s + P, st[s]);
+            }
+        }
+        if (sum == 0x9e3779b9u) p.err[1] = (int)sum;  // keeps the loads; practically never taken
+        return;
+    }
+    {
+        Regs st[P];
+#pragma unroll
+        for (int s = 0; s < P; ++s) load_tile(s, st[s]);
+        for (int j0 = 0; j0 < nj; j0 += P) {
+#pragma unroll
+            for (int s = 0; s < P; ++s) {
+                const int j = j0 + s;
+                if (j < nj && (BPT > 1 || __builtin_amdgcn_readlane(my_pb, j) >= 0)) compute_tile(j, st[s]);
+                load_tile(j + P, st[s]);
+            }
+        }
+    }
+
+}
+
 // PROBE = true: the calibration instance of mx_kv_gather_probe. The same partition and the same
 // K/V loads, with the math replaced by an xor of the loaded words (nothing is written unless
 // that checksum hits a magic value), so its duration is the gather alone.
 template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false>
 __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
-    constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
-    constexpr int TPB = BS >= kTile ? BS / kTile : 1;  // tiles per KV block (block sizes 16, 32)
     constexpr int BPT = BS >= kTile ? 1 : kTile / BS;  // KV blocks per tile (block sizes 4, 8)
     constexpr int kMaxRange = kMaxRangeTiles / BPT;    // tiles whose block ids fit one vector
-    constexpr int P = kDepth;
     using VF = typename VFragT<D>::type;
-    using Regs = TileRegs<KK, VF>;
-    const float kNegInf = -__builtin_huge_valf();
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -300,13 +484,6 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
     if (worker >= W) return;
     const int64_t hi = range_lo(worker + 1, T, W);
     int64_t x = range_lo(worker, T, W);
-
-    // K: token r, dims 8g + 32kk; V: tokens 4g + j, dims DPL*r + e. With BPT > 1 a tile spans
-    // BPT blocks: lane's K token lies in block slot kslot of the tile and its V tokens (and the
-    // 4 scores it holds) in slot vslot, at the given offsets inside those blocks.
-    const int koff = (BPT == 1 ? r : r % BS) * D + 8 * g;
-    const int voff = (BPT == 1 ? 4 * g : (4 * g) % BS) * D + DPL * r;
-    const int kslot = r / BS, vslot = (4 * g) / BS;
 
     while (x < hi) {
         Seg sg;
@@ -336,169 +513,10 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
         if (one_pass) s_eff = __builtin_amdgcn_readlane(s_eff_lane, b);
         else row_tiles<BS>(p, b, s_eff);
         const int h0 = kvh * G;
-
-        // Block ids of the piece: lane j holds the id of tile t0 + j (BPT == 1) or of block
-        // slot j of the piece's tiles (BPT > 1, only the row's blocks below s_eff are read);
-        // an id outside the pool becomes -1 (its tokens skipped, error recorded).
-        const int32_t* bt_row = p.bt + (int64_t)b * p.bt_sb;
-        int my_pb = 0;
-        bool fetch;
-        int bslot;
-        if constexpr (BPT == 1) {
-            fetch = lane < nj;
-            bslot = (t0 + lane) / TPB;
-        } else {
-            bslot = t0 * BPT + lane;
-            fetch = lane < nj * BPT && bslot < (s_eff + BS - 1) / BS;
-        }
-        if (fetch) {
-            my_pb = bt_row[bslot];
-            if ((unsigned)my_pb >= (unsigned)p.num_pool_blocks) {  // never read outside the pool
-                atomicOr(p.err, 1);
-                my_pb = -1;
-            }
-        }
-
-        // B operand: query head r (zero past G), dims 32*kk + 8*g + [0, 8).
-        half8v qf[KK];
-        if (r < G && !PROBE) {
-            const _Float16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h0 + r) * p.q_sh + 8 * g;
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) qf[kk] = load_half8(qp + 32 * kk);
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) qf[kk] = (_Float16)0.0f;
-        }
-
-        float m_run = kNegInf;  // running max of head r (same in all 4 lane groups)
-        float l_run = 0.0f;     // partial denominator over this lane's tokens
-        float4v acc[DPL];       // acc[e][i]: head r, dim (4g + i) * DPL + e
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-
-        const _Float16* kbase = p.k + (int64_t)kvh * p.kv_shead;
-        const _Float16* vbase = p.v + (int64_t)kvh * p.kv_shead;
-
-        // Loads are unconditional: past the piece's last tile the index is clamped
-        // (an L2 hit) and a skipped block reads block 0; only the compute below is
-        // predicated, by wave-uniform flags, so waits count exact stages.
-        auto load_tile = [&](int j, Regs& tr) {
-            const int jc = j < nj ? j : nj - 1;
-            const _Float16* kt;
-            const _Float16* vt;
-            if constexpr (BPT == 1) {
-                const int pb = __builtin_amdgcn_readlane(my_pb, jc);
-                const int t = t0 + jc;
-                const int64_t base = (int64_t)(pb < 0 ? 0 : pb) * p.kv_sblk + (t % TPB) * kTile * D;
-                kt = kbase + base;
-                vt = vbase + base;
-            } else {
-                const int pk = __shfl(my_pb, jc * BPT + kslot);
-                const int pv = __shfl(my_pb, jc * BPT + vslot);
-                kt = kbase + (int64_t)(pk < 0 ? 0 : pk) * p.kv_sblk;
-                vt = vbase + (int64_t)(pv < 0 ? 0 : pv) * p.kv_sblk;
-            }
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) tr.k[kk] = load_kv8<STREAM>(kt + koff + 32 * kk);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) tr.v[jj] = VFragT<D>::template load<STREAM>(vt + voff + jj * D);
-        };
-
-        auto compute_tile = [&](int j, const Regs& tr) {
-            const int t = t0 + j;
-            float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) s = Elt<BF16>::mma32(tr.k[kk], qf[kk], s);
-            // s[i] = score of token t*16 + 4g + i for head r.
-            const int tok0 = t * kTile + 4 * g;
-            // BPT > 1: this lane's 4 tokens lie in one block (slot vslot); a skipped block masks them.
-            const bool skipped = BPT > 1 && __shfl(my_pb, j * BPT + vslot) < 0;
-            float sc[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sc[i] = (tok0 + i < s_eff && !skipped) ? s[i] * p.scale_log2e : kNegInf;
-            const float mx = xor_max_16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-            // Lazy rescale: the reference point m_run moves only when a score exceeds it
-            // by more than kLazyLog2, so p = exp2(s - m_run) <= 2^kLazyLog2 (exact range
-            // for fp16, same relative rounding) and acc / l is unchanged. Rescaling all
-            // accumulators at every new maximum cost ~100 instructions on most early tiles.
-            const bool grow = mx > m_run + kLazyLog2;  // always true on the first tile
-            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-                const float m_new = grow ? mx : m_run;
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
-                l_run *= alpha;
-#pragma unroll
-                for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
-                m_run = m_new;
-            }
-            half4v pv;
-            float psum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pv[i] = Elt<BF16>::round(__builtin_amdgcn_exp2f(sc[i] - m_run));
-                // BPT > 1: every block of a tile may be outside the pool while m_run is still
-                // -inf; exp2(-inf - -inf) is NaN, so masked scores give p = 0 explicitly.
-                if constexpr (BPT > 1) pv[i] = sc[i] == kNegInf ? (_Float16)0.0f : pv[i];
-                psum += Elt<BF16>::widen(pv[i]);
-            }
-            l_run += psum;
-            // V rows past the sequence end are zeroed: p is 0 there, but stale pool
-            // memory may hold Inf/NaN, and 0 * NaN would poison the sum.
-            VF v[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) v[jj] = tr.v[jj];
-            if (t * kTile + kTile > s_eff || skipped) {
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-                    if (tok0 + jj >= s_eff || skipped) v[jj] = VF{};
-            }
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) {
-                const half4v a = {v[0][e], v[1][e], v[2][e], v[3][e]};
-                acc[e] = Elt<BF16>::mma16(a, pv, acc[e]);
-            }
-        };
-
-        if constexpr (PROBE) {
-            Regs st[P];
-            uint32_t sum = 0;
-#pragma unroll
-            for (int s = 0; s < P; ++s) load_tile(s, st[s]);
-            for (int j0 = 0; j0 < nj; j0 += P) {
-#pragma unroll
-                for (int s = 0; s < P; ++s) {
-                    if (j0 + s < nj) {
-                        const Regs& tr = st[s];
-#pragma unroll
-                        for (int kk = 0; kk < KK; ++kk) {
-                            const uint4 w = __builtin_bit_cast(uint4, tr.k[kk]);
-                            sum ^= w.x ^ w.y ^ w.z ^ w.w;
-                        }
-#pragma unroll
-                        for (int jj = 0; jj < 4; ++jj) {
-                            const auto w = __builtin_bit_cast(typename std::conditional<D == 128, uint4, uint2>::type,
-                                                              tr.v[jj]);
-                            sum ^= w.x ^ w.y;
-                        }
-                    }
-                    load_tile(j0 + s + P, st[s]);
-                }
-            }
-            if (sum == 0x9e3779b9u) p.err[1] = (int)sum;  // keeps the loads; practically never taken
-            continue;
-        }
-        {
-            Regs st[P];
-#pragma unroll
-            for (int s = 0; s < P; ++s) load_tile(s, st[s]);
-            for (int j0 = 0; j0 < nj; j0 += P) {
-#pragma unroll
-                for (int s = 0; s < P; ++s) {
-                    const int j = j0 + s;
-                    if (j < nj && (BPT > 1 || __builtin_amdgcn_readlane(my_pb, j) >= 0)) compute_tile(j, st[s]);
-                    load_tile(j + P, st[s]);
-                }
-            }
-        }
+        float m_run, l_run;
+        float4v acc[DPL];
+        run_piece<D, BS, G, STREAM, BF16, PROBE>(p, b, kvh, t0, nj, s_eff, lane, m_run, l_run, acc);
+        if constexpr (PROBE) continue;
 
         // Denominator of head r over the 4 lane groups; acc already sums all 16 tokens of a tile.
         l_run = xor_sum_16_32(l_run);

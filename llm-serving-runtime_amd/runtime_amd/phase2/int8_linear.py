@@ -132,17 +132,10 @@ def linear_splits(m: int, n: int, k: int) -> int:
     return int(_hip.load().mx_w8a16_splits(m, n, k))
 
 
-MAX_CHUNK_ROWS = 128  # rows per launch of the linear kernels; larger M runs in chunks
-
-
 def gateup_fusable(m: int, n: int, k: int) -> bool:
-    """Whether :func:`int8_gateup_swiglu` takes ``m`` rows of a ``[n, k]`` gate||up weight:
-    no 128-row chunk of ``m`` may split K (``mx_w8a16_splits(chunk, n, k) == 1``; the VALU
-    GEMV at ``chunk <= 4`` never splits)."""
-    sizes = {min(m, MAX_CHUNK_ROWS)}
-    if m > MAX_CHUNK_ROWS and m % MAX_CHUNK_ROWS:
-        sizes.add(m % MAX_CHUNK_ROWS)
-    return all(linear_splits(c, n, k) == 1 for c in sizes)
+    """Whether :func:`int8_gateup_swiglu` takes ``m`` rows of a ``[n, k]`` gate||up weight: any
+    ``m >= 1`` (its launches never split K; ``n`` a multiple of 16, ``k`` of 64)."""
+    return m >= 1 and n % 16 == 0 and k % 64 == 0
 
 
 def int8_linear_partials(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, out_features: int,

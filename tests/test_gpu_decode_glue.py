@@ -105,9 +105,14 @@ def test_pool_write_tokens_batch_uses_kernel_and_keeps_reference_errors():
     v_ref = pool.v_layer_view(0).cpu().clone()
     og.append_tokens(k_ref, v_ref, tables.cpu(), start.tolist(), ks.cpu(), vs.cpu())
     pool.write_tokens_batch(0, tables, start, ks, vs)
+    pool.check_write_errors()
     assert torch.equal(pool.k_layer_view(0).cpu(), k_ref) and torch.equal(pool.v_layer_view(0).cpu(), v_ref)
+    # Row 1 at positions 47..49 runs past its 3 blocks: the write is queued without a host sync,
+    # the slots inside the table are written, and the reference's IndexError comes from the check.
+    pool.write_tokens_batch(0, tables, torch.tensor([5, 47], device=DEV), ks, vs)
     with pytest.raises(IndexError):
-        pool.write_tokens_batch(0, tables, torch.tensor([5, 47], device=DEV), ks, vs)
+        pool.check_write_errors()
+    assert torch.equal(pool.k_layer_view(0)[4, :, 15].cpu(), ks[1, :, 0].cpu())
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64)])

@@ -133,7 +133,8 @@ def test_native_step_qwen2_shape_small_batches(batch):
     (whose MFMA launch would split K) with the SwiGLU product in the GEMV's epilogue."""
     from runtime_amd.phase2.int8_linear import gateup_fusable, linear_splits
 
-    assert linear_splits(5, 2 * 4864, 896) > 1 and gateup_fusable(batch, 2 * 4864, 896)
+    assert linear_splits(5, 2 * 4864, 896) > 1 and linear_splits(batch, 2 * 4864, 896) == 1
+    assert gateup_fusable(batch, 2 * 4864, 896)
     _run(om.random_qwen2(seed=4, num_hidden_layers=2, vocab_size=32768), batch=batch, lo=30, hi=200, seed=4,
          graph=batch == 4)
 

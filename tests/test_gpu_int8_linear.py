@@ -243,9 +243,11 @@ def test_swiglu_linear_equals_silu_mul_then_linear(m, n, k):
                                         (4, 4864, 896), (1, 14336, 4096), (4, 14336, 4096)])
 def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     """gate||up with interleaved rows and the SwiGLU product in the epilogue equals the plain
-    [gate | up] projection followed by mx_silu_mul, bit for bit. At M <= 4 on the Qwen2-0.5B
+    [gate | up] projection followed by mx_silu_mul, bit for bit where both take the same K
+    accumulation (within fp16 rounding where the plain projection splits K). At M <= 4 on the Qwen2-0.5B
     MLP (a shape whose MFMA launch splits K) the VALU GEMV takes both, with the product in
-    the GEMV's own epilogue; the Llama MLP at M <= 4 runs the unsplit MFMA kernel."""
+    the GEMV's own epilogue; the Llama MLP at M <= 4 runs the unsplit MFMA kernel, and shapes whose
+    plain projection splits K (the Qwen2 MLP at 7 and 70 rows) run one unsplit MFMA launch."""
     from runtime_amd.phase2.decode_glue import silu_mul
     from runtime_amd.phase2.int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu,
                                                 linear_splits)
@@ -260,10 +262,14 @@ def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     iq, iscale = quantize_weight(inter_w)
     assert torch.equal(gateup_interleave(plain_s[:inter], plain_s[inter:]), iscale)  # row-wise quantization
     want = silu_mul(int8_linear(x, pack_weight(plain_q), plain_s, None, 2 * inter))
-    if linear_splits(min(m, 128), 2 * inter, k) != 1:
-        pytest.skip("gate||up splits K at this shape; the epilogue fusion does not apply")
     got = int8_gateup_swiglu(x, pack_weight(iq), iscale, None, inter)
-    assert torch.equal(got, want)
+    if linear_splits(min(m, 128), 2 * inter, k) == 1:
+        assert torch.equal(got, want)
+    else:
+        # The plain projection sums two scaled split partials; the fused launch scales one sum over
+        # the whole K: the same value up to fp32 rounding, so g and u may differ by an fp16 ulp.
+        torch.testing.assert_close(got, want, atol=1e-2, rtol=1e-2)
+        assert (got.float() - want.float()).abs().max() <= 4e-3 * want.float().abs().max()
 
 
 # N chosen so that the unsplit launch takes each wide workgroup shape: about one
