@@ -399,29 +399,39 @@ def family_launches(d: Decoder) -> dict:
     return out
 
 
-def headline(args, d: Decoder) -> dict:
+def family_table(d: Decoder, args, lens_after) -> tuple[dict, dict, dict, dict]:
+    """Per kernel family of the step: seconds per launch (graph replays of that family's launches
+    alone, run after the timed steps, so at contexts ``lens_after`` + 1), algorithmic bytes per
+    launch, launches per step, and the JSON entries."""
     from runtime_amd.phase2.roofline import attention_hbm_bytes
 
-    s, bsz = d.shape, d.batch
-    lens_before = d.seq_lens.cpu().tolist()
-    ms = time_step(d.step, args.steps, args.warmup, use_graph=not args.no_graph)
-    lens_after = d.seq_lens.cpu().tolist()
+    s = d.shape
     kdur = {name: graph_time(run, launches, args.kernel_steps) for name, (run, launches) in family_launches(d).items()}
-    lin = d.model.linear_bytes(bsz)
-    step_bytes = d.step_bytes(lens_before, lens_after)
-    # The family graphs ran after the timed steps, at contexts lens_after (+1 token).
     per_launch = {"attn": attention_hbm_bytes([x + 1 for x in lens_after], s.kv_heads, s.head_dim, s.heads, d.bs),
-                  **lin}
+                  **d.model.linear_bytes(d.batch)}
     per_step = {k: (d.n_layers if k != "lm_head" else 1) for k in kdur}
-    dominant = max(kdur, key=lambda k: kdur[k] * per_step[k])
-    counters = committed_figures(GEMM_COUNTER_PROFILE, "gemm-counters")
     kernels = {}
     for k in kdur:
         gbps = per_launch[k] / kdur[k] / 1e9
         kernels[k] = {"avg_us": round(kdur[k] * 1e6, 2), "launches_per_step": per_step[k],
                       "bytes_per_launch": per_launch[k], "gbps": round(gbps, 1), "frac": frac(gbps)}
-        if k in counters:
-            kernels[k]["counters"] = counters[k]
+    return kdur, per_launch, per_step, kernels
+
+
+def headline(args, d: Decoder) -> dict:
+    s, bsz = d.shape, d.batch
+    lens_before = d.seq_lens.cpu().tolist()
+    ms = time_step(d.step, args.steps, args.warmup, use_graph=not args.no_graph)
+    lens_after = d.seq_lens.cpu().tolist()
+    kdur, per_launch, per_step, kernels = family_table(d, args, lens_after)
+    lin = d.model.linear_bytes(bsz)
+    step_bytes = d.step_bytes(lens_before, lens_after)
+    dominant = max(kdur, key=lambda k: kdur[k] * per_step[k])
+    counters = committed_figures(GEMM_COUNTER_PROFILE, "gemm-counters")
+    if bsz == 32 and args.model == "llama3-8b":
+        for k in kernels:
+            if k in counters:
+                kernels[k]["counters"] = counters[k]
     layer_linear_b = sum(lin[k] for k in ("qkv", "o", "gate_up", "down"))
     layer_linear_s = sum(kdur[k] for k in ("qkv", "o", "gate_up", "down"))
     achieved = per_launch[dominant] / kdur[dominant] / 1e9
@@ -643,6 +653,7 @@ def config3_qwen(args) -> dict:
     lens_after = d.seq_lens.cpu().tolist()
     byts = d.step_bytes(lens_before, lens_after)
     gbps = byts / (ms * 1e-3) / 1e9
+    kdur, _, per_step, kernels = family_table(d, args, lens_after)
     out = {
         "workload": "Qwen2-0.5B-shaped int8 decode step (hidden 896, 24 layers, 14/2 heads, head_dim 64, "
                     "SwiGLU 4864, vocab 151936, qkv bias), batch 16, contexts U[512,2048] seed 0, block 16, "
@@ -650,6 +661,10 @@ def config3_qwen(args) -> dict:
         "value": round(16 / (ms * 1e-3), 2), "unit": "tokens/s", "ms_per_step": round(ms, 4),
         "step_hbm_bytes": byts, "gbps": round(gbps, 1), "frac": frac(gbps),
         "roofline_tokens_per_s": round(16 / (byts / (HBM_PEAK_GBPS * 1e9)), 1),
+        "kernels": kernels,
+        # Step time not covered by the families' own graph-replay time: the RMSNorm/residual
+        # launches, the embedding and argmax, and the dependency gaps between launches.
+        "other_us_per_step": round(ms * 1e3 - sum(kdur[k] * per_step[k] for k in kdur) * 1e6, 1),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_step_baseline(QWEN2_05B, 16, d.lens.tolist(), d.n_layers)
