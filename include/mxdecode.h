@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 12
+#define MX_ABI_VERSION 13
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -338,6 +338,17 @@ int mx_add_rmsnorm_splits(const float* partials, int32_t splits, const uint16_t*
  * KV lengths past the token just decoded. */
 int mx_argmax_rows(const uint16_t* logits, int64_t stride, int32_t M, int32_t N, int64_t* out, int32_t* seq_lens,
                    void* stream);
+
+/* mx_argmax_rows with each row cut into 4096-logit chunks reduced by separate
+ * workgroups (two launches on `stream`), for rows too long for one CU to read
+ * fast: the same results (first index on ties, -0 == +0, the first NaN above
+ * any number). workspace: at least mx_argmax_workspace_bytes(M, N) bytes,
+ * 8-byte aligned, not shared by concurrent calls; it needs no initialisation.
+ * M <= 65535. Same reference counterpart as mx_argmax_rows
+ * (worker_server.py:786). */
+size_t mx_argmax_workspace_bytes(int32_t M, int32_t N);
+int mx_argmax_rows_split(const uint16_t* logits, int64_t stride, int32_t M, int32_t N, int64_t* out,
+                         int32_t* seq_lens, void* workspace, size_t workspace_bytes, void* stream);
 
 /* SwiGLU of the interleaved gate||up projection used by mx_w8a16_gateup_swiglu
  * (rows 16t + [0, 8) gate channels 8t + [0, 8), rows 16t + [8, 16) the matching

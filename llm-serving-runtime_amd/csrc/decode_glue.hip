@@ -359,6 +359,88 @@ __global__ __launch_bounds__(kThreads) void swiglu_interleaved_kernel(const uint
     st16(out + m * os + 8 * t, as_u4(o));
 }
 
+// Chunked greedy argmax (mx_argmax_rows_split): workgroup (c, m) reduces logits
+// [c * kArgChunk, (c + 1) * kArgChunk) of row m to one 64-bit key, and one wave per row takes
+// the largest key. A key orders (value, index) the way torch.argmax does: the value as an
+// order-preserving 17-bit code of the fp16 bits (-0 coded as +0, so they tie; NaN above +inf)
+// in the high word, and 0xffffffff - index in the low word, so the larger key of two equal
+// values is the earlier index. A row is thus read once, by many CUs: one workgroup per row
+// (argmax_kernel below) is bounded by what one CU streams (~50 GB/s), 18.6 us for 16 rows of
+// 151936 logits on MI355X.
+constexpr int kArgChunk = 4096;
+constexpr int kArgChunkThreads = 256;  // 16 logits per thread
+
+__device__ __forceinline__ uint64_t argmax_key(uint32_t bits, uint32_t idx) {
+    bits &= 0xffffu;
+    const uint32_t mag = bits & 0x7fffu;
+    uint32_t ord = (bits & 0x8000u) ? 0x7fffu - mag : 0x8000u + mag;  // -x below +y, larger |x| lower
+    ord = mag == 0 ? 0x8000u : ord;                                   // -0 == +0
+    ord = mag > 0x7c00u ? 0x10000u : ord;                             // NaN above every number
+    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)v, o), hi = __shfl_xor((uint32_t)(v >> 32), o);
+        v = max_u64(v, ((uint64_t)hi << 32) | lo);
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(kArgChunkThreads) void argmax_chunk_kernel(const uint16_t* __restrict__ logits,
+                                                                         int64_t ls, int N, uint64_t* __restrict__ keys,
+                                                                         int nchunks) {
+    constexpr int kIters = kArgChunk / (8 * kArgChunkThreads);
+    const int chunk = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+    const uint16_t* row = logits + (int64_t)m * ls;
+    const int base = chunk * kArgChunk;
+    uint4 v[kIters];
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {  // both loads in flight before the first compare
+        const int n0 = base + (it * kArgChunkThreads + tid) * 8;
+        v[it] = n0 + 8 <= N ? *reinterpret_cast<const uint4*>(row + n0) : uint4{0, 0, 0, 0};
+    }
+    uint64_t best = 0;  // below every key: the lowest number (-inf) has code 0x3ff
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+        const int n0 = base + (it * kArgChunkThreads + tid) * 8;
+        if (n0 + 8 <= N) {
+            const uint32_t w[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                best = max_u64(best, argmax_key(w[j], (uint32_t)(n0 + 2 * j)));
+                best = max_u64(best, argmax_key(w[j] >> 16, (uint32_t)(n0 + 2 * j + 1)));
+            }
+        } else {
+            for (int e = 0; e < 8 && n0 + e < N; ++e) best = max_u64(best, argmax_key(row[n0 + e], (uint32_t)(n0 + e)));
+        }
+    }
+    best = wave_max_u64(best);
+    __shared__ uint64_t s_best[kArgChunkThreads / 64];
+    if ((tid & 63) == 0) s_best[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+#pragma unroll
+        for (int w = 1; w < kArgChunkThreads / 64; ++w) best = max_u64(best, s_best[w]);
+        keys[(int64_t)m * nchunks + chunk] = best;
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_keys_kernel(const uint64_t* __restrict__ keys, int nchunks,
+                                                         int64_t* __restrict__ out, int32_t* seq_lens) {
+    const int m = blockIdx.x, lane = threadIdx.x;
+    uint64_t best = 0;
+    for (int c = lane; c < nchunks; c += 64) best = max_u64(best, keys[(int64_t)m * nchunks + c]);
+    best = wave_max_u64(best);
+    if (lane == 0) {
+        out[m] = (int64_t)(0xffffffffu - (uint32_t)best);
+        if (seq_lens) seq_lens[m] += 1;
+    }
+}
+
 // Greedy token of each row: index of the largest logit, the first one on ties; NaN counts as
 // larger than any number (torch.argmax's convention). One workgroup of 1024 threads per row.
 constexpr int kArgThreads = 1024;
@@ -665,4 +747,32 @@ extern "C" int mx_argmax_rows(const uint16_t* logits, int64_t stride, int32_t M,
     hipLaunchKernelGGL(glue::argmax_kernel, dim3(M), dim3(glue::kArgThreads), 0, as_stream(stream), logits, stride, N,
                        out, seq_lens);
     return check_launch("mx_argmax_rows");
+}
+
+extern "C" size_t mx_argmax_workspace_bytes(int32_t M, int32_t N) {
+    if (M <= 0 || N <= 0) return 0;
+    return (size_t)M * (size_t)ceil_div((int64_t)N, glue::kArgChunk) * sizeof(uint64_t);
+}
+
+extern "C" int mx_argmax_rows_split(const uint16_t* logits, int64_t stride, int32_t M, int32_t N, int64_t* out,
+                                    int32_t* seq_lens, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    const char* what = "mx_argmax_rows_split";
+    if (M < 0 || N <= 0) return fail(MX_ERR_INVALID, "%s: need M >= 0 and N > 0", what);
+    if (M == 0) return MX_OK;
+    if (M > 65535) return fail(MX_ERR_UNSUPPORTED, "%s: M > 65535", what);
+    if (!logits || !out || !workspace) return fail(MX_ERR_NULL, "%s: null pointer", what);
+    if (stride < N || stride % 8 || !glue::a16(logits))
+        return fail(MX_ERR_ALIGNMENT, "%s: rows must be 16-byte aligned and cover N", what);
+    if (reinterpret_cast<uintptr_t>(workspace) % 8) return fail(MX_ERR_ALIGNMENT, "%s: workspace alignment", what);
+    const size_t need = mx_argmax_workspace_bytes(M, N);
+    if (workspace_bytes < need)
+        return fail(MX_ERR_WORKSPACE, "%s: workspace needs %zu bytes, got %zu", what, need, workspace_bytes);
+    const int nchunks = (int)ceil_div((int64_t)N, glue::kArgChunk);
+    uint64_t* keys = static_cast<uint64_t*>(workspace);
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(glue::argmax_chunk_kernel, dim3(nchunks, M), dim3(glue::kArgChunkThreads), 0, st, logits, stride,
+                       N, keys, nchunks);
+    hipLaunchKernelGGL(glue::argmax_keys_kernel, dim3(M), dim3(64), 0, st, keys, nchunks, out, seq_lens);
+    return check_launch(what);
 }

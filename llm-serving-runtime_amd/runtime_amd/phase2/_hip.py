@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -74,6 +74,8 @@ SIGNATURES = {
         [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, ctypes.c_float, _p, _i64, _p, _i64, _p],
     ),
     "mx_argmax_rows": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p]),
+    "mx_argmax_workspace_bytes": (ctypes.c_size_t, [_i32, _i32]),
+    "mx_argmax_rows_split": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, ctypes.c_size_t, _p]),
     "mx_swiglu_interleaved": (ctypes.c_int, [_p, _i64, _p, _i32, _p, _i32, _i32, _p, _i64, _p]),
     "mx_qkv_rope_append_splits": (
         ctypes.c_int,

@@ -37,9 +37,13 @@ def _i32(t: torch.Tensor, device: torch.device) -> torch.Tensor:
 
 
 def _rows16(t: torch.Tensor) -> torch.Tensor:
-    """2-D fp16 view with unit inner stride and 16-byte aligned rows (copy if needed)."""
+    """2-D fp16 view with unit inner stride and 16-byte aligned rows (copied into rows padded to a
+    multiple of 8 elements if needed)."""
     if t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
-        t = t.contiguous()
+        n = int(t.shape[-1])
+        buf = torch.empty(int(t.shape[0]), (n + 7) // 8 * 8, dtype=t.dtype, device=t.device)
+        buf[:, :n].copy_(t)
+        t = buf[:, :n]
     return t
 
 
@@ -51,9 +55,29 @@ def _lens_ptr(lens_out: torch.Tensor | None, b: int):
     return lens_out.data_ptr()
 
 
-def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None,
-                seq_lens: torch.Tensor | None = None) -> torch.Tensor:
-    """Greedy tokens ``[M]`` (int64) of fp16 ``logits [M, N]``; ``seq_lens`` (int32) is advanced by one."""
+_argmax_workspaces: dict[tuple, torch.Tensor] = {}
+
+
+def argmax_workspace(device: torch.device, m: int, n: int) -> torch.Tensor:
+    """The chunk keys of ``mx_argmax_rows_split`` for ``[m, n]`` logits, cached per device and
+    shape (created outside graph capture, like the attention workspaces)."""
+    key = (torch.device(device), int(m), int(n))
+    ws = _argmax_workspaces.get(key)
+    if ws is None:
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("argmax workspace must be created before graph capture; run one eager call first")
+        nbytes = int(_hip.load().mx_argmax_workspace_bytes(int(m), int(n)))
+        ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=device)
+        _argmax_workspaces[key] = ws
+    return ws
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None,
+                split: bool = True) -> torch.Tensor:
+    """Greedy tokens ``[M]`` (int64) of fp16 ``logits [M, N]``; ``seq_lens`` (int32) is advanced by one.
+    ``split`` (default) reduces each row in 4096-logit chunks across workgroups
+    (``mx_argmax_rows_split``); ``split=False`` runs one workgroup per row (``mx_argmax_rows``).
+    Both give torch.argmax's index."""
     _hip.require_device_tensor(logits, "logits")
     if logits.dtype != torch.float16 or logits.dim() != 2:
         raise ValueError("argmax_rows expects fp16 logits [M, N]")
@@ -64,9 +88,15 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None,
         raise ValueError("out must be a contiguous int64 tensor of M elements")
     if seq_lens is not None and (seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous()):
         raise ValueError("seq_lens must be a contiguous int32 tensor")
-    _hip.check(_hip.load().mx_argmax_rows(lg.data_ptr(), lg.stride(0), m, n, out.data_ptr(),
-                                          seq_lens.data_ptr() if seq_lens is not None else None,
-                                          _hip.stream_handle(lg.device)), "mx_argmax_rows")
+    lens_p = seq_lens.data_ptr() if seq_lens is not None else None
+    lib = _hip.load()
+    if split and 0 < m <= 65535:
+        ws = argmax_workspace(lg.device, m, n)
+        _hip.check(lib.mx_argmax_rows_split(lg.data_ptr(), lg.stride(0), m, n, out.data_ptr(), lens_p, ws.data_ptr(),
+                                            ws.numel(), _hip.stream_handle(lg.device)), "mx_argmax_rows_split")
+    else:
+        _hip.check(lib.mx_argmax_rows(lg.data_ptr(), lg.stride(0), m, n, out.data_ptr(), lens_p,
+                                      _hip.stream_handle(lg.device)), "mx_argmax_rows")
     return out
 
 

@@ -19,7 +19,7 @@ current stream:
     a = silu(x Wg^T) * (x Wu^T)            mx_w8a16_gateup_swiglu (gate and up rows
                                            interleaved by 8, product in the epilogue)
     h += a Wdown^T                         mx_w8a16_linear (+ the next add_rmsnorm)
-    logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, mx_argmax_rows
+    logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, mx_argmax_rows_split
 
 The first norm gathers the embedding rows of the step's tokens itself, layer
 0's RoPE kernel writes the attention lengths (positions + 1) and the argmax

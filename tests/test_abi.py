@@ -105,6 +105,16 @@ def test_invalid_arguments_return_status_codes():
     _status(call(flags=4), _hip.MX_ERR_INVALID)  # only MX_PA_SHARED_BLOCKS and MX_PA_BF16 are defined
     _status(call(), _hip.MX_ERR_WORKSPACE)
     _status(call(q_sh=60), _hip.MX_ERR_ALIGNMENT)
+    # Chunked argmax: the key workspace is M x ceil(N / 4096) x 8 bytes, and every argument is
+    # checked before anything is launched.
+    assert lib.mx_argmax_workspace_bytes(16, 151936) == 16 * 38 * 8
+    assert lib.mx_argmax_workspace_bytes(1, 4096) == 8 and lib.mx_argmax_workspace_bytes(1, 4097) == 16
+    assert lib.mx_argmax_workspace_bytes(0, 10) == 0
+    assert lib.mx_argmax_rows_split(fake, 64, 0, 64, fake, None, None, 0, None) == _hip.MX_OK
+    _status(lib.mx_argmax_rows_split(fake, 64, 2, 64, fake, None, None, 0, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_argmax_rows_split(fake, 64, 2, 64, fake, None, fake, 8, None), _hip.MX_ERR_WORKSPACE)
+    _status(lib.mx_argmax_rows_split(fake, 60, 2, 60, fake, None, fake, 64, None), _hip.MX_ERR_ALIGNMENT)
+    _status(lib.mx_argmax_rows_split(fake, 64, 2, 0, fake, None, fake, 64, None), _hip.MX_ERR_INVALID)
     with pytest.raises(ValueError):
         _hip.check(_hip.MX_ERR_INVALID, "probe")
     with pytest.raises(RuntimeError):

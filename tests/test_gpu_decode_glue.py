@@ -335,18 +335,42 @@ def test_add_rmsnorm_gathers_rows():
     assert float(out[~valid.to(DEV)].abs().max()) == 0.0
 
 
-@pytest.mark.parametrize("m,n", [(1, 8), (3, 128256), (32, 151936), (5, 1000)])
-def test_argmax_rows_matches_torch(m, n):
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("m,n", [(1, 8), (3, 128256), (32, 151936), (5, 1000), (2, 4096), (2, 4097), (128, 128256)])
+def test_argmax_rows_matches_torch(m, n, split):
     from runtime_amd.phase2.decode_glue import argmax_rows
 
     g = torch.Generator().manual_seed(m * 1000 + n)
     logits = torch.randn(m, n, generator=g).half()
-    got = argmax_rows(logits.to(DEV)).cpu()
+    got = argmax_rows(logits.to(DEV), split=split).cpu()
     assert got.dtype == torch.int64
     assert torch.equal(got, logits.float().argmax(dim=-1))
 
 
-def test_argmax_rows_ties_nan_inf_and_lengths():
+def test_argmax_split_ties_across_chunks_and_signed_zero():
+    """The chunked argmax keys: equal maxima in different 4096-logit chunks give the first index;
+    -0 and +0 tie (the first wins, as torch compares values); the smallest negative numbers order
+    below -0 and above -inf; a NaN in a later chunk still wins over +inf in an earlier one."""
+    from runtime_amd.phase2.decode_glue import argmax_rows
+
+    n = 3 * 4096 + 5
+    lg = torch.full((6, n), -1.0, dtype=torch.float16)
+    lg[0, [9000, 4100, 12000]] = 3.0                     # first of three equal maxima: 4100
+    lg[1, :] = 0.0; lg[1, :5000] = -0.0                  # -0 before +0: index 0
+    lg[2, :] = float("-inf"); lg[2, 7000] = -65504.0     # the only finite value
+    lg[2, 8000] = -2.0**-24                              # smallest-magnitude negative beats -65504
+    lg[3, 100] = float("inf"); lg[3, 8200] = float("nan")
+    lg[4, n - 1] = 0.5; lg[4, n - 5] = 0.5               # ties in the partial last chunk
+    lg[5, :] = float("nan")                              # all NaN: index 0
+    want = [4100, 0, 8000, 8200, n - 5, 0]
+    for split in (True, False):
+        got = argmax_rows(lg.to(DEV), split=split).cpu().tolist()
+        assert got == want, f"split={split}: {got}"
+    assert lg.float().argmax(dim=-1).tolist() == want
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_argmax_rows_ties_nan_inf_and_lengths(split):
     """First index on ties; NaN counts above every number (torch's convention, first NaN wins); -inf rows;
     ``seq_lens`` advances by one per row; a strided logits view reads only its N columns."""
     from runtime_amd.phase2.decode_glue import argmax_rows
@@ -364,7 +388,7 @@ def test_argmax_rows_ties_nan_inf_and_lengths():
     dev = base.to(DEV)[:, :n]
     lens = torch.tensor([3, 0, 9, 1, 1, 2047], dtype=torch.int32, device=DEV)
     out = torch.full((6,), -1, dtype=torch.int64, device=DEV)
-    argmax_rows(dev, out=out, seq_lens=lens)
+    argmax_rows(dev, out=out, seq_lens=lens, split=split)
     assert out.cpu().tolist() == [17, 0, 300, 2500, n - 1, 1234]
     assert out.cpu().tolist() == lg.float().argmax(dim=-1).tolist()
     assert lens.cpu().tolist() == [4, 1, 10, 2, 2, 2048]
