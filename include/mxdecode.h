@@ -172,7 +172,8 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  *      counterpart: the reference copies prefix blocks per request
  *      (runtime/phase2/worker_server.py:1442-1449), so its rows never alias.
  * Supported: D in {64, 128}; block_size in {4, 8, 16, 32}; Hq = G * Hkv, G in 1..8.
- * The workspace holds fp32 split partials and the error word; zero it once at
+ * The workspace holds the split partials (per piece: fp32 m and l, and its
+ * output normalised by l in the element type) and the error word; zero it once at
  * allocation so the error word starts clear. Concurrent calls must not share
  * a workspace. out rows must be 16-byte aligned (o_sb, o_sh multiples of 8).
  * ------------------------------------------------------------------------- */

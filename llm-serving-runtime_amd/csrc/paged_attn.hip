@@ -37,7 +37,9 @@
 //   * keeps P tiles of K/V loads in flight and reads the piece's block ids
 //     with one vector load (a range never exceeds 64 tiles).
 // A piece that is a whole segment is written as fp16 output; otherwise its
-// fp32 partial (m, l, acc[G][D]) goes to workspace slot w + s. Pairs (w, s)
+// partial goes to workspace slot w + s: (m, l) in fp32 and its own output
+// acc / l rounded to the element type (fp16 or bf16, half the bytes of the fp32
+// accumulator; the merge weights it by l again). Pairs (w, s)
 // that overlap form a monotone staircase, so w + s is unique and at most
 // W + B*Hkv - 1 slots exist. The workers holding a segment's first and last
 // tile record themselves in seg_w, so the merge needs no prefix sums.
@@ -75,7 +77,7 @@ struct Params {
     _Float16* out;
     int64_t o_sb, o_sh;
     float* part_ml;   // [slots][G][2]  (m, l) on the exp2 scale
-    float* part_acc;  // [slots][G][D]
+    _Float16* part_out;  // [slots][G][D]: each piece's output normalised by its own l, element type
     int* seg_w;       // [B*Hkv][2]: workers holding the first and the last tile of a segment
     int* err;         // error word
     int workers;
@@ -539,13 +541,16 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
                     *reinterpret_cast<VF*>(orow + (4 * g + i) * DPL) = o;
                 }
             } else {
-                float* arow = p.part_acc + (slot * G + r) * D;
+                // The piece's own normalised output, rounded to the element type: half the
+                // bytes of the fp32 accumulator, and the merge re-weights it by l.
+                _Float16* arow = p.part_out + (slot * G + r) * D;
+                const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float4v* dst = reinterpret_cast<float4v*>(arow + (4 * g + i) * DPL);
+                    VF o;
 #pragma unroll
-                    for (int c = 0; c < DPL / 4; ++c)
-                        dst[c] = float4v{acc[4 * c][i], acc[4 * c + 1][i], acc[4 * c + 2][i], acc[4 * c + 3][i]};
+                    for (int e = 0; e < DPL; ++e) o[e] = Elt<BF16>::round(acc[e][i] * inv);
+                    *reinterpret_cast<VF*>(arow + (4 * g + i) * DPL) = o;
                 }
                 if (g == 0) {
                     p.part_ml[(slot * G + r) * 2 + 0] = m_run;
@@ -588,7 +593,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     const int np = w1 - w0 + 1;
     const float kNegInf = -__builtin_huge_valf();
     const float* mlp = p.part_ml + (((int64_t)w0 + s) * G + h) * 2;
-    const float* accp = p.part_acc + (((int64_t)w0 + s) * G + h) * D + d;
+    const _Float16* accp = p.part_out + (((int64_t)w0 + s) * G + h) * D + d;
     float mg = kNegInf, l = 0.0f;
     float4v a = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int i0 = 0; i0 < np; i0 += U) {
@@ -599,7 +604,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
             const int64_t i = i0 + u < np ? i0 + u : np - 1;
             mv[u] = mlp[i * G * 2];
             lv[u] = mlp[i * G * 2 + 1];
-            av[u] = *reinterpret_cast<const float4v*>(accp + i * G * D);
+            const half4v hv = *reinterpret_cast<const half4v*>(accp + i * G * D);
+            av[u] = float4v{Elt<BF16>::widen(hv[0]), Elt<BF16>::widen(hv[1]), Elt<BF16>::widen(hv[2]),
+                            Elt<BF16>::widen(hv[3])};
         }
         float mc = kNegInf;
 #pragma unroll
@@ -615,7 +622,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
             if (i0 + u < np) {
                 const float f = exp2f(mv[u] - mn);
                 l += f * lv[u];
-                a += f * av[u];
+                a += (f * lv[u]) * av[u];  // the piece's output, normalised by its own l
             }
         }
         mg = mn;
@@ -670,7 +677,7 @@ static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_si
     L.segw = 256;
     L.ml = L.segw + align256((size_t)B * Hkv * 2 * sizeof(int));
     L.acc = L.ml + align256(slots * G * 2 * sizeof(float));
-    L.total = L.acc + align256(slots * G * D * sizeof(float));
+    L.total = L.acc + align256(slots * G * D * sizeof(uint16_t));
     return L;
 }
 
@@ -868,7 +875,7 @@ static int launch_decode(const char* what, Params prm, const Layout& L, char* ws
     const int G = Hq / Hkv;
     prm.err = err ? err : reinterpret_cast<int*>(ws + L.err);
     prm.part_ml = reinterpret_cast<float*>(ws + L.ml);
-    prm.part_acc = reinterpret_cast<float*>(ws + L.acc);
+    prm.part_out = reinterpret_cast<_Float16*>(ws + L.acc);
     prm.seg_w = reinterpret_cast<int*>(ws + L.segw);
     prm.workers = L.workers;
     hipStream_t st = as_stream(stream);

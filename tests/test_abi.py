@@ -36,9 +36,11 @@ def test_paged_attn_workspace_layout_is_host_computable():
     small = lib.mx_paged_attn_workspace_bytes(4, 8, 2, 64, 8, 16, 0)
     big = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 256)
     assert 0 < small < big
-    # One fp32 partial (G x (D + 2)) per worker + segment slot: 65536 tiles at the table
-    # width in ranges of 16 tiles -> 4096 workers, + 256 segments.
-    assert big >= (4096 + 256) * 4 * 128 * 4
+    # One partial per worker + segment slot (fp32 m, l and a 16-bit output of D per head, G heads):
+    # 65536 tiles at the table width in ranges of 16 tiles -> 4096 workers, + 256 segments.
+    slots = 4096 + 256
+    assert big >= slots * 4 * (2 * 4 + 128 * 2)
+    assert big < slots * 4 * (2 * 4 + 128 * 4)  # half the bytes of an fp32 accumulator
     assert lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 512) < big
     # Default split: 2048 workers for config 2's table (ranges of 32 tiles = 512 tokens at full
     # width); a single short row gets ranges of 4 tiles (64 tokens).

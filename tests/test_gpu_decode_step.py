@@ -113,14 +113,21 @@ def _run(hf, batch, lo, hi, seed, graph):
         err16 = float((t16 - ref_logits).abs().max())
         allowed = max(LOGIT_ATOL, YARDSTICK_SLACK * err16)
         agree = om.greedy_agreement(ref_logits, toks[b], tie_tol=2 * allowed)
-        results.append((b, err, allowed, agree))
+        # torch fp16's own flips on the same prefixes (its argmax against the oracle's).
+        yard = int((t16.argmax(dim=-1) != ref_logits.argmax(dim=-1)).sum())
+        results.append((b, err, allowed, agree, yard))
         print(f"[step] row {b} prompt {lens[b]}: max|dL| native {err:.3e} torch16 {err16:.3e} "
-              f"mismatches {agree['mismatches']}/{agree['steps']}", flush=True)
-    for b, err, allowed, agree in results:
+              f"mismatches {agree['mismatches']}/{agree['steps']} (torch16 {yard})", flush=True)
+    for b, err, allowed, agree, _ in results:
         assert err <= allowed, f"row {b}: logits off by {err:.3e} (allowed {allowed:.3e})"
         assert agree["ties_ok"], f"row {b}: mismatch outside the near-tie band {agree}"
+    # Near-tie flips are a property of fp16 activations on random weights (the oracle's top-1
+    # margin drops below the logit error now and then); they must stay rare: at most 2 % of the
+    # steps, or as many as torch fp16 itself makes plus one (the fraction alone allows none at
+    # one row of 32 steps).
     ties = sum(r[3]["mismatches"] for r in results)
-    assert ties <= MAX_TIE_FRACTION * batch * STEPS
+    yard = sum(r[4] for r in results)
+    assert ties <= max(MAX_TIE_FRACTION * batch * STEPS, yard + 1), f"{ties} near-tie flips (torch fp16 {yard})"
 
 
 def test_native_step_qwen2_shape():
