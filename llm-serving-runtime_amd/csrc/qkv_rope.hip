@@ -28,7 +28,12 @@ using w8a16::kTileK;
 using w8a16::kTileN;
 
 constexpr int kWaves = 8;  // k ranges per workgroup (the split count of the two-launch path)
-constexpr int kDepth = 8;  // k-tiles of loads in flight per wave
+// k-tiles of loads in flight per wave: 8 covers a wave's whole range at K = 4096 (one round
+// trip); one m-tile (M <= 16) keeps 4, which leaves the registers for the epilogue's early loads.
+template <int MT>
+constexpr int depth_for() {
+    return MT == 1 ? 4 : 8;
+}
 constexpr int kMaxRows = 32;
 
 struct Params {
@@ -123,17 +128,26 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
             }
         }
     };
-    if (nj > 0) {
-        St st[kDepth];
-        PIPELINE_BODY(kDepth, nj, st, load, compute(st[s]))
-    }
-
-    // Rotation factors and pool slots of the epilogue thread's rows, loaded before the
-    // barrier so that they arrive while the workgroup waits for its slowest wave.
+    // Rotation factors, pool slots, scales and bias of the epilogue thread's rows. With one m-tile
+    // their loads are issued right after the first pipeline stages (the positions, loaded first,
+    // have arrived by then), so they overlap the main loop instead of adding a round trip after
+    // it: qkv 8.2 -> 6.5 us on the Qwen2-0.5B shape at 16 rows. With two m-tiles the early loads
+    // would hold their registers through a loop that already needs 236 of them (the kernel then
+    // took 256 and ran 12.6 -> 13.3 us at 32 rows), so they follow the loop there, still ahead
+    // of the workgroup's final barrier.
     const int c = jt * kTileN + r;  // dim of the pair's first element within the head
+    const int n0 = nt0 * kTileN + r, n1 = nt1 * kTileN + r;
     float2 cs[4];
     int64_t dst[4];
-    if (epi) {
+    float sc0 = 0.0f, sc1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+    auto epilogue_inputs = [&]() {
+        sc0 = h2f(p.scale, n0);
+        sc1 = h2f(p.scale, n1);
+        if (p.bias) {
+            b0 = h2f(p.bias, n0);
+            b1 = h2f(p.bias, n1);
+        }
+        if (!epi) return;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = (tid >> 6) * 16 + 4 * g + i;
@@ -147,12 +161,17 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
                                            p.shead, kvh, D);
             }
         }
+    };
+    constexpr bool kEarly = MT == 1;
+    if (nj > 0) {
+        constexpr int P = depth_for<MT>();
+        St st[P];
+        PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), if (kEarly) epilogue_inputs())
     }
+    if (!kEarly || nj <= 0) epilogue_inputs();
 
     // Scaled accumulators (the split partials) to LDS; acc[t][mt][i] is row
     // 16 mt + 4 g + i, column 16 nt + r of tile t.
-    const int n0 = nt0 * kTileN + r, n1 = nt1 * kTileN + r;
-    const float sc0 = h2f(p.scale, n0), sc1 = h2f(p.scale, n1);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         float4v v0, v1;
@@ -169,7 +188,6 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
 
     const int mt = tid >> 6;
     float s0[4], s1[4];
-    const float b0 = p.bias ? h2f(p.bias, n0) : 0.0f, b1 = p.bias ? h2f(p.bias, n1) : 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         s0[i] = b0;

@@ -80,8 +80,13 @@ __device__ __forceinline__ float h2f(const uint16_t* p, int64_t i) {
 // clamped when nj < P). Full rounds issue the loads of tile j+P right after
 // tile j is consumed, unconditionally. The last round and a half issue only
 // the loads still in range, then drain.
-#define PIPELINE_BODY(P, nj, st, load, COMPUTE)                  \
+#define PIPELINE_BODY(P, nj, st, load, COMPUTE) PIPELINE_BODY_HOOK(P, nj, st, load, COMPUTE, (void)0)
+
+// HOOK runs once, after the first P stages' loads are issued and before the first compute:
+// loads it issues overlap the pipeline's first round trip.
+#define PIPELINE_BODY_HOOK(P, nj, st, load, COMPUTE, HOOK)         \
     _Pragma("unroll") for (int s = 0; s < P; ++s) load(s, st[s]); \
+    HOOK;                                                           \
     int j0 = 0;                                                     \
     for (; j0 + 2 * P <= nj; j0 += P) {                             \
         _Pragma("unroll") for (int s = 0; s < P; ++s) {             \
