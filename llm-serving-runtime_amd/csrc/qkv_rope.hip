@@ -28,12 +28,8 @@ using w8a16::kTileK;
 using w8a16::kTileN;
 
 constexpr int kWaves = 8;  // k ranges per workgroup (the split count of the two-launch path)
-// k-tiles of loads in flight per wave: 8 covers a wave's whole range at K = 4096 (one round
-// trip); one m-tile (M <= 16) keeps 4, which leaves the registers for the epilogue's early loads.
-template <int MT>
-constexpr int depth_for() {
-    return MT == 1 ? 4 : 8;
-}
+constexpr int kDepth = 8;       // k-tiles of loads in flight per wave: a whole range at K = 4096
+constexpr int kShortDepth = 4;  // ranges of at most this many k-tiles (K <= 2048) with one m-tile
 constexpr int kMaxRows = 32;
 
 struct Params {
@@ -129,12 +125,13 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
         }
     };
     // Rotation factors, pool slots, scales and bias of the epilogue thread's rows. With one m-tile
-    // their loads are issued right after the first pipeline stages (the positions, loaded first,
-    // have arrived by then), so they overlap the main loop instead of adding a round trip after
-    // it: qkv 8.2 -> 6.5 us on the Qwen2-0.5B shape at 16 rows. With two m-tiles the early loads
-    // would hold their registers through a loop that already needs 236 of them (the kernel then
-    // took 256 and ran 12.6 -> 13.3 us at 32 rows), so they follow the loop there, still ahead
-    // of the workgroup's final barrier.
+    // and a short k range (at most kShortDepth k-tiles, all in flight at once) their loads are
+    // issued right after the pipeline's loads (the positions, loaded first, have arrived by
+    // then), so they overlap the main loop instead of adding a round trip after it: qkv
+    // 8.2 -> 6.5 us on the Qwen2-0.5B shape at 16 rows. Otherwise they follow the loop, still
+    // ahead of the workgroup's final barrier: held through the 8-deep loop the early values cost
+    // registers (two m-tiles: 236 -> 256 VGPRs, 12.6 -> 13.3 us at 32 rows; one m-tile at
+    // K = 4096 with a 4-deep loop instead: 9.3-10.1 -> 10.4 us at 16 rows).
     const int c = jt * kTileN + r;  // dim of the pair's first element within the head
     const int n0 = nt0 * kTileN + r, n1 = nt1 * kTileN + r;
     float2 cs[4];
@@ -162,13 +159,16 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
             }
         }
     };
-    constexpr bool kEarly = MT == 1;
-    if (nj > 0) {
-        constexpr int P = depth_for<MT>();
-        St st[P];
-        PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), if (kEarly) epilogue_inputs())
+    if (MT == 1 && nj > 0 && nj <= kShortDepth) {
+        St st[kShortDepth];
+        PIPELINE_BODY_HOOK(kShortDepth, nj, st, load, compute(st[s]), epilogue_inputs())
+    } else {
+        if (nj > 0) {
+            St st[kDepth];
+            PIPELINE_BODY(kDepth, nj, st, load, compute(st[s]))
+        }
+        epilogue_inputs();
     }
-    if (!kEarly || nj <= 0) epilogue_inputs();
 
     // Scaled accumulators (the split partials) to LDS; acc[t][mt][i] is row
     // 16 mt + 4 g + i, column 16 nt + r of tile t.
