@@ -472,8 +472,9 @@ static int splits_for(int NT, int KT) {
     return ks;
 }
 
-// Chunks of more than 64 rows (6 or 8 m-tiles): 8-wave workgroups of 2 waves along M
-// (each 3 or 4 m-tiles, all of the chunk's rows staged once in LDS) by 4 along N, each
+// Chunks of more than 64 rows (6 or 8 m-tiles), and of 49-64 rows where use_m_split says so:
+// 8-wave workgroups of 2 waves along M (each 2, 3 or 4 m-tiles, all of the chunk's rows
+// staged once in LDS) by 4 along N, each
 // wave holding 2 n-tiles, so every x fragment read from LDS feeds two MFMAs. The two
 // m-halves read the same weight tiles (the second read is an L2 hit). With one 4-wave
 // workgroup of 8 m-tiles x 1 n-tile (254 VGPRs + 48 AGPRs, one wave per SIMD) the
@@ -490,11 +491,23 @@ static int big_splits(int NT, int KT) {
     return ks;
 }
 
+// Where the M-split shape takes a chunk: above 64 rows always (when NT is even), and at 49-64
+// rows (4 m-tiles, two per wave) when its k ranges are long enough to fill its 4-deep pipeline
+// several times. Measured on the Llama-3-8B shapes at M = 64 (MI355X): qkv 23.3 -> 16.5 us,
+// gate_up 36.9 -> 32.7, down 24.9 -> 23.0-24.0 (k ranges of 32, 64 and 28 tiles); o, whose
+// 8-tile k ranges would take two pipeline rounds, measured 14.0 -> 16.2 and keeps the 4-wave
+// shape.
+constexpr int kMwMinRangeTiles = 16;
+static bool use_m_split(int MT, int NT, int KT) {
+    if (!big_m_shape(NT)) return false;
+    return MT >= 6 || (MT == 4 && KT / big_splits(NT, KT) >= kMwMinRangeTiles);
+}
+
 static Plan plan_for(int M, int NT, int KT) {
     Plan pl{};
     pl.KS = 1;
     pl.KW = 1;
-    if (mt_for(M) >= 6 && big_m_shape(NT)) {
+    if (mt_for(M) >= 4 && use_m_split(mt_for(M), NT, KT)) {
         pl.valu = false;
         pl.MT = mt_for(M);
         pl.KS = big_splits(NT, KT);
@@ -583,8 +596,8 @@ static void launch_shape(const uint16_t* x, int64_t xs, int M, const uint8_t* w,
 template <int MT, bool SW, bool GU = false>
 static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, int KS, int KW, float* partial, hipStream_t st) {
-    if constexpr (MT >= 6 && !SW) {
-        if (big_m_shape(NT)) {
+    if constexpr (MT >= 4 && !SW) {
+        if (use_m_split(MT, NT, KT)) {
             launch_shape<MT / 2, kBigNpw, kBigWaves, SW, GU, 1, 2>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);
             return;
         }
