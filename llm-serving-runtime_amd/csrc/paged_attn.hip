@@ -81,9 +81,11 @@ struct Params {
     int* seg_w;       // [B*Hkv][2]: workers holding the first and the last tile of a segment
     int* err;         // error word
     int workers;
+    int wg_waves;     // waves per workgroup of the split launch (<= kWaves)
 };
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;               // waves per workgroup of the split launch (at most)
+constexpr int kSmallWorkers = 1024;     // up to this many workers the split launch uses 2-wave workgroups
 constexpr int kTile = 16;               // tokens per MFMA tile
 constexpr int kMaxRangeTiles = 64;      // a worker's range fits one vector of block ids (block size >= 16)
 // Tiles whose block ids fit one vector: block sizes 4 and 8 put 4 or 2 blocks in a tile.
@@ -468,7 +470,7 @@ __global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_ker
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int worker = blockIdx.x * kWaves + wave;
+    const int worker = blockIdx.x * p.wg_waves + wave;
     const int g = lane >> 4, r = lane & 15;
 
     // Up to 64 rows: one read of seq_lens per wave, reused to locate every piece.
@@ -705,8 +707,14 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     // one round unless ranges would then exceed max_range_tiles.
     const int cap = resident_waves<D, BS, G, STREAM, BF16>();
     if (cap > 0 && prm.workers > cap) prm.workers = (int)(floor_workers > cap ? floor_workers : cap);
-    const int blocks = (int)ceil_div(prm.workers, kWaves);
-    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16>), dim3(blocks), dim3(kWaves * 64), 0, st, prm);
+    // Up to kSmallWorkers workers, 2-wave workgroups spread the waves over twice as many CUs (one
+    // CU streams at most ~55 GB/s of this gather): Qwen2-0.5B shape, 512 workers, 13.8-14.2 ->
+    // 13.4-13.5 us per call on MI355X. With 2048 workers, 4-wave workgroups measured 56.0 us against
+    // 56.3 (2 waves) and 57.3 (1 wave).
+    prm.wg_waves = prm.workers <= kSmallWorkers ? 2 : kWaves;
+    const int blocks = (int)ceil_div(prm.workers, prm.wg_waves);
+    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16>), dim3(blocks), dim3(prm.wg_waves * 64), 0, st,
+                       prm);
     hipLaunchKernelGGL((decode_merge_kernel<D, BS, G, BF16>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0, st,
                        prm);
 }
@@ -1003,6 +1011,7 @@ extern "C" int mx_kv_gather_probe(const uint16_t* k, const uint16_t* v, int64_t 
     if (mode == 0) {
         // The decode kernel's default partition: one round of 2048 waves (or the range floor).
         prm.workers = pa::resolve_workers(0, B, Hkv, max_blocks, block_size);
+        prm.wg_waves = pa::kWaves;
         const int blocks = (int)ceil_div(prm.workers, pa::kWaves);
         if (D == 128)
             hipLaunchKernelGGL((pa::decode_split_kernel<128, 16, 1, true, false, true>), dim3(blocks),
