@@ -26,6 +26,11 @@ ARCH = os.environ.get("MX_OFFLOAD_ARCH", "gfx950")
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in generated code.
 # -fhip-fp32-correctly-rounded-divide-sqrt: IEEE fp32 division for the
 # bit-exact quantizer. No fast-math anywhere.
+# -amdgpu-kernarg-preload-count: the first 16 dwords of scalar kernel arguments arrive in
+# SGPRs with the dispatch (gfx950), so a kernel starts without the kernarg load round trip;
+# the compiler keeps a prologue that loads them for firmware that does not preload.
+# Measured on MI355X: o projection 8.42 -> 8.15 us in the batch-32 step, Qwen2-0.5B step
+# 1.097-1.107 -> 1.088 ms.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -33,6 +38,7 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
     f"-I{INCLUDE}",
