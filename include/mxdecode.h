@@ -171,7 +171,9 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  *      same blocks in L2 / MALL. Results are the same either way. No reference
  *      counterpart: the reference copies prefix blocks per request
  *      (runtime/phase2/worker_server.py:1442-1449), so its rows never alias.
- * Supported: D in {64, 128}; block_size in {4, 8, 16, 32}; Hq = G * Hkv, G in 1..8.
+ * Supported: D in {64, 128}; block_size in {4, 8, 16, 32}; Hq = G * Hkv, any G >= 1
+ * (G > 8 runs as vg virtual kv-heads of G / vg <= 8 query heads each, vg the smallest
+ * such divisor of G; each reads its pool head's K/V, so K/V bytes are read vg times).
  * The workspace holds the split partials (per piece: fp32 m and l, and its
  * output normalised by l in the element type) and the error word; zero it once at
  * allocation so the error word starts clear. Concurrent calls must not share

@@ -82,6 +82,7 @@ struct Params {
     int* err;         // error word
     int workers;
     int wg_waves;     // waves per workgroup of the split launch (<= kWaves)
+    int vg;           // virtual kv-heads per pool head (GQA groups above 8, see kv_virtual_groups)
 };
 
 constexpr int kWaves = 4;               // waves per workgroup of the split launch (at most)
@@ -332,8 +333,8 @@ __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t
 #pragma unroll
     for (int e = 0; e < DPL; ++e) acc[e] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const _Float16* kbase = p.k + (int64_t)kvh * p.kv_shead;
-    const _Float16* vbase = p.v + (int64_t)kvh * p.kv_shead;
+    const _Float16* kbase = p.k + (int64_t)(kvh / p.vg) * p.kv_shead;
+    const _Float16* vbase = p.v + (int64_t)(kvh / p.vg) * p.kv_shead;
 
     // Loads are unconditional: past the piece's last tile the index is clamped
     // (an L2 hit) and a skipped block reads block 0; only the compute below is
@@ -637,6 +638,18 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     }
 }
 
+// GQA groups above 8 (the kernels' largest G) are served as virtual kv-heads: pool head k
+// becomes heads k * vg .. k * vg + vg - 1 of G / vg query heads each (query head order is
+// unchanged), with vg the smallest divisor of G that brings the group to 8 or fewer. Each
+// virtual head reads its pool head's K/V, so K/V bytes are read vg times (the reference's
+// kernels read them G times, paged_attention_triton.py:179-181).
+static inline int kv_virtual_groups(int Hq, int Hkv) {
+    const int G = Hkv > 0 ? Hq / Hkv : 1;
+    for (int vg = 1; vg <= G; ++vg)
+        if (G % vg == 0 && G / vg <= 8) return vg;
+    return G;
+}
+
 struct Layout {
     size_t err, segw, ml, acc, total;
     int workers;
@@ -670,6 +683,7 @@ static int resolve_workers(int chunk_tokens, int B, int Hkv, int max_blocks, int
     return (int)(w > (1 << 30) ? (1 << 30) : w);
 }
 
+// Hkv: kv-heads as the kernels see them (after kv_virtual_groups).
 static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_size, int chunk_tokens) {
     Layout L{};
     L.workers = resolve_workers(chunk_tokens, B, Hkv, max_blocks, block_size);
@@ -818,12 +832,13 @@ using namespace mx;
 extern "C" size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                                 int32_t block_size, int32_t chunk_tokens) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_blocks < 0 || block_size <= 0) return 0;
-    return pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens).total;
+    return pa::layout(B, Hq, Hkv * pa::kv_virtual_groups(Hq, Hkv), D, max_blocks, block_size, chunk_tokens).total;
 }
 
 extern "C" size_t mx_paged_attn_error_offset(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                              int32_t block_size, int32_t chunk_tokens) {
-    return pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens).err;
+    if (Hkv <= 0) return 0;
+    return pa::layout(B, Hq, Hkv * pa::kv_virtual_groups(Hq, Hkv), D, max_blocks, block_size, chunk_tokens).err;
 }
 
 namespace mx {
@@ -839,18 +854,17 @@ static int check_args(const char* what, const uint16_t* q, int64_t q_sb, int64_t
     if (!q || !k || !v || !block_tables || !seq_lens || !out) return fail(MX_ERR_NULL, "%s: null pointer", what);
     if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
         return fail(MX_ERR_INVALID, "%s: Hq (%d) must be a positive multiple of Hkv (%d)", what, Hq, Hkv);
-    const int G = Hq / Hkv;
-    if (G > 8) return fail(MX_ERR_UNSUPPORTED, "%s: GQA group %d > 8 unsupported", what, G);
     if (D != 64 && D != 128) return fail(MX_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", what, D);
     if (block_size != 4 && block_size != 8 && block_size != 16 && block_size != 32)
         return fail(MX_ERR_UNSUPPORTED, "%s: block_size %d unsupported (4, 8, 16 or 32)", what, block_size);
     if (max_blocks < 1 || num_pool_blocks < 1)
         return fail(MX_ERR_INVALID, "%s: max_blocks and num_pool_blocks must be >= 1", what);
-    if (B > 65535 || Hkv > 65535) return fail(MX_ERR_UNSUPPORTED, "%s: B or Hkv too large", what);
+    const int vg = kv_virtual_groups(Hq, Hkv);
+    if (B > 65535 || (int64_t)Hkv * vg > 65535) return fail(MX_ERR_UNSUPPORTED, "%s: B or Hq too large", what);
     if (flags & ~(uint32_t)(MX_PA_SHARED_BLOCKS | MX_PA_BF16)) return fail(MX_ERR_INVALID, "%s: unknown flags 0x%x", what, flags);
     if (chunk_tokens < 0 || chunk_tokens % kTile != 0 || chunk_tokens > kMaxChunkTokens)
         return fail(MX_ERR_INVALID, "%s: chunk_tokens must be 0 or a multiple of 16 <= %d", what, kMaxChunkTokens);
-    if ((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, kTile) > ((int64_t)1 << 31))
+    if ((int64_t)B * Hkv * vg * ceil_div((int64_t)max_blocks * block_size, kTile) > ((int64_t)1 << 31))
         return fail(MX_ERR_UNSUPPORTED, "%s: more than 2^31 tiles", what);
     if (!aligned(q, 16) || q_sb % 8 || q_sh % 8 || !aligned(k, 16) || !aligned(v, 16) || kv_sblk % 8 ||
         kv_shead % 8 || !aligned(out, 16) || o_sb % 8 || o_sh % 8)
@@ -868,7 +882,8 @@ static int check_args(const char* what, const uint16_t* q, int64_t q_sb, int64_t
     prm.max_blocks = max_blocks;
     prm.seq_lens = seq_lens;
     prm.B = B;
-    prm.Hkv = Hkv;
+    prm.Hkv = Hkv * vg;  // kv-heads as the kernels see them
+    prm.vg = vg;
     prm.num_pool_blocks = num_pool_blocks;
     prm.scale_log2e = scale * 1.4426950408889634f;
     prm.out = reinterpret_cast<_Float16*>(out);
@@ -946,11 +961,11 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     int rc = pa::check_args(what, q, q_sb, q_sh, k, v, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, seq_lens, B,
                             Hq, Hkv, D, block_size, num_pool_blocks, scale, out, o_sb, o_sh, chunk_tokens, flags, prm);
     if (rc != MX_OK) return rc;
-    const pa::Layout L = pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens);
+    const pa::Layout L = pa::layout(B, Hq, prm.Hkv, D, max_blocks, block_size, chunk_tokens);
     if (!workspace || workspace_bytes < L.total)
         return fail(MX_ERR_WORKSPACE, "%s: workspace needs %zu bytes, got %zu", what, L.total, workspace_bytes);
     if (!aligned(workspace, 256)) return fail(MX_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", what);
-    return pa::launch_decode(what, prm, L, static_cast<char*>(workspace), nullptr, B, Hq, Hkv, D, max_blocks,
+    return pa::launch_decode(what, prm, L, static_cast<char*>(workspace), nullptr, B, Hq, prm.Hkv, D, max_blocks,
                              block_size, flags, stream);
 }
 
@@ -969,7 +984,7 @@ extern "C" int mx_paged_attn_decode_noalloc(const uint16_t* q, int64_t q_sb, int
                             Hq, Hkv, D, block_size, num_pool_blocks, scale, out, o_sb, o_sh, chunk_tokens, flags, prm);
     if (rc != MX_OK) return rc;
     if (err && !aligned(err, 4)) return fail(MX_ERR_ALIGNMENT, "%s: err must be 4-byte aligned", what);
-    const pa::Layout L = pa::layout(B, Hq, Hkv, D, max_blocks, block_size, chunk_tokens);
+    const pa::Layout L = pa::layout(B, Hq, prm.Hkv, D, max_blocks, block_size, chunk_tokens);
     if (L.total > (size_t)MX_PA_NOALLOC_SCRATCH_BYTES)
         return fail(MX_ERR_WORKSPACE, "%s: this shape needs %zu bytes of scratch, more than the %zu the library holds "
                                       "per GPU; use mx_paged_attn_decode with a workspace",
@@ -977,7 +992,7 @@ extern "C" int mx_paged_attn_decode_noalloc(const uint16_t* q, int64_t q_sb, int
     char* ws = nullptr;
     rc = pa::scratch_of_current_device(&ws);
     if (rc != MX_OK) return rc;
-    return pa::launch_decode(what, prm, L, ws, err, B, Hq, Hkv, D, max_blocks, block_size, flags, stream);
+    return pa::launch_decode(what, prm, L, ws, err, B, Hq, prm.Hkv, D, max_blocks, block_size, flags, stream);
 }
 
 extern "C" int mx_kv_gather_probe(const uint16_t* k, const uint16_t* v, int64_t kv_sblk, int64_t kv_shead,
@@ -1005,6 +1020,7 @@ extern "C" int mx_kv_gather_probe(const uint16_t* k, const uint16_t* v, int64_t 
     prm.seq_lens = seq_lens;
     prm.B = B;
     prm.Hkv = Hkv;
+    prm.vg = 1;
     prm.num_pool_blocks = num_pool_blocks;
     prm.err = sink;
     hipStream_t st = as_stream(stream);

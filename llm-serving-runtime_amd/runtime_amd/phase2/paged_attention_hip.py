@@ -12,7 +12,8 @@ Differences from the reference that a caller can observe:
 * device tensors only: a CPU query raises ``ValueError`` instead of running a
   torch fallback (``:761-775``);
 * fp16 or bf16 queries and pools (one dtype), ``head_dim`` in {64, 128}, ``block_size``
-  in {4, 8, 16, 32}, GQA group 1..8 (``ValueError`` otherwise);
+  in {4, 8, 16, 32} (``ValueError`` otherwise); any GQA group (above 8 the kernel splits a
+  kv-head's query heads into groups of at most 8 and reads its K/V once per group);
 * ``seq_len == 0`` rows produce zeros (the reference divides by zero,
   ``:238``); ``paged_attention_decode`` still rejects ``seq_len <= 0`` (``:789-790``);
 * the returned tensor is freshly allocated, never an alias of a cached buffer

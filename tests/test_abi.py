@@ -99,7 +99,11 @@ def test_invalid_arguments_return_status_codes():
     assert call(B=0) == _hip.MX_OK
     _status(call(q=None), _hip.MX_ERR_NULL)
     _status(call(Hq=7), _hip.MX_ERR_INVALID)
-    _status(call(Hq=36, Hkv=2), _hip.MX_ERR_UNSUPPORTED)  # G = 18
+    # G = 18 passes validation (3 virtual kv-heads of 6 query heads per pool head) and stops at the
+    # missing workspace, which is sized like the 6-kv-head layout.
+    _status(call(Hq=36, Hkv=2), _hip.MX_ERR_WORKSPACE)
+    assert lib.mx_paged_attn_workspace_bytes(4, 36, 2, 64, 8, 16, 0) == lib.mx_paged_attn_workspace_bytes(4, 36, 6, 64, 8, 16, 0)
+    assert lib.mx_paged_attn_workspace_bytes(4, 22, 2, 64, 8, 16, 0) == lib.mx_paged_attn_workspace_bytes(4, 22, 22, 64, 8, 16, 0)
     _status(call(D=96), _hip.MX_ERR_UNSUPPORTED)
     _status(call(bs=12), _hip.MX_ERR_UNSUPPORTED)
     _status(call(ct=40), _hip.MX_ERR_INVALID)

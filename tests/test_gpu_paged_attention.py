@@ -280,6 +280,22 @@ def test_gqa_dims_and_block_sizes(hkv, grp, d, bs):
     _check(_decode(q, k, v, tables, sl, scale, grp), oracle_out(q, k, v, tables, sl, scale, grp))
 
 
+@pytest.mark.parametrize("hkv,grp,d,bs,bf16", [(2, 12, 128, 16, False), (1, 16, 64, 16, False), (2, 11, 64, 16, False),
+                                                (1, 24, 128, 32, True), (4, 9, 64, 8, False), (1, 14, 64, 16, True)])
+def test_gqa_groups_above_eight(hkv, grp, d, bs, bf16):
+    # Groups above 8 run as virtual kv-heads (12 -> 2 x 6, 16 -> 2 x 8, 11 -> 11 x 1, 24 -> 3 x 8, 9 -> 3 x 3,
+    # 14 -> 2 x 7); the result is still the oracle's over the pool head's K/V.
+    lens = [1, 17, 300, 1000, 64]
+    q, k, v, tables, sl = _random_case(41 + grp + d + bs, len(lens), hkv, grp, d, bs, lens)
+    if bf16:
+        q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    scale = d**-0.5
+    got = _decode(q, k, v, tables, sl, scale, grp).float()
+    want = oracle_out(q.float(), k.float(), v.float(), tables, sl, scale, grp)
+    tol = 2e-2 if bf16 else 1e-2
+    torch.testing.assert_close(got.cpu(), want.float().cpu().view_as(got), atol=tol, rtol=tol)
+
+
 def test_zero_length_rows_and_table_clamp():
     lens = [0, 40, 0, 100]
     q, k, v, tables, sl = _random_case(21, 4, 2, 4, 64, 16, lens)
