@@ -230,7 +230,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 #ifndef MX_GEMM_MIN_WAVES
 #define MX_GEMM_MIN_WAVES 3
 #endif
-template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false, int KW = 1, int MW = 1>
+// NJX > 0: the k part's whole x range (at most NJX k-tiles) is staged in LDS once, its loads issued
+// before the pipeline's weight loads and stored after them, with one barrier; the main loop then
+// reads fragments at the k-tile's column offset and meets no barrier. Results are identical to the
+// per-k-tile staging. Measured on MI355X: a barrier per k-tile cost the Qwen2-0.5B step (k ranges
+// of 5-14 tiles) about 9 % of its time.
+template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false, int KW = 1, int MW = 1, int NJX = 0>
 __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 && MW == 1) ? MX_GEMM_MIN_WAVES : 1) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
                                                                const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scale,
@@ -244,7 +249,10 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     static_assert(WN * KW * MW == WAVES && (KW == 1 || !GU), "k parts split only partial launches");
     constexpr int XCH = ROWS * 8;   // 16-byte chunks of one x k-tile
     constexpr int XC = (XCH + WP * 64 - 1) / (WP * 64);
-    __shared__ __attribute__((aligned(16))) _Float16 xl[KW][2][ROWS * RS];
+    static_assert(NJX == 0 || (!SW && MW == 1), "whole-range x staging: plain x, one m group");
+    constexpr int RSX = NJX * kTileK + 8;  // row stride (halfs) of a whole-range buffer: rows 4 banks apart
+    constexpr int XF = NJX > 0 ? (ROWS * NJX * 8 + WP * 64 - 1) / (WP * 64) : 1;  // chunks per thread
+    __shared__ __attribute__((aligned(16))) _Float16 xl[KW][NJX > 0 ? 1 : 2][NJX > 0 ? ROWS * RSX : ROWS * RS];
 
     const int ks = blockIdx.y, KS = gridDim.y;
     const int tid = threadIdx.x;
@@ -285,12 +293,36 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
         const int kt = kt_lo + (j < nj ? j : nj - 1);
 #pragma unroll
         for (int p = 0; p < NPW; ++p) st.w[p] = load_wtile<MW == 1>(wbase + ((int64_t)kt * NT + p) * 64 + lane);
+        if constexpr (NJX == 0) {
 #pragma unroll
-        for (int u = 0; u < XC; ++u) {
-            st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
-            if (SW) st.up[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + up_off + kt * kTileK);
+            for (int u = 0; u < XC; ++u) {
+                st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
+                if (SW) st.up[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + up_off + kt * kTileK);
+            }
         }
     };
+    // NJX: chunk c = ltid + u * WP * 64 of the part's ROWS x (nj * 64) range (rows past M read row
+    // M - 1; chunks past the range load chunk 0 and are stored to row 0's padding, which no fragment
+    // read touches). Stores are unconditional and a scheduling barrier keeps these loads ahead of
+    // the pipeline's weight loads: waiting for them then never waits for the weights (loads
+    // complete in order). Sunk into conditional stores, they made the compiler drain every weight
+    // load before the first MFMA.
+    uint4 xf[XF];
+    int xfo[XF];
+    if constexpr (NJX > 0) {
+        const int cpr = nj * 8;  // chunks per row
+#pragma unroll
+        for (int u = 0; u < XF; ++u) {
+            const int c = ltid + u * WP * 64;
+            const bool in = c < ROWS * cpr;
+            const int cc = in ? c : 0;
+            const int row = cc / cpr, col = (cc - row * cpr) * 8;
+            const int rc = row < M ? row : M - 1;
+            xf[u] = *reinterpret_cast<const uint4*>(xbase + (int64_t)rc * xs + (int64_t)kt_lo * kTileK + col);
+            xfo[u] = in ? row * RSX + col : NJX * kTileK;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     float4v acc[NPW][MT];
 #pragma unroll
@@ -302,7 +334,11 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     // it was read; every wave finished that read before the barrier in between.
     int step = 0;
     auto compute = [&](const St& st) {
+        const _Float16* frag = &xl[kw][0][0] + step * kTileK;  // NJX: this k-tile's columns
+        constexpr int FRS = NJX > 0 ? RSX : RS;
+        if constexpr (NJX == 0) {
         _Float16* buf = xl[kw][step & 1];
+        frag = buf;
 #pragma unroll
         for (int u = 0; u < XC; ++u) {
             if (SW) {
@@ -320,10 +356,11 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
             }
         }
         __syncthreads();
+        }
         half8v a[MT][2];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const _Float16* src = buf + ((mw * MT + mt) * 16 + r) * RS + 16 * g;
+            const _Float16* src = frag + ((mw * MT + mt) * 16 + r) * FRS + 16 * g;
             a[mt][0] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(src));
             a[mt][1] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(src + 8));
         }
@@ -357,12 +394,22 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
             bi_pre[p] = (gridDim.y == 1 && bias) ? h2f(bias, n) : 0.0f;
         }
     };
+    // NJX: the whole-range x reaches LDS after the pipeline's first weight loads are issued. The
+    // stores are written inline (not in a lambda): captured by reference, xf went to scratch memory.
+#define MX_NJX_HOOK                                                                       \
+    load_epilogue();                                                                      \
+    if constexpr (NJX > 0) {                                                              \
+        _Pragma("unroll") for (int u = 0; u < XF; ++u)                                    \
+            *reinterpret_cast<uint4*>(&xl[kw][0][0] + xfo[u]) = xf[u];                    \
+        __syncthreads();                                                                  \
+    }
     if (nj > 0) {
         St st[P];
-        PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), load_epilogue())
+        PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), MX_NJX_HOOK)
     } else {
         load_epilogue();
     }
+#undef MX_NJX_HOOK
     const int N = NT * kTileN;
     if (GU) {
         // Every lane takes part in the swap; out-of-range waves just do not store.
@@ -601,14 +648,14 @@ static WideShape wide_shape(int NT, bool npw1_only) {
     return WideShape{kMfmaWaves, 1};
 }
 
-template <int MT, int NPW, int WAVES, bool SW, bool GU, int KW = 1, int MW = 1>
+template <int MT, int NPW, int WAVES, bool SW, bool GU, int KW = 1, int MW = 1, int NJX = 0>
 static void launch_shape(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                          uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
     // Pipeline depth: 6 for the M-split shape spilled (24 VGPRs at 4 m-tiles); 4 fits.
     constexpr int P = MW > 1 ? 4 : (NPW == 1 ? mfma_depth(MT) : (NPW == 2 ? 6 : 4));
     const int groups = ceil_div(NT, (WAVES / (KW * MW)) * NPW);
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, WAVES, P, SW, GU, KW, MW>), dim3(groups, KS), dim3(WAVES * 64), 0, st,
-                       x, xs, M, w, s, b, y, ys, KT, NT, partial);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, WAVES, P, SW, GU, KW, MW, NJX>), dim3(groups, KS), dim3(WAVES * 64), 0,
+                       st, x, xs, M, w, s, b, y, ys, KT, NT, partial);
 }
 
 // The MFMA kernel alone: KS == 1 writes fp16 y, KS > 1 writes the scaled fp32
@@ -622,8 +669,22 @@ static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, 
             return;
         }
     }
+    // Whole-range x staging (NJX) where a k part's range is at most 16 k-tiles and M <= 32.
+    const int range = (int)ceil_div(KT, (int64_t)KS * KW);
     if constexpr (MT <= 4 && !GU && kKParts > 1) {
         if (KS > 1 && KW == kKParts) {
+            if constexpr (MT <= 2 && !SW) {
+                if (range <= 8) {
+                    launch_shape<MT, 1, kMfmaWaves * kKParts, SW, GU, kKParts, 1, 8>(x, xs, M, w, s, b, y, ys, NT, KT, KS,
+                                                                                       partial, st);
+                    return;
+                }
+                if (range <= 16) {
+                    launch_shape<MT, 1, kMfmaWaves * kKParts, SW, GU, kKParts, 1, 16>(x, xs, M, w, s, b, y, ys, NT, KT,
+                                                                                        KS, partial, st);
+                    return;
+                }
+            }
             launch_shape<MT, 1, kMfmaWaves * kKParts, SW, GU, kKParts>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);
             return;
         }
@@ -645,6 +706,16 @@ static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, 
                 MX_WIDE(8, 4)
             }
 #undef MX_WIDE
+        }
+    }
+    if constexpr (MT <= 2 && !SW) {
+        if (range <= 8) {
+            launch_shape<MT, 1, kMfmaWaves, SW, GU, 1, 1, 8>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);
+            return;
+        }
+        if (range <= 16) {
+            launch_shape<MT, 1, kMfmaWaves, SW, GU, 1, 1, 16>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);
+            return;
         }
     }
     launch_shape<MT, 1, kMfmaWaves, SW, GU>(x, xs, M, w, s, b, y, ys, NT, KT, KS, partial, st);
