@@ -321,7 +321,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
             xf[u] = *reinterpret_cast<const uint4*>(xbase + (int64_t)rc * xs + (int64_t)kt_lo * kTileK + col);
             xfo[u] = in ? row * RSX + col : NJX * kTileK;
         }
-        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");  // no load moves across: x first, then the weights
     }
 
     float4v acc[NPW][MT];
@@ -383,15 +383,24 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     // instances and the wide ones (several n-tiles and m-tiles per wave) keep the loads in the
     // epilogue: the extra registers made them spill (the SwiGLU ones at 32 rows under their
     // occupancy bound), and their main loops are long.
-    constexpr bool kEarly = !GU && (NPW == 1 || MT == 1);
+    // NJX instances load them raw with the weights and convert them after the MFMAs, behind a
+    // scheduling barrier: converted where they were loaded, the scheduler placed the conversion
+    // (and so a wait for the loads) at the kernel's start.
+    constexpr bool kEarly = NJX > 0 || (!GU && (NPW == 1 || MT == 1));
     float sc_pre[NPW], bi_pre[NPW];
+    uint16_t sc_raw[NPW], bi_raw[NPW];
     auto load_epilogue = [&]() {
         if constexpr (!kEarly) return;
 #pragma unroll
         for (int p = 0; p < NPW; ++p) {
             const int64_t n = (int64_t)(nt_c + p) * kTileN + r;
-            sc_pre[p] = h2f(scale, n);
-            bi_pre[p] = (gridDim.y == 1 && bias) ? h2f(bias, n) : 0.0f;
+            if constexpr (NJX > 0) {  // unconditional loads (no bias: read the scale, use 0)
+                sc_raw[p] = scale[n];
+                bi_raw[p] = ((gridDim.y == 1 && bias) ? bias : scale)[n];
+            } else {
+                sc_pre[p] = h2f(scale, n);
+                bi_pre[p] = (gridDim.y == 1 && bias) ? h2f(bias, n) : 0.0f;
+            }
         }
     };
     // NJX: the whole-range x reaches LDS after the pipeline's first weight loads are issued. The
@@ -404,8 +413,29 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
         __syncthreads();                                                                  \
     }
     if (nj > 0) {
-        St st[P];
-        PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), MX_NJX_HOOK)
+        if constexpr (NJX > 0) {
+            // Every k-tile of the range in flight at once (nj <= NJX) and the compute unrolled: no
+            // loop-carried stages, whose register copies at the loop entry made the first MFMA wait
+            // for every load of the pipeline's first round.
+            St st[NJX];
+#pragma unroll
+            for (int j = 0; j < NJX; ++j)
+                if (j < nj) load(j, st[j]);
+            MX_NJX_HOOK
+#pragma unroll
+            for (int j = 0; j < NJX; ++j)
+                if (j < nj) compute(st[j]);
+            __builtin_amdgcn_sched_barrier(0);
+            const bool with_bias = gridDim.y == 1 && bias;
+#pragma unroll
+            for (int p = 0; p < NPW; ++p) {
+                sc_pre[p] = (float)__builtin_bit_cast(_Float16, sc_raw[p]);
+                bi_pre[p] = with_bias ? (float)__builtin_bit_cast(_Float16, bi_raw[p]) : 0.0f;
+            }
+        } else {
+            St st[P];
+            PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), MX_NJX_HOOK)
+        }
     } else {
         load_epilogue();
     }
@@ -417,8 +447,8 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
         for (int p = 0; p < NPW; ++p) {
             const int c = (nt_c + p) * (kTileN / 2) + (r & 7);  // SwiGLU channel of this lane pair
             const int64_t n = (int64_t)(nt_c + p) * kTileN + r;
-            const float sc = h2f(scale, n);
-            const float bi = bias ? h2f(bias, n) : 0.0f;
+            const float sc = kEarly ? sc_pre[p] : h2f(scale, n);
+            const float bi = kEarly ? bi_pre[p] : (bias ? h2f(bias, n) : 0.0f);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
