@@ -443,6 +443,23 @@ __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t
         if (sum == 0x9e3779b9u) p.err[1] = (int)sum;  // keeps the loads; practically never taken
         return;
     }
+    // Short pieces at D = 64 (the Qwen2-0.5B shape: ranges of about 5 tiles): every tile of the
+    // piece in flight at once, then the unrolled compute, instead of P-deep rounds (one K/V round
+    // trip instead of about three). 8 stages of 16 VGPRs fit beside the rest at 2 waves per SIMD,
+    // enough for the default 2048 workers; at D = 128 they would not.
+    constexpr int kUnrolled = (D == 64 && BPT == 1) ? 8 : 0;
+    if constexpr (kUnrolled > 0) {
+        if (nj <= kUnrolled) {
+            Regs su[kUnrolled];
+#pragma unroll
+            for (int j = 0; j < kUnrolled; ++j)
+                if (j < nj) load_tile(j, su[j]);
+#pragma unroll
+            for (int j = 0; j < kUnrolled; ++j)
+                if (j < nj && __builtin_amdgcn_readlane(my_pb, j) >= 0) compute_tile(j, su[j]);
+            return;
+        }
+    }
     {
         Regs st[P];
 #pragma unroll
@@ -463,7 +480,7 @@ __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t
 // K/V loads, with the math replaced by an xor of the loaded words (nothing is written unless
 // that checksum hits a magic value), so its duration is the gather alone.
 template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false>
-__global__ __launch_bounds__(kWaves * 64, MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
+__global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
     constexpr int BPT = BS >= kTile ? 1 : kTile / BS;  // KV blocks per tile (block sizes 4, 8)
     constexpr int kMaxRange = kMaxRangeTiles / BPT;    // tiles whose block ids fit one vector
