@@ -589,7 +589,10 @@ template <int D, int G>
 constexpr int merge_threads() {
     return ((G * D / 4 + 63) / 64) * 64;
 }
-template <int D, int BS, int G, bool BF16>
+// U: partials loaded per memory round trip. 32 where segments are cut into more than about 10 pieces
+// on average (the launch picks it from workers / segments), so their longest segments still take one
+// round trip: Qwen2-0.5B shape (16 pieces on average, up to about 25), see the launch.
+template <int D, int BS, int G, bool BF16, int U = 16>
 __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     constexpr int Q = D / 4;  // 4-dim groups per head
     const int kvh = blockIdx.x, b = blockIdx.y;
@@ -609,7 +612,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     // One online pass over the pieces, U at a time: every load of a batch is issued before
     // the first is used (indices clamped, values masked), so a segment cut by at most U
     // workers needs one memory round trip.
-    constexpr int U = 16;
     const int np = w1 - w0 + 1;
     const float kNegInf = -__builtin_huge_valf();
     const float* mlp = p.part_ml + (((int64_t)w0 + s) * G + h) * 2;
@@ -746,8 +748,13 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     const int blocks = (int)ceil_div(prm.workers, prm.wg_waves);
     hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16>), dim3(blocks), dim3(prm.wg_waves * 64), 0, st,
                        prm);
-    hipLaunchKernelGGL((decode_merge_kernel<D, BS, G, BF16>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0, st,
-                       prm);
+    const int64_t segs = (int64_t)B * prm.Hkv;
+    if (prm.workers > 10 * segs)
+        hipLaunchKernelGGL((decode_merge_kernel<D, BS, G, BF16, 32>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0,
+                           st, prm);
+    else
+        hipLaunchKernelGGL((decode_merge_kernel<D, BS, G, BF16, 16>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0,
+                           st, prm);
 }
 
 template <int D, int BS, bool STREAM, bool BF16>
