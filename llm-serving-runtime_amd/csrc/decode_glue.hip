@@ -9,6 +9,8 @@
 #include "common.h"
 #include "glue_common.h"
 
+#include <type_traits>
+
 namespace mx {
 namespace glue {
 
@@ -18,12 +20,20 @@ constexpr int kThreads = 256;
 // the value mx_w8a16_linear would have written (its reduce adds the bias, then the splits in order).
 // KS > 0 is the split count known at compile time: every load is issued before the first add, so
 // the partials cost one memory round trip; KS == 0 reads `splits` in a loop.
+// The bias is read as one E * 2-byte vector load that is issued whether or not there is a
+// bias (from the partials' own first bytes when there is none, then discarded), so no branch
+// or wait separates it from the partial loads. Callers keep bias + col aligned to E * 2 bytes.
 template <int KS, int E>
 __device__ __forceinline__ void sum_splits(const float* part, int splits, int64_t split_stride, int64_t off,
                                            const uint16_t* bias, int col, _Float16 (&out)[E]) {
+    using BiasVec = typename std::conditional<E == 8, uint4, uint2>::type;
+    static_assert(E == 4 || E == 8, "sum_splits: E is 4 or 8");
+    const BiasVec braw = *reinterpret_cast<const BiasVec*>(bias ? bias + col : reinterpret_cast<const uint16_t*>(part));
+    _Float16 bv[E];
+    __builtin_memcpy(bv, &braw, sizeof(bv));
     float acc[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] = bias ? (float)reinterpret_cast<const _Float16*>(bias)[col + e] : 0.0f;
+    for (int e = 0; e < E; ++e) acc[e] = bias ? (float)bv[e] : 0.0f;
     if (KS > 0) {
         float4v v[KS > 0 ? KS : 1][E / 4];
 #pragma unroll
@@ -247,12 +257,18 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(NormParams p)
     __shared__ float red[kNormThreads / 64];
     const int m = blockIdx.x;
     const int chunks = p.H >> 3;
-    half8v h[kNormMaxChunks];
+    const int64_t xr = SPLIT ? 0 : (p.rows ? p.rows[m] : m);
+    const bool x_in = (uint64_t)xr < (uint64_t)p.xcount;
+    half8v h[kNormMaxChunks], wv[kNormMaxChunks];
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kNormMaxChunks; ++u) {
         const int c = threadIdx.x + u * kNormThreads;
         if (c < chunks) {
+            // Norm weight, residual and x (or its partials) all go out before the first wait;
+            // without a residual the residual load re-reads the weights and is discarded.
+            wv[u] = as_h8(ld16(p.w + c * 8));
+            const half8v r = as_h8(ld16(p.res ? p.res + (int64_t)m * p.rs + c * 8 : p.w + c * 8));
             half8v v;
             if (SPLIT) {
                 _Float16 t[8];
@@ -261,29 +277,18 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(NormParams p)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = t[e];
             } else {
-                const int64_t xr = p.rows ? p.rows[m] : m;
-                const bool in = (uint64_t)xr < (uint64_t)p.xcount;
-                v = as_h8(ld16(p.x + (in ? xr : 0) * p.xs + c * 8));
-                if (!in) v = half8v{};
+                v = as_h8(ld16(p.x + (x_in ? xr : 0) * p.xs + c * 8));
+                if (!x_in) v = half8v{};
             }
-            if (p.res) {
-                const half8v r = as_h8(ld16(p.res + (int64_t)m * p.rs + c * 8));
+            // Without a residual the addend is -0.0, the exact identity of IEEE addition (it
+            // keeps -0 as -0), so the load's use, and with it the load, stays unconditional.
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] + (float)r[e]);
-            }
+            for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] + (p.res ? (float)r[e] : -0.0f));
             if (p.res_out) st16(p.res_out + (int64_t)m * p.ros + c * 8, as_u4(v));
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
             h[u] = v;
         }
-    }
-    // The norm weights are loaded before the row reduction's barrier, so their round trip
-    // overlaps it instead of following it.
-    half8v wv[kNormMaxChunks];
-#pragma unroll
-    for (int u = 0; u < kNormMaxChunks; ++u) {
-        const int c = threadIdx.x + u * kNormThreads;
-        if (c < chunks) wv[u] = as_h8(ld16(p.w + c * 8));
     }
     const float scale = rsqrtf(block_sum<kNormThreads>(ss, red) / (float)p.H + p.eps);
 #pragma unroll
