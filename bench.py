@@ -337,7 +337,7 @@ def family_launches(d: Decoder) -> dict:
 
     from runtime_amd.phase2.decode_glue import qkv_linear_rope_append
     from runtime_amd.phase2.int8_linear import int8_linear, int8_linear_partials
-    from runtime_amd.phase2.paged_attention_hip import _decode
+    from runtime_amd.phase2.paged_attention_hip import MX_PA_PLAN_READ, MX_PA_PLAN_WRITE, _decode
 
     model, pool, bsz, dev, s = d.model, d.pool, d.batch, d.dev, d.shape
     g = torch.Generator(device=dev).manual_seed(3)
@@ -383,9 +383,14 @@ def family_launches(d: Decoder) -> dict:
     out["gate_up"] = (gate_up, nl)
     out["down"] = (lin("down", buf.act), nl)
 
+    # As the step calls it: layer 0 records the tile plan, the later layers start from it.
+    planned = model.attn_plan and not model.shared_kv_blocks and pool.block_size_tokens >= 16
+
     def attn():
         for li in range(nl):
-            _decode(q, pool.k_layer_view(li), pool.v_layer_view(li), d.tables_d, lens, s.head_dim**-0.5, s.group)
+            plan = (MX_PA_PLAN_WRITE if li == 0 else MX_PA_PLAN_READ) if planned else 0
+            _decode(q, pool.k_layer_view(li), pool.v_layer_view(li), d.tables_d, lens, s.head_dim**-0.5, s.group,
+                    plan=plan)
     out["attn"] = (attn, nl)
     lm_y = torch.empty(bsz, s.vocab, device=dev, dtype=torch.float16)
 

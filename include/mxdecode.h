@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 13
+#define MX_ABI_VERSION 14
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -159,7 +159,8 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  *      the value the workspace was sized for. A
  *      second, small kernel on the same stream merges the ranges of a
  *      sequence that more than one wave touched.
- * flags: an OR of MX_PA_SHARED_BLOCKS and MX_PA_BF16 (or 0).
+ * flags: an OR of MX_PA_SHARED_BLOCKS, MX_PA_BF16 and one of MX_PA_PLAN_WRITE /
+ *      MX_PA_PLAN_READ (or 0).
  *      MX_PA_BF16: q, K, V and out hold bf16 instead of fp16 (the same layouts;
  *      scores, softmax and accumulation stay fp32, probabilities enter P.V in
  *      bf16). The reference kernel takes the pool's dtype
@@ -171,16 +172,32 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  *      same blocks in L2 / MALL. Results are the same either way. No reference
  *      counterpart: the reference copies prefix blocks per request
  *      (runtime/phase2/worker_server.py:1442-1449), so its rows never alias.
+ *      MX_PA_PLAN_WRITE / MX_PA_PLAN_READ (block_size >= 16, without
+ *      MX_PA_SHARED_BLOCKS): a decode step calls attention once per layer with
+ *      the same seq_lens, block_tables and shape. A PLAN_WRITE call also records
+ *      each wave's tiles (block id, sequence, kv-head, tile) in the workspace; a
+ *      later PLAN_READ call with the same workspace starts from that record
+ *      instead of locating its range from seq_lens and reading block_tables,
+ *      one dependent memory round trip less. Results are identical to a call
+ *      without the flags when seq_lens and block_tables are unchanged since
+ *      the PLAN_WRITE call (other inputs, such as q and the layer's K/V views,
+ *      may differ). Otherwise the output is undefined, no access leaves the
+ *      pool, q, out or the workspace, and mismatching pieces set bit 3 (value
+ *      8) of the error word. No reference counterpart: the reference re-derives
+ *      its grid per layer (paged_attention_triton.py:460-552).
  * Supported: D in {64, 128}; block_size in {4, 8, 16, 32}; Hq = G * Hkv, any G >= 1
  * (G > 8 runs as vg virtual kv-heads of G / vg <= 8 query heads each, vg the smallest
  * such divisor of G; each reads its pool head's K/V, so K/V bytes are read vg times).
  * The workspace holds the split partials (per piece: fp32 m and l, and its
- * output normalised by l in the element type) and the error word; zero it once at
+ * output normalised by l in the element type), the tile plan (16 bytes per tile
+ * slot, 64 slots per wave, block_size >= 16) and the error word; zero it once at
  * allocation so the error word starts clear. Concurrent calls must not share
  * a workspace. out rows must be 16-byte aligned (o_sb, o_sh multiples of 8).
  * ------------------------------------------------------------------------- */
 #define MX_PA_SHARED_BLOCKS 1u
 #define MX_PA_BF16 2u
+#define MX_PA_PLAN_WRITE 4u
+#define MX_PA_PLAN_READ 8u
 
 size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                      int32_t block_size, int32_t chunk_tokens);
@@ -198,8 +215,10 @@ int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const ui
  * decode path allocates scratch per shape (paged_attention_triton.py:90-115).
  * The split partials live in a static device array of
  * MX_PA_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
- * until the process ends; shapes whose workspace (mx_paged_attn_workspace_bytes)
- * exceeds it are refused with MX_ERR_WORKSPACE. The call allocates nothing.
+ * until the process ends; shapes whose workspace without the tile plan
+ * (mx_paged_attn_workspace_bytes less 1 KiB per wave) exceeds it are refused
+ * with MX_ERR_WORKSPACE, and the plan flags with MX_ERR_INVALID. The call
+ * allocates nothing.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (concurrent streams) race, so serialise them. err (nullable) is a
  * caller-owned int32 device word OR-ed with the error bits (bit 0: a block id

@@ -83,6 +83,7 @@ struct Params {
     int workers;
     int wg_waves;     // waves per workgroup of the split launch (<= kWaves)
     int vg;           // virtual kv-heads per pool head (GQA groups above 8, see kv_virtual_groups)
+    int4* plan;       // [workers][64] tile plan: written by a MX_PA_PLAN_WRITE call, read by MX_PA_PLAN_READ
 };
 
 constexpr int kWaves = 4;               // waves per workgroup of the split launch (at most)
@@ -276,9 +277,14 @@ constexpr int kDepth = MX_PA_DEPTH;
 // partial denominator (sum over the 4 lane groups with xor_sum_16_32); acc[e][i] the
 // unnormalised output of head r at dim (4g + i) * DPL + e, g = lane / 16. PROBE: the loads
 // alone (see decode_split_kernel).
-template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false, int P = kDepth>
+//
+// PLANNED: the piece's block ids come from the plan (pb_in: lane j holds tile t0 + j's, -1 for an id
+// outside the pool) instead of the block table. plan_dst (block size >= 16, not PLANNED): lanes
+// j < nj also record their tile there as {block id, b << 16 | kvh, t0 + j, s_eff}.
+template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false, bool PLANNED = false, int P = kDepth>
 __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t0, int nj, int s_eff, int lane,
-                                          float& m_run, float& l_run, float4v (&acc)[D / 16]) {
+                                          float& m_run, float& l_run, float4v (&acc)[D / 16], int pb_in = 0,
+                                          int4* plan_dst = nullptr) {
     constexpr int KK = D / 32;       // score MFMA k-steps over the head dim
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
     constexpr int TPB = BS >= kTile ? BS / kTile : 1;  // tiles per KV block (block sizes 16, 32)
@@ -298,22 +304,30 @@ __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t
     // Block ids of the piece: lane j holds the id of tile t0 + j (BPT == 1) or of block
     // slot j of the piece's tiles (BPT > 1, only the row's blocks below s_eff are read);
     // an id outside the pool becomes -1 (its tokens skipped, error recorded).
-    const int32_t* bt_row = p.bt + (int64_t)b * p.bt_sb;
     int my_pb = 0;
-    bool fetch;
-    int bslot;
-    if constexpr (BPT == 1) {
-        fetch = lane < nj;
-        bslot = (t0 + lane) / TPB;
+    if constexpr (PLANNED) {
+        static_assert(BPT == 1, "the tile plan covers block sizes >= 16");
+        my_pb = pb_in;
     } else {
-        bslot = t0 * BPT + lane;
-        fetch = lane < nj * BPT && bslot < (s_eff + BS - 1) / BS;
-    }
-    if (fetch) {
-        my_pb = bt_row[bslot];
-        if ((unsigned)my_pb >= (unsigned)p.num_pool_blocks) {  // never read outside the pool
-            atomicOr(p.err, 1);
-            my_pb = -1;
+        const int32_t* bt_row = p.bt + (int64_t)b * p.bt_sb;
+        bool fetch;
+        int bslot;
+        if constexpr (BPT == 1) {
+            fetch = lane < nj;
+            bslot = (t0 + lane) / TPB;
+        } else {
+            bslot = t0 * BPT + lane;
+            fetch = lane < nj * BPT && bslot < (s_eff + BS - 1) / BS;
+        }
+        if (fetch) {
+            my_pb = bt_row[bslot];
+            if ((unsigned)my_pb >= (unsigned)p.num_pool_blocks) {  // never read outside the pool
+                atomicOr(p.err, 1);
+                my_pb = -1;
+            }
+        }
+        if constexpr (BPT == 1) {
+            if (plan_dst && lane < nj) plan_dst[lane] = int4{my_pb, (int)((unsigned)b << 16 | (unsigned)kvh), t0 + lane, s_eff};
         }
     }
 
@@ -485,7 +499,7 @@ __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t
 // PROBE = true: the calibration instance of mx_kv_gather_probe. The same partition and the same
 // K/V loads, with the math replaced by an xor of the loaded words (nothing is written unless
 // that checksum hits a magic value), so its duration is the gather alone.
-template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false>
+template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false, bool PLANNED = false>
 __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
     constexpr int BPT = BS >= kTile ? 1 : kTile / BS;  // KV blocks per tile (block sizes 4, 8)
@@ -497,55 +511,10 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
     const int worker = blockIdx.x * p.wg_waves + wave;
     const int g = lane >> 4, r = lane & 15;
 
-    // Up to 64 rows: one read of seq_lens per wave, reused to locate every piece.
-    const bool one_pass = p.B <= 64;
-    int n_lane = 0, s_eff_lane = 0, incl_lane = 0;
-    int64_t T;
-    if (one_pass) {
-        if (lane < p.B) n_lane = row_tiles<BS>(p, lane, s_eff_lane);
-        incl_lane = wave_incl_scan(n_lane, lane);
-        T = (int64_t)__builtin_amdgcn_readlane(incl_lane, 63) * p.Hkv;
-    } else {
-        T = total_tiles<BS>(p, lane);
-    }
-    const int W = T < p.workers ? (int)T : p.workers;  // every worker gets >= 1 tile
-    if (worker >= W) return;
-    const int64_t hi = range_lo(worker + 1, T, W);
-    int64_t x = range_lo(worker, T, W);
-
-    while (x < hi) {
-        Seg sg;
-        if (one_pass) {
-            const int excl = incl_lane - n_lane;
-            const bool le = lane < p.B && (int64_t)excl * p.Hkv <= x;
-            const int bl = __builtin_popcountll(__builtin_amdgcn_ballot_w64(le)) - 1;
-            sg = Seg{bl, __builtin_amdgcn_readlane(n_lane, bl), (int64_t)__builtin_amdgcn_readlane(excl, bl) * p.Hkv};
-        } else {
-            sg = locate<BS>(p, x, lane);
-        }
-        const int b = sg.b, nt = sg.ntiles;
-        if (nt <= 0) {  // cannot happen for x < T; stop rather than divide by zero
-            atomicOr(p.err, 4);
-            break;
-        }
-        const int kvh = (int)((x - sg.row_start) / nt);
-        const int t0 = (int)((x - sg.row_start) % nt);
-        const int t1 = (int64_t)(nt - t0) < hi - x ? nt : (int)(t0 + (hi - x));
-        const int nj = t1 - t0;  // <= kMaxRange because W >= ceil(T_max / kMaxRange)
-        if (nj > kMaxRange) {
-            atomicOr(p.err, 4);
-            break;
-        }
-        x += nj;
-        int s_eff;
-        if (one_pass) s_eff = __builtin_amdgcn_readlane(s_eff_lane, b);
-        else row_tiles<BS>(p, b, s_eff);
+    // A finished piece: tiles [t0, t1) of segment (b, kvh), whose row has nt tiles. A whole
+    // segment writes the output; a cut one its partial at slot worker + segment.
+    auto finish = [&](int b, int kvh, int t0, int t1, int nt, float m_run, float l_run, const float4v (&acc)[DPL]) {
         const int h0 = kvh * G;
-        float m_run, l_run;
-        float4v acc[DPL];
-        run_piece<D, BS, G, STREAM, BF16, PROBE>(p, b, kvh, t0, nj, s_eff, lane, m_run, l_run, acc);
-        if constexpr (PROBE) continue;
-
         // Denominator of head r over the 4 lane groups; acc already sums all 16 tokens of a tile.
         l_run = xor_sum_16_32(l_run);
         const bool whole = t0 == 0 && t1 == nt;
@@ -584,6 +553,108 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
                 }
             }
         }
+    };
+
+    if constexpr (PLANNED) {
+        // The worker's tiles as a MX_PA_PLAN_WRITE call with the same lengths and tables recorded
+        // them: lane j holds tile j of the range as {block id, b << 16 | kvh, t, s_eff} (-1 in the
+        // second word past the range). One load replaces the lengths -> range -> block ids chain.
+        // Entries are checked before use, so a plan that does not match the call reads nothing
+        // outside the pool, q or the workspace; such pieces (also those whose row length changed
+        // since, checked after their loads) write nothing and set error bit 8.
+        const int4 e = p.plan[(int64_t)worker * 64 + lane];
+        const bool live = e.y != -1;
+        const int prev_y = __shfl_up(e.y, 1), prev_t = __shfl_up(e.z, 1);
+        const bool start = live && (lane == 0 || e.y != prev_y || e.z != prev_t + 1);
+        uint64_t starts = __builtin_amdgcn_ballot_w64(start);
+        const int count = __builtin_popcountll(__builtin_amdgcn_ballot_w64(live));
+        while (starts) {
+            const int j0 = (int)__builtin_ctzll(starts);
+            starts &= starts - 1;
+            const int j1 = starts ? (int)__builtin_ctzll(starts) : count;
+            const unsigned bk = (unsigned)__builtin_amdgcn_readlane(e.y, j0);
+            const int b = (int)(bk >> 16), kvh = (int)(bk & 0xffffu);
+            const int t0 = __builtin_amdgcn_readlane(e.z, j0), s_eff = __builtin_amdgcn_readlane(e.w, j0);
+            const int nj = j1 - j0;
+            const int nt = (s_eff + kTile - 1) / kTile;
+            if (b >= p.B || kvh >= p.Hkv || t0 < 0 || nj <= 0 || s_eff < 0 || s_eff > p.max_blocks * BS ||
+                t0 + nj > nt) {
+                if (lane == 0) atomicOr(p.err, 8);
+                break;
+            }
+            int pb = __shfl(e.x, j0 + lane);
+            if (lane >= nj || (unsigned)pb >= (unsigned)p.num_pool_blocks) pb = -1;
+            float m_run, l_run;
+            float4v acc[DPL];
+            run_piece<D, BS, G, STREAM, BF16, false, true>(p, b, kvh, t0, nj, s_eff, lane, m_run, l_run, acc, pb);
+            int s_now;
+            row_tiles<BS>(p, b, s_now);
+            if (s_now != s_eff) {  // the row's length changed since the plan was recorded
+                if (lane == 0) atomicOr(p.err, 8);
+                continue;
+            }
+            finish(b, kvh, t0, t0 + nj, nt, m_run, l_run, acc);
+        }
+        return;
+    }
+
+    // Up to 64 rows: one read of seq_lens per wave, reused to locate every piece.
+    const bool one_pass = p.B <= 64;
+    int n_lane = 0, s_eff_lane = 0, incl_lane = 0;
+    int64_t T;
+    if (one_pass) {
+        if (lane < p.B) n_lane = row_tiles<BS>(p, lane, s_eff_lane);
+        incl_lane = wave_incl_scan(n_lane, lane);
+        T = (int64_t)__builtin_amdgcn_readlane(incl_lane, 63) * p.Hkv;
+    } else {
+        T = total_tiles<BS>(p, lane);
+    }
+    const int W = T < p.workers ? (int)T : p.workers;  // every worker gets >= 1 tile
+    // MX_PA_PLAN_WRITE (block size >= 16): record every tile of the range for later calls; lanes
+    // past the range (all of them for an idle worker) mark the end.
+    int4* const plan_w = (!PROBE && BPT == 1 && p.plan) ? p.plan + (int64_t)worker * 64 : nullptr;
+    if (worker >= W) {
+        if (plan_w) plan_w[lane] = int4{0, -1, 0, 0};
+        return;
+    }
+    const int64_t hi = range_lo(worker + 1, T, W);
+    int64_t x = range_lo(worker, T, W);
+    const int64_t x_first = x;
+    if (plan_w && lane >= hi - x_first) plan_w[lane] = int4{0, -1, 0, 0};
+
+    while (x < hi) {
+        Seg sg;
+        if (one_pass) {
+            const int excl = incl_lane - n_lane;
+            const bool le = lane < p.B && (int64_t)excl * p.Hkv <= x;
+            const int bl = __builtin_popcountll(__builtin_amdgcn_ballot_w64(le)) - 1;
+            sg = Seg{bl, __builtin_amdgcn_readlane(n_lane, bl), (int64_t)__builtin_amdgcn_readlane(excl, bl) * p.Hkv};
+        } else {
+            sg = locate<BS>(p, x, lane);
+        }
+        const int b = sg.b, nt = sg.ntiles;
+        if (nt <= 0) {  // cannot happen for x < T; stop rather than divide by zero
+            atomicOr(p.err, 4);
+            break;
+        }
+        const int kvh = (int)((x - sg.row_start) / nt);
+        const int t0 = (int)((x - sg.row_start) % nt);
+        const int t1 = (int64_t)(nt - t0) < hi - x ? nt : (int)(t0 + (hi - x));
+        const int nj = t1 - t0;  // <= kMaxRange because W >= ceil(T_max / kMaxRange)
+        if (nj > kMaxRange) {
+            atomicOr(p.err, 4);
+            break;
+        }
+        int4* const plan_dst = plan_w ? plan_w + (x - x_first) : nullptr;
+        x += nj;
+        int s_eff;
+        if (one_pass) s_eff = __builtin_amdgcn_readlane(s_eff_lane, b);
+        else row_tiles<BS>(p, b, s_eff);
+        float m_run, l_run;
+        float4v acc[DPL];
+        run_piece<D, BS, G, STREAM, BF16, PROBE>(p, b, kvh, t0, nj, s_eff, lane, m_run, l_run, acc, 0, plan_dst);
+        if constexpr (PROBE) continue;
+        finish(b, kvh, t0, t1, nt, m_run, l_run, acc);
     }
 }
 
@@ -676,7 +747,7 @@ static inline int kv_virtual_groups(int Hq, int Hkv) {
 }
 
 struct Layout {
-    size_t err, segw, ml, acc, total;
+    size_t err, segw, ml, acc, plan, total;  // plan == total: no tile plan in this layout
     int workers;
 };
 
@@ -708,8 +779,10 @@ static int resolve_workers(int chunk_tokens, int B, int Hkv, int max_blocks, int
     return (int)(w > (1 << 30) ? (1 << 30) : w);
 }
 
-// Hkv: kv-heads as the kernels see them (after kv_virtual_groups).
-static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_size, int chunk_tokens) {
+// Hkv: kv-heads as the kernels see them (after kv_virtual_groups). with_plan: room for the tile
+// plan of MX_PA_PLAN_WRITE / MX_PA_PLAN_READ (64 entries of 16 bytes per worker, block size >= 16).
+static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_size, int chunk_tokens,
+                     bool with_plan) {
     Layout L{};
     L.workers = resolve_workers(chunk_tokens, B, Hkv, max_blocks, block_size);
     const int G = Hkv > 0 ? Hq / Hkv : 0;
@@ -718,7 +791,8 @@ static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_si
     L.segw = 256;
     L.ml = L.segw + align256((size_t)B * Hkv * 2 * sizeof(int));
     L.acc = L.ml + align256(slots * G * 2 * sizeof(float));
-    L.total = L.acc + align256(slots * G * D * sizeof(uint16_t));
+    L.plan = L.acc + align256(slots * G * D * sizeof(uint16_t));
+    L.total = L.plan + (with_plan && block_size >= kTile ? align256((size_t)L.workers * 64 * sizeof(int4)) : 0);
     return L;
 }
 
@@ -740,8 +814,10 @@ static int resident_waves() {
     return cache[dev];
 }
 
-template <int D, int BS, int G, bool STREAM, bool BF16>
+template <int D, int BS, int G, bool STREAM, bool BF16, bool PLANNED = false>
 static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
+    // The worker count comes from the plain instance, so a MX_PA_PLAN_READ call has exactly the
+    // workers whose plans the MX_PA_PLAN_WRITE call recorded.
     // More workers than resident waves would leave a second, partial round; use
     // one round unless ranges would then exceed max_range_tiles.
     const int cap = resident_waves<D, BS, G, STREAM, BF16>();
@@ -752,8 +828,8 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     // 56.3 (2 waves) and 57.3 (1 wave).
     prm.wg_waves = prm.workers <= kSmallWorkers ? 2 : kWaves;
     const int blocks = (int)ceil_div(prm.workers, prm.wg_waves);
-    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16>), dim3(blocks), dim3(prm.wg_waves * 64), 0, st,
-                       prm);
+    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16, false, PLANNED>), dim3(blocks),
+                       dim3(prm.wg_waves * 64), 0, st, prm);
     const int64_t segs = (int64_t)B * prm.Hkv;
     if (prm.workers > 10 * segs)
         hipLaunchKernelGGL((decode_merge_kernel<D, BS, G, BF16, 32>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0,
@@ -764,7 +840,23 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
 }
 
 template <int D, int BS, bool STREAM, bool BF16>
-static bool dispatch_g(int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
+static bool dispatch_g(int G, bool planned, const Params& prm, int B, hipStream_t st, int64_t fw) {
+    if (planned) {  // plan reads: block sizes >= 16 with streaming loads only
+        if constexpr (BS >= kTile && STREAM) {
+            switch (G) {
+                case 1: launch<D, BS, 1, STREAM, BF16, true>(prm, B, st, fw); return true;
+                case 2: launch<D, BS, 2, STREAM, BF16, true>(prm, B, st, fw); return true;
+                case 3: launch<D, BS, 3, STREAM, BF16, true>(prm, B, st, fw); return true;
+                case 4: launch<D, BS, 4, STREAM, BF16, true>(prm, B, st, fw); return true;
+                case 5: launch<D, BS, 5, STREAM, BF16, true>(prm, B, st, fw); return true;
+                case 6: launch<D, BS, 6, STREAM, BF16, true>(prm, B, st, fw); return true;
+                case 7: launch<D, BS, 7, STREAM, BF16, true>(prm, B, st, fw); return true;
+                case 8: launch<D, BS, 8, STREAM, BF16, true>(prm, B, st, fw); return true;
+                default: return false;
+            }
+        }
+        return false;
+    }
     switch (G) {
         case 1: launch<D, BS, 1, STREAM, BF16>(prm, B, st, fw); return true;
         case 2: launch<D, BS, 2, STREAM, BF16>(prm, B, st, fw); return true;
@@ -779,16 +871,16 @@ static bool dispatch_g(int G, const Params& prm, int B, hipStream_t st, int64_t 
 }
 
 template <bool STREAM, bool BF16>
-static bool dispatch_d_bs(int D, int BS, int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
+static bool dispatch_d_bs(int D, int BS, int G, bool planned, const Params& prm, int B, hipStream_t st, int64_t fw) {
     switch (D * 100 + BS) {
-        case 12804: return dispatch_g<128, 4, STREAM, BF16>(G, prm, B, st, fw);
-        case 12808: return dispatch_g<128, 8, STREAM, BF16>(G, prm, B, st, fw);
-        case 12816: return dispatch_g<128, 16, STREAM, BF16>(G, prm, B, st, fw);
-        case 12832: return dispatch_g<128, 32, STREAM, BF16>(G, prm, B, st, fw);
-        case 6404: return dispatch_g<64, 4, STREAM, BF16>(G, prm, B, st, fw);
-        case 6408: return dispatch_g<64, 8, STREAM, BF16>(G, prm, B, st, fw);
-        case 6416: return dispatch_g<64, 16, STREAM, BF16>(G, prm, B, st, fw);
-        case 6432: return dispatch_g<64, 32, STREAM, BF16>(G, prm, B, st, fw);
+        case 12804: return dispatch_g<128, 4, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 12808: return dispatch_g<128, 8, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 12816: return dispatch_g<128, 16, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 12832: return dispatch_g<128, 32, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 6404: return dispatch_g<64, 4, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 6408: return dispatch_g<64, 8, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 6416: return dispatch_g<64, 16, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 6432: return dispatch_g<64, 32, STREAM, BF16>(G, planned, prm, B, st, fw);
         default: return false;
     }
 }
@@ -862,13 +954,13 @@ using namespace mx;
 extern "C" size_t mx_paged_attn_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                                 int32_t block_size, int32_t chunk_tokens) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_blocks < 0 || block_size <= 0) return 0;
-    return pa::layout(B, Hq, Hkv * pa::kv_virtual_groups(Hq, Hkv), D, max_blocks, block_size, chunk_tokens).total;
+    return pa::layout(B, Hq, Hkv * pa::kv_virtual_groups(Hq, Hkv), D, max_blocks, block_size, chunk_tokens, true).total;
 }
 
 extern "C" size_t mx_paged_attn_error_offset(int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t max_blocks,
                                              int32_t block_size, int32_t chunk_tokens) {
     if (Hkv <= 0) return 0;
-    return pa::layout(B, Hq, Hkv * pa::kv_virtual_groups(Hq, Hkv), D, max_blocks, block_size, chunk_tokens).err;
+    return pa::layout(B, Hq, Hkv * pa::kv_virtual_groups(Hq, Hkv), D, max_blocks, block_size, chunk_tokens, true).err;
 }
 
 namespace mx {
@@ -891,7 +983,12 @@ static int check_args(const char* what, const uint16_t* q, int64_t q_sb, int64_t
         return fail(MX_ERR_INVALID, "%s: max_blocks and num_pool_blocks must be >= 1", what);
     const int vg = kv_virtual_groups(Hq, Hkv);
     if (B > 65535 || (int64_t)Hkv * vg > 65535) return fail(MX_ERR_UNSUPPORTED, "%s: B or Hq too large", what);
-    if (flags & ~(uint32_t)(MX_PA_SHARED_BLOCKS | MX_PA_BF16)) return fail(MX_ERR_INVALID, "%s: unknown flags 0x%x", what, flags);
+    if (flags & ~(uint32_t)(MX_PA_SHARED_BLOCKS | MX_PA_BF16 | MX_PA_PLAN_WRITE | MX_PA_PLAN_READ))
+        return fail(MX_ERR_INVALID, "%s: unknown flags 0x%x", what, flags);
+    if ((flags & MX_PA_PLAN_WRITE) && (flags & MX_PA_PLAN_READ))
+        return fail(MX_ERR_INVALID, "%s: MX_PA_PLAN_WRITE and MX_PA_PLAN_READ exclude each other", what);
+    if ((flags & (MX_PA_PLAN_WRITE | MX_PA_PLAN_READ)) && (block_size < kTile || (flags & MX_PA_SHARED_BLOCKS)))
+        return fail(MX_ERR_UNSUPPORTED, "%s: the tile plan needs block_size >= 16 and no MX_PA_SHARED_BLOCKS", what);
     if (chunk_tokens < 0 || chunk_tokens % kTile != 0 || chunk_tokens > kMaxChunkTokens)
         return fail(MX_ERR_INVALID, "%s: chunk_tokens must be 0 or a multiple of 16 <= %d", what, kMaxChunkTokens);
     if ((int64_t)B * Hkv * vg * ceil_div((int64_t)max_blocks * block_size, kTile) > ((int64_t)1 << 31))
@@ -930,19 +1027,20 @@ static int launch_decode(const char* what, Params prm, const Layout& L, char* ws
     prm.part_ml = reinterpret_cast<float*>(ws + L.ml);
     prm.part_out = reinterpret_cast<_Float16*>(ws + L.acc);
     prm.seg_w = reinterpret_cast<int*>(ws + L.segw);
+    prm.plan = (flags & (MX_PA_PLAN_WRITE | MX_PA_PLAN_READ)) ? reinterpret_cast<int4*>(ws + L.plan) : nullptr;
     prm.workers = L.workers;
     hipStream_t st = as_stream(stream);
     // Fewest workers that keep every range within one vector of block ids.
     const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, kTile),
                                 max_range_tiles(block_size));
-    const bool shared = flags & MX_PA_SHARED_BLOCKS, bf16 = flags & MX_PA_BF16;
+    const bool shared = flags & MX_PA_SHARED_BLOCKS, bf16 = flags & MX_PA_BF16, planned = flags & MX_PA_PLAN_READ;
     bool ok;
     if (bf16)
-        ok = shared ? dispatch_d_bs<false, true>(D, block_size, G, prm, B, st, fw)
-                    : dispatch_d_bs<true, true>(D, block_size, G, prm, B, st, fw);
+        ok = shared ? dispatch_d_bs<false, true>(D, block_size, G, planned, prm, B, st, fw)
+                    : dispatch_d_bs<true, true>(D, block_size, G, planned, prm, B, st, fw);
     else
-        ok = shared ? dispatch_d_bs<false, false>(D, block_size, G, prm, B, st, fw)
-                    : dispatch_d_bs<true, false>(D, block_size, G, prm, B, st, fw);
+        ok = shared ? dispatch_d_bs<false, false>(D, block_size, G, planned, prm, B, st, fw)
+                    : dispatch_d_bs<true, false>(D, block_size, G, planned, prm, B, st, fw);
     if (!ok) return fail(MX_ERR_UNSUPPORTED, "%s: unsupported configuration", what);
     return check_launch(what);
 }
@@ -991,7 +1089,7 @@ extern "C" int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_s
     int rc = pa::check_args(what, q, q_sb, q_sh, k, v, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, seq_lens, B,
                             Hq, Hkv, D, block_size, num_pool_blocks, scale, out, o_sb, o_sh, chunk_tokens, flags, prm);
     if (rc != MX_OK) return rc;
-    const pa::Layout L = pa::layout(B, Hq, prm.Hkv, D, max_blocks, block_size, chunk_tokens);
+    const pa::Layout L = pa::layout(B, Hq, prm.Hkv, D, max_blocks, block_size, chunk_tokens, true);
     if (!workspace || workspace_bytes < L.total)
         return fail(MX_ERR_WORKSPACE, "%s: workspace needs %zu bytes, got %zu", what, L.total, workspace_bytes);
     if (!aligned(workspace, 256)) return fail(MX_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", what);
@@ -1014,7 +1112,9 @@ extern "C" int mx_paged_attn_decode_noalloc(const uint16_t* q, int64_t q_sb, int
                             Hq, Hkv, D, block_size, num_pool_blocks, scale, out, o_sb, o_sh, chunk_tokens, flags, prm);
     if (rc != MX_OK) return rc;
     if (err && !aligned(err, 4)) return fail(MX_ERR_ALIGNMENT, "%s: err must be 4-byte aligned", what);
-    const pa::Layout L = pa::layout(B, Hq, prm.Hkv, D, max_blocks, block_size, chunk_tokens);
+    if (flags & (MX_PA_PLAN_WRITE | MX_PA_PLAN_READ))
+        return fail(MX_ERR_INVALID, "%s: the tile plan lives in a caller's workspace (mx_paged_attn_decode)", what);
+    const pa::Layout L = pa::layout(B, Hq, prm.Hkv, D, max_blocks, block_size, chunk_tokens, false);
     if (L.total > (size_t)MX_PA_NOALLOC_SCRATCH_BYTES)
         return fail(MX_ERR_WORKSPACE, "%s: this shape needs %zu bytes of scratch, more than the %zu the library holds "
                                       "per GPU; use mx_paged_attn_decode with a workspace",

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 MX_OK = 0
 MX_ERR_INVALID = -1

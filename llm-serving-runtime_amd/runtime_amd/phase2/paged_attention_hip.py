@@ -43,6 +43,8 @@ if TYPE_CHECKING:
 _CHUNK_TOKENS = int(os.getenv("MX_PAGED_ATTN_CHUNK_TOKENS", "0"))
 MX_PA_SHARED_BLOCKS = 1
 MX_PA_BF16 = 2
+MX_PA_PLAN_WRITE = 4  # also record each wave's tiles in the workspace (block size >= 16)
+MX_PA_PLAN_READ = 8   # start from the tiles a PLAN_WRITE call recorded (same lengths and tables)
 _DTYPE_FLAGS = {torch.float16: 0, torch.bfloat16: MX_PA_BF16}
 
 _decode_batch_metadata: contextvars.ContextVar["PagedDecodeBatchMetadata | None"] = contextvars.ContextVar(
@@ -131,7 +133,10 @@ def workspace_error_flag(device: torch.device | None = None) -> int:
 
 def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor,
             seq_lens: torch.Tensor, scaling: float, num_kv_groups: int, out: torch.Tensor | None = None,
-            shared_blocks: bool = False) -> torch.Tensor:
+            shared_blocks: bool = False, plan: int = 0) -> torch.Tensor:
+    """One ``mx_paged_attn_decode`` call. ``plan`` is 0, ``MX_PA_PLAN_WRITE`` or ``MX_PA_PLAN_READ``:
+    a decode step records the tile plan at its first layer and the later layers, whose lengths and
+    tables are the same, start from it (block size >= 16, not with ``shared_blocks``)."""
     bsz, hq, q_len, d = query.shape
     if q_len != 1:
         raise ValueError("paged decode expects q_len=1")
@@ -172,7 +177,7 @@ def _decode(query: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor, b
             k_layer.stride(0), k_layer.stride(1), block_tables.data_ptr(), block_tables.stride(0), max_blocks,
             seq_lens.data_ptr(), bsz, hq, hkv, d, bs, nb, float(scaling), out.data_ptr(), out.stride(0),
             out.stride(1), ws.data_ptr(), nbytes, _CHUNK_TOKENS,
-            _DTYPE_FLAGS[query.dtype] | (MX_PA_SHARED_BLOCKS if shared_blocks else 0),
+            _DTYPE_FLAGS[query.dtype] | (MX_PA_SHARED_BLOCKS if shared_blocks else 0) | plan,
             _hip.stream_handle(query.device),
         ),
         "mx_paged_attn_decode",

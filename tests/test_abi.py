@@ -38,9 +38,14 @@ def test_paged_attn_workspace_layout_is_host_computable():
     assert 0 < small < big
     # One partial per worker + segment slot (fp32 m, l and a 16-bit output of D per head, G heads):
     # 65536 tiles at the table width in ranges of 16 tiles -> 4096 workers, + 256 segments.
+    # Block size 16 also holds the tile plan of MX_PA_PLAN_WRITE / MX_PA_PLAN_READ: 64 entries of
+    # 16 bytes per worker; block sizes 4 and 8 have none.
     slots = 4096 + 256
-    assert big >= slots * 4 * (2 * 4 + 128 * 2)
-    assert big < slots * 4 * (2 * 4 + 128 * 4)  # half the bytes of an fp32 accumulator
+    plan = 4096 * 64 * 16
+    assert big >= slots * 4 * (2 * 4 + 128 * 2) + plan
+    assert big < slots * 4 * (2 * 4 + 128 * 4) + plan  # half the bytes of an fp32 accumulator
+    w8 = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 512, 8, 256)  # same tiles and workers, no plan
+    assert w8 + plan == big
     assert lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 512) < big
     # Default split: 2048 workers for config 2's table (ranges of 32 tiles = 512 tokens at full
     # width); a single short row gets ranges of 4 tiles (64 tokens).
@@ -108,7 +113,17 @@ def test_invalid_arguments_return_status_codes():
     _status(call(bs=12), _hip.MX_ERR_UNSUPPORTED)
     _status(call(ct=40), _hip.MX_ERR_INVALID)
     _status(call(ct=2048), _hip.MX_ERR_INVALID)  # split granularity is at most 64 tiles
-    _status(call(flags=4), _hip.MX_ERR_INVALID)  # only MX_PA_SHARED_BLOCKS and MX_PA_BF16 are defined
+    _status(call(flags=16), _hip.MX_ERR_INVALID)  # bits 0-3 are the defined flags
+    _status(call(flags=4 | 8), _hip.MX_ERR_INVALID)  # PLAN_WRITE and PLAN_READ exclude each other
+    _status(call(flags=8, bs=8), _hip.MX_ERR_UNSUPPORTED)  # the tile plan needs block_size >= 16
+    _status(call(flags=4 | 1), _hip.MX_ERR_UNSUPPORTED)  # ... and no MX_PA_SHARED_BLOCKS
+    _status(call(flags=4), _hip.MX_ERR_WORKSPACE)
+    # The workspace-free entry point has no room for the plan (checked before it touches a device).
+    a = args
+    _status(lib.mx_paged_attn_decode_noalloc(a["q"], a["q_sb"], a["q_sh"], a["k"], a["v"], a["kv_sblk"],
+                                             a["kv_shead"], a["bt"], a["bt_sb"], a["mb"], a["sl"], a["B"], a["Hq"],
+                                             a["Hkv"], a["D"], a["bs"], a["npool"], a["scale"], a["out"], a["o_sb"],
+                                             a["o_sh"], a["ct"], 8, None, a["st"]), _hip.MX_ERR_INVALID)
     _status(call(), _hip.MX_ERR_WORKSPACE)
     _status(call(q_sh=60), _hip.MX_ERR_ALIGNMENT)
     # Chunked argmax: the key workspace is M x ceil(N / 4096) x 8 bytes, and every argument is

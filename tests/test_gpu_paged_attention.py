@@ -427,3 +427,77 @@ def test_config5_shared_prefix_full_shape():
     assert err0 == 0 and err1 == 0
     assert torch.equal(shared, stream)
     _check(shared, oracle_out(q, k, v, tables, lens_h, scale, grp))
+
+
+@pytest.mark.parametrize("bsz,hq,hkv,d,bs,dtype", [
+    (16, 14, 2, 64, 16, torch.float16),    # config 3 heads
+    (32, 32, 8, 128, 16, torch.float16),   # config 2 heads
+    (8, 16, 4, 128, 32, torch.bfloat16),   # block size 32 (2 tiles per block), bf16
+    (72, 8, 2, 64, 16, torch.float16),     # more than 64 rows (the lengths are not read in one pass)
+    (4, 24, 2, 64, 16, torch.float16),     # G = 12: virtual kv-heads
+])
+def test_tile_plan_matches_plain_calls(bsz, hq, hkv, d, bs, dtype):
+    """MX_PA_PLAN_WRITE then MX_PA_PLAN_READ, as a decode step uses them (layer 0 records, the later
+    layers start from the record): with the same lengths and tables, both calls equal the plain
+    call bit for bit, for another query and another layer's K/V too, and no error bit is set.
+    Rows of length 0, 1 and ones that fill their last block exactly are included."""
+    from runtime_amd.phase2.paged_attention_hip import MX_PA_PLAN_READ, MX_PA_PLAN_WRITE
+    from runtime_amd.phase2.paged_attention_hip import _decode as hip_decode
+
+    grp = hq // hkv
+    g = torch.Generator().manual_seed(bsz * 7 + d)
+    lens = torch.randint(1, 1500, (bsz,), generator=g)
+    lens[0], lens[1 % bsz] = 0, 1
+    lens[2 % bsz] = 4 * bs
+    print(f"[plan] B={bsz} Hq={hq} Hkv={hkv} D={d} bs={bs} {dtype}", flush=True)
+    q, k, v, tables, seq_lens = _random_case(11, bsz, hkv, grp, d, bs, lens.tolist())
+    k2, v2 = torch.randn_like(k.float()).to(dtype), torch.randn_like(v.float()).to(dtype)
+    k, v, q = k.to(dtype), v.to(dtype), q.to(dtype)
+    q2 = torch.randn_like(q.float()).to(dtype)
+    scale = d ** -0.5
+    dev = q.device
+    before = workspace_error_flag(dev)
+    plain1 = hip_decode(q, k, v, tables, seq_lens, scale, grp)
+    plain2 = hip_decode(q2, k2, v2, tables, seq_lens, scale, grp)
+    rec = hip_decode(q, k, v, tables, seq_lens, scale, grp, plan=MX_PA_PLAN_WRITE)
+    read2 = hip_decode(q2, k2, v2, tables, seq_lens, scale, grp, plan=MX_PA_PLAN_READ)
+    read1 = hip_decode(q, k, v, tables, seq_lens, scale, grp, plan=MX_PA_PLAN_READ)
+    torch.cuda.synchronize()
+    assert torch.equal(rec.view(torch.int16), plain1.view(torch.int16))
+    assert torch.equal(read1.view(torch.int16), plain1.view(torch.int16))
+    assert torch.equal(read2.view(torch.int16), plain2.view(torch.int16))
+    assert (workspace_error_flag(dev) & ~before & 8) == 0
+    if dtype == torch.float16:
+        _check(read2, oracle_out(q2, k2, v2, tables, seq_lens, scale, grp), "plan read vs oracle")
+
+
+def test_tile_plan_flags_changed_lengths():
+    """A MX_PA_PLAN_READ call whose lengths differ from the recording call: the pieces of the rows
+    that changed are dropped and error bit 8 is set; nothing is read outside the pool (every
+    plan entry is checked), and a plain call afterwards is still exact."""
+    from runtime_amd.phase2.paged_attention_hip import MX_PA_PLAN_READ, MX_PA_PLAN_WRITE
+    from runtime_amd.phase2.paged_attention_hip import _decode as hip_decode
+
+    bsz, hkv, grp, d, bs = 6, 2, 4, 128, 16
+    lens = [700, 33, 64, 1000, 5, 300]
+    print("[plan] changed lengths", flush=True)
+    q, k, v, tables, seq_lens = _random_case(5, bsz, hkv, grp, d, bs, lens)
+    scale = d ** -0.5
+    dev = q.device
+    hip_decode(q, k, v, tables, seq_lens, scale, grp, plan=MX_PA_PLAN_WRITE)
+    torch.cuda.synchronize()
+    assert (workspace_error_flag(dev) & 8) == 0
+    shorter = seq_lens.clone()
+    shorter[0] -= 20  # still within the row's blocks: only the length check can catch it
+    hip_decode(q, k, v, tables, shorter, scale, grp, plan=MX_PA_PLAN_READ)
+    torch.cuda.synchronize()
+    assert workspace_error_flag(dev) & 8
+    out = hip_decode(q, k, v, tables, shorter, scale, grp)
+    _check(out, oracle_out(q, k, v, tables, shorter, scale, grp), "plain call after a mismatched plan")
+    # Clear the bit this test set on purpose, so later checks of the cached workspaces start clean.
+    from runtime_amd.phase2 import paged_attention_hip as pah
+    for key, ws in list(pah._workspaces.items()):
+        off = int(_hip.load().mx_paged_attn_error_offset(*key[1:]))
+        ws[off:off + 4].zero_()
+    torch.cuda.synchronize()
+    assert workspace_error_flag(dev) == 0
