@@ -379,22 +379,35 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     // The epilogue's per-channel scale and bias are loaded right after the pipeline's first
     // stages, so their round trip overlaps the main loop instead of following it (measured
     // 0.4-0.9 us per wave between the last k-tile and the stores when loaded in the epilogue).
-    // Out-of-range waves load the clamped tiles' values and store nothing. The gate||up SwiGLU
-    // instances and the wide ones (several n-tiles and m-tiles per wave) keep the loads in the
-    // epilogue: the extra registers made them spill (the SwiGLU ones at 32 rows under their
-    // occupancy bound), and their main loops are long.
-    // NJX instances load them raw with the weights and convert them after the MFMAs, behind a
-    // scheduling barrier: converted where they were loaded, the scheduler placed the conversion
-    // (and so a wait for the loads) at the kernel's start.
-    constexpr bool kEarly = NJX > 0 || (!GU && (NPW == 1 || MT == 1));
+    // Out-of-range waves load the clamped tiles' values and store nothing.
+    // - One n-tile or one m-tile per wave, not SwiGLU: converted to fp32 where they are loaded.
+    // - NJX instances, the gate||up SwiGLU ones and the wide ones of at most two m-tiles and four
+    //   n-tiles: loaded raw (16-bit values held through the loop) and converted after the MFMAs,
+    //   behind a scheduling barrier. Converted where they were loaded, the conversion (and so a
+    //   wait for the loads, which follow the first stages in the queue) went to the loop's start;
+    //   held as fp32 they made the SwiGLU instances spill.
+    // - The other wide instances (two n-tiles at two m-tiles, three or more m-tiles), which are at
+    //   or past their register budget, load them in the epilogue.
+    constexpr bool kFloatEarly = !GU && (NPW == 1 || MT == 1);
+    constexpr bool kRaw = NJX > 0 || (!kFloatEarly && (NPW == 1 || (MT <= 2 && NPW == 4)));
+    constexpr bool kEarly = kFloatEarly || kRaw;
     float sc_pre[NPW], bi_pre[NPW];
     uint16_t sc_raw[NPW], bi_raw[NPW];
+    auto convert_epilogue = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        const bool with_bias = gridDim.y == 1 && bias;
+#pragma unroll
+        for (int p = 0; p < NPW; ++p) {
+            sc_pre[p] = (float)__builtin_bit_cast(_Float16, sc_raw[p]);
+            bi_pre[p] = with_bias ? (float)__builtin_bit_cast(_Float16, bi_raw[p]) : 0.0f;
+        }
+    };
     auto load_epilogue = [&]() {
         if constexpr (!kEarly) return;
 #pragma unroll
         for (int p = 0; p < NPW; ++p) {
             const int64_t n = (int64_t)(nt_c + p) * kTileN + r;
-            if constexpr (NJX > 0) {  // unconditional loads (no bias: read the scale, use 0)
+            if constexpr (kRaw) {  // unconditional loads (no bias: read the scale, use 0)
                 sc_raw[p] = scale[n];
                 bi_raw[p] = ((gridDim.y == 1 && bias) ? bias : scale)[n];
             } else {
@@ -425,13 +438,6 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
 #pragma unroll
             for (int j = 0; j < NJX; ++j)
                 if (j < nj) compute(st[j]);
-            __builtin_amdgcn_sched_barrier(0);
-            const bool with_bias = gridDim.y == 1 && bias;
-#pragma unroll
-            for (int p = 0; p < NPW; ++p) {
-                sc_pre[p] = (float)__builtin_bit_cast(_Float16, sc_raw[p]);
-                bi_pre[p] = with_bias ? (float)__builtin_bit_cast(_Float16, bi_raw[p]) : 0.0f;
-            }
         } else {
             St st[P];
             PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), MX_NJX_HOOK)
@@ -439,6 +445,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     } else {
         load_epilogue();
     }
+    if constexpr (kRaw) convert_epilogue();
 #undef MX_NJX_HOOK
     const int N = NT * kTileN;
     if (GU) {
