@@ -37,17 +37,19 @@
 //   * keeps P tiles of K/V loads in flight and reads the piece's block ids
 //     with one vector load (a range never exceeds 64 tiles).
 // A piece that is a whole segment is written as fp16 output; otherwise its
-// partial goes to workspace slot w + s: (m, l) in fp32 and its own output
-// acc / l rounded to the element type (fp16 or bf16, half the bytes of the fp32
-// accumulator; the merge weights it by l again). Pairs (w, s)
-// that overlap form a monotone staircase, so w + s is unique and at most
-// W + B*Hkv - 1 slots exist. The workers holding a segment's first and last
-// tile record themselves in seg_w, so the merge needs no prefix sums.
+// partial, (m, l) in fp32 and its own output acc / l rounded to the element type
+// (fp16 or bf16, half the bytes of the fp32 accumulator; the merge weights it by
+// l again), goes to the segment's window of U slots: piece k of segment s (the
+// k-th worker that cuts it) to slot s*U + k, and pieces k >= U to an overflow
+// slot, B*Hkv*U + w (only a worker's first piece can have k >= 1, so one
+// overflow slot per worker suffices). The workers holding a segment's first and
+// last tile record themselves in seg_w.
 //
-// Kernel 2 (merge): one workgroup per segment reads its worker span, applies
-// the log-sum-exp merge of the partials and writes fp16 output (zeros for an
-// empty row). Each thread owns output elements and issues all of its loads
-// at once, so a merge costs two dependent memory round trips. The merge has a
+// Kernel 2 (merge): one workgroup per segment issues the loads of its lengths,
+// its worker span and its whole window of U slots at once, applies the
+// log-sum-exp merge of the partials and writes fp16 output (zeros for an empty
+// row): one memory round trip for a segment of at most U pieces, a second one
+// for the overflow slots of longer ones. The merge has a
 // launch of its own because handing partials between workgroups inside one
 // launch costs more on gfx950 than the launch: an agent-scope release/acquire
 // writes back and invalidates the XCD's L2 (measured 2.6x slower at the bench
@@ -83,8 +85,14 @@ struct Params {
     int workers;
     int wg_waves;     // waves per workgroup of the split launch (<= kWaves)
     int vg;           // virtual kv-heads per pool head (GQA groups above 8, see kv_virtual_groups)
-    int4* plan;       // [workers][64] tile plan: written by a MX_PA_PLAN_WRITE call, read by MX_PA_PLAN_READ
+    int4* plan;       // [workers][65] tile plan: written by a MX_PA_PLAN_WRITE call, read by MX_PA_PLAN_READ
+    int seg_slots;    // U: partial slots per segment window (the merge's batch)
 };
+
+// Slots per segment window, from the launch's workers and segments: 32 where segments are cut into
+// more than about 10 pieces on average, else 16 (the merge then loads a window in one batch).
+constexpr int seg_slots_for(int64_t workers, int64_t segs) { return workers > 10 * segs ? 32 : 16; }
+constexpr int kPlanStride = 65;  // tile plan entries per worker: 64 tiles and a header {k of the first piece}
 
 constexpr int kWaves = 4;               // waves per workgroup of the split launch (at most)
 constexpr int kSmallWorkers = 1024;     // up to this many workers the split launch uses 2-wave workgroups
@@ -511,15 +519,17 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
     const int worker = blockIdx.x * p.wg_waves + wave;
     const int g = lane >> 4, r = lane & 15;
 
-    // A finished piece: tiles [t0, t1) of segment (b, kvh), whose row has nt tiles. A whole
-    // segment writes the output; a cut one its partial at slot worker + segment.
-    auto finish = [&](int b, int kvh, int t0, int t1, int nt, float m_run, float l_run, const float4v (&acc)[DPL]) {
+    // A finished piece: tiles [t0, t1) of segment (b, kvh), whose row has nt tiles, the segment's
+    // k-th piece. A whole segment writes the output; a cut one its partial at slot seg*U + k of the
+    // segment's window, or at the worker's overflow slot for k >= U.
+    auto finish = [&](int b, int kvh, int t0, int t1, int nt, int64_t k, float m_run, float l_run,
+                      const float4v (&acc)[DPL]) {
         const int h0 = kvh * G;
         // Denominator of head r over the 4 lane groups; acc already sums all 16 tokens of a tile.
         l_run = xor_sum_16_32(l_run);
         const bool whole = t0 == 0 && t1 == nt;
         const int64_t seg = (int64_t)b * p.Hkv + kvh;
-        const int64_t slot = worker + seg;
+        const int64_t slot = k < p.seg_slots ? seg * p.seg_slots + k : (int64_t)p.B * p.Hkv * p.seg_slots + worker;
         if (lane == 0) {
             if (t0 == 0) p.seg_w[2 * seg] = worker;
             if (t1 == nt) p.seg_w[2 * seg + 1] = worker;
@@ -562,7 +572,8 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
         // Entries are checked before use, so a plan that does not match the call reads nothing
         // outside the pool, q or the workspace; such pieces (also those whose row length changed
         // since, checked after their loads) write nothing and set error bit 8.
-        const int4 e = p.plan[(int64_t)worker * 64 + lane];
+        const int4 e = p.plan[(int64_t)worker * kPlanStride + lane];
+        const int k_first = p.plan[(int64_t)worker * kPlanStride + 64].x;
         const bool live = e.y != -1;
         const int prev_y = __shfl_up(e.y, 1), prev_t = __shfl_up(e.z, 1);
         const bool start = live && (lane == 0 || e.y != prev_y || e.z != prev_t + 1);
@@ -577,8 +588,11 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
             const int t0 = __builtin_amdgcn_readlane(e.z, j0), s_eff = __builtin_amdgcn_readlane(e.w, j0);
             const int nj = j1 - j0;
             const int nt = (s_eff + kTile - 1) / kTile;
+            // Only a worker's first piece can start inside its segment (k = k_first); the others
+            // start their segments (k = 0).
+            const int k = t0 == 0 ? 0 : k_first;
             if (b >= p.B || kvh >= p.Hkv || t0 < 0 || nj <= 0 || s_eff < 0 || s_eff > p.max_blocks * BS ||
-                t0 + nj > nt) {
+                t0 + nj > nt || (t0 > 0 && (j0 != 0 || k < 1 || k > worker))) {
                 if (lane == 0) atomicOr(p.err, 8);
                 break;
             }
@@ -593,7 +607,7 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
                 if (lane == 0) atomicOr(p.err, 8);
                 continue;
             }
-            finish(b, kvh, t0, t0 + nj, nt, m_run, l_run, acc);
+            finish(b, kvh, t0, t0 + nj, nt, k, m_run, l_run, acc);
         }
         return;
     }
@@ -612,7 +626,7 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
     const int W = T < p.workers ? (int)T : p.workers;  // every worker gets >= 1 tile
     // MX_PA_PLAN_WRITE (block size >= 16): record every tile of the range for later calls; lanes
     // past the range (all of them for an idle worker) mark the end.
-    int4* const plan_w = (!PROBE && BPT == 1 && p.plan) ? p.plan + (int64_t)worker * 64 : nullptr;
+    int4* const plan_w = (!PROBE && BPT == 1 && p.plan) ? p.plan + (int64_t)worker * kPlanStride : nullptr;
     if (worker >= W) {
         if (plan_w) plan_w[lane] = int4{0, -1, 0, 0};
         return;
@@ -646,6 +660,15 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
             break;
         }
         int4* const plan_dst = plan_w ? plan_w + (x - x_first) : nullptr;
+        // The segment's k-th piece: 0 when the piece starts the segment; otherwise this worker
+        // minus the one holding the segment's first tile xs, floor(((xs + 1) W - 1) / T), the w
+        // with range_lo(w) <= xs < range_lo(w + 1).
+        int64_t k = 0;
+        if (t0 > 0) {
+            const int64_t xs = sg.row_start + (int64_t)kvh * nt;
+            k = worker - ((xs + 1) * W - 1) / T;
+        }
+        if (plan_w && x == x_first && lane == 0) plan_w[64] = int4{(int)k, 0, 0, 0};
         x += nj;
         int s_eff;
         if (one_pass) s_eff = __builtin_amdgcn_readlane(s_eff_lane, b);
@@ -654,21 +677,51 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
         float4v acc[DPL];
         run_piece<D, BS, G, STREAM, BF16, PROBE>(p, b, kvh, t0, nj, s_eff, lane, m_run, l_run, acc, 0, plan_dst);
         if constexpr (PROBE) continue;
-        finish(b, kvh, t0, t1, nt, m_run, l_run, acc);
+        finish(b, kvh, t0, t1, nt, k, m_run, l_run, acc);
     }
 }
 
 // Log-sum-exp merge of the partials of one (kv-head, sequence); zeros for an empty row.
-// Workers seg_w[s] .. seg_w[s + 1] cut segment s, each with a partial at slot w + s.
+// Workers seg_w[s] .. seg_w[s + 1] cut segment s; piece k's partial is at slot s*U + k of the
+// segment's window, or at overflow slot B*Hkv*U + seg_w[s] + k for k >= U.
 // Thread t owns 4 consecutive dims of one head (16-byte partial loads; m and l are shared
 // by the head's threads).
 template <int D, int G>
 constexpr int merge_threads() {
     return ((G * D / 4 + 63) / 64) * 64;
 }
-// U: partials loaded per memory round trip. 32 where segments are cut into more than about 10 pieces
-// on average (the launch picks it from workers / segments), so their longest segments still take one
-// round trip: Qwen2-0.5B shape (16 pieces on average, up to about 25), see the launch.
+
+// One batch of the online log-sum-exp: the UB pieces' (m, l) and normalised outputs, of which the
+// first cnt are real (the rest masked). Branch-free, so that loads issued before it are not
+// sunk behind anything.
+template <int UB, bool BF16>
+__device__ __forceinline__ void merge_step(const float (&mv)[UB], const float (&lv)[UB], const half4v (&av)[UB],
+                                           int cnt, float& mg, float& l, float4v& a) {
+    const float kNegInf = -__builtin_huge_valf();
+    float mc = kNegInf;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) mc = u < cnt ? fmaxf(mc, mv[u]) : mc;
+    const float mn = fmaxf(mg, mc);
+    const bool any = mn != kNegInf;  // false while every tile so far was skipped
+    const float r = any ? exp2f(mg - mn) : 1.0f;
+    l *= r;
+    a *= r;
+    // Masked slots may hold anything (an earlier call's pieces, NaN): their terms are selected
+    // away, never multiplied by 0.
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+        const bool v = u < cnt && any;
+        const float wgt = exp2f(mv[u] - mn) * lv[u];
+        l = v ? l + wgt : l;
+        const float4v o = {Elt<BF16>::widen(av[u][0]), Elt<BF16>::widen(av[u][1]), Elt<BF16>::widen(av[u][2]),
+                           Elt<BF16>::widen(av[u][3])};
+        const float4v t = a + wgt * o;  // the piece's output, normalised by its own l
+        a = v ? t : a;
+    }
+    mg = any ? mn : mg;
+}
+
+// U: slots per segment window and partials loaded per memory round trip (Params::seg_slots).
 template <int D, int BS, int G, bool BF16, int U = 16>
 __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     constexpr int Q = D / 4;  // 4-dim groups per head
@@ -677,59 +730,52 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(Params p) {
     const bool active = tid < G * Q;
     const int h = active ? tid / Q : 0, d = active ? (tid % Q) * 4 : 0;
     const int64_t s = (int64_t)b * p.Hkv + kvh;
+    // Every load of the common case goes out at once: the row's length, the segment's worker span
+    // and the segment's whole window (slots that hold no piece of this call are loaded and masked).
     int s_eff;
     const int nt = row_tiles<BS>(p, b, s_eff);
     const int w0 = p.seg_w[2 * s], w1 = p.seg_w[2 * s + 1];
-    _Float16* out = p.out + (int64_t)b * p.o_sb + (int64_t)(kvh * G + h) * p.o_sh + d;
-    if (nt == 0) {
-        if (active) *reinterpret_cast<half4v*>(out) = half4v{};
-        return;
+    float mv[U], lv[U];
+    half4v av[U];  // 16-bit until used: half the registers of fp32
+    {
+        const float* mlp = p.part_ml + ((s * U) * G + h) * 2;
+        const _Float16* accp = p.part_out + ((s * U) * G + h) * D + d;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            mv[u] = mlp[u * G * 2];
+            lv[u] = mlp[u * G * 2 + 1];
+            av[u] = *reinterpret_cast<const half4v*>(accp + u * G * D);
+        }
     }
-    if (w0 == w1) return;  // one worker held the whole segment and wrote the output
-    // One online pass over the pieces, U at a time: every load of a batch is issued before
-    // the first is used (indices clamped, values masked), so a segment cut by at most U
-    // workers needs one memory round trip.
-    const int np = w1 - w0 + 1;
+    // Keep the scheduler from interleaving the window's loads with the math below (it would
+    // issue the later ones only after the first ones are consumed).
+    __builtin_amdgcn_sched_barrier(0);
+    // Pieces of this call: none for an empty row or a segment one worker held whole (that worker
+    // wrote the output; nothing is stored here).
+    const bool whole = nt > 0 && w0 == w1;
+    const int np = (nt == 0 || whole || w1 < w0) ? 0 : w1 - w0 + 1;
     const float kNegInf = -__builtin_huge_valf();
-    const float* mlp = p.part_ml + (((int64_t)w0 + s) * G + h) * 2;
-    const _Float16* accp = p.part_out + (((int64_t)w0 + s) * G + h) * D + d;
     float mg = kNegInf, l = 0.0f;
     float4v a = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i0 = 0; i0 < np; i0 += U) {
-        float mv[U], lv[U];
-        float4v av[U];
+    merge_step<U, BF16>(mv, lv, av, np < U ? np : U, mg, l, a);
+    // Segments of more than U pieces: the rest from the overflow slots of their workers.
+    const int64_t ovf = (int64_t)p.B * p.Hkv * U;
+    for (int i0 = U; i0 < np; i0 += U) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t i = i0 + u < np ? i0 + u : np - 1;
-            mv[u] = mlp[i * G * 2];
-            lv[u] = mlp[i * G * 2 + 1];
-            const half4v hv = *reinterpret_cast<const half4v*>(accp + i * G * D);
-            av[u] = float4v{Elt<BF16>::widen(hv[0]), Elt<BF16>::widen(hv[1]), Elt<BF16>::widen(hv[2]),
-                            Elt<BF16>::widen(hv[3])};
+            const int64_t slot = ovf + w0 + i;
+            mv[u] = p.part_ml[(slot * G + h) * 2];
+            lv[u] = p.part_ml[(slot * G + h) * 2 + 1];
+            av[u] = *reinterpret_cast<const half4v*>(p.part_out + (slot * G + h) * D + d);
         }
-        float mc = kNegInf;
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (i0 + u < np) mc = fmaxf(mc, mv[u]);
-        const float mn = fmaxf(mg, mc);
-        if (mn == kNegInf) continue;  // only skipped tiles so far
-        const float r = exp2f(mg - mn);
-        l *= r;
-        a *= r;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (i0 + u < np) {
-                const float f = exp2f(mv[u] - mn);
-                l += f * lv[u];
-                a += (f * lv[u]) * av[u];  // the piece's output, normalised by its own l
-            }
-        }
-        mg = mn;
+        merge_step<U, BF16>(mv, lv, av, np - i0 < U ? np - i0 : U, mg, l, a);
     }
-    if (active) {
+    if (active && !whole) {
         half4v o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = Elt<BF16>::round(l > 0.0f ? a[e] / l : 0.0f);
+        _Float16* out = p.out + (int64_t)b * p.o_sb + (int64_t)(kvh * G + h) * p.o_sh + d;
         *reinterpret_cast<half4v*>(out) = o;
     }
 }
@@ -786,13 +832,15 @@ static Layout layout(int B, int Hq, int Hkv, int D, int max_blocks, int block_si
     Layout L{};
     L.workers = resolve_workers(chunk_tokens, B, Hkv, max_blocks, block_size);
     const int G = Hkv > 0 ? Hq / Hkv : 0;
-    const size_t slots = (size_t)L.workers + (size_t)B * Hkv;
+    // Segment windows (U slots each, U for the uncapped worker count: a launch that caps its
+    // workers never uses a larger U) and one overflow slot per worker.
+    const size_t slots = (size_t)B * Hkv * seg_slots_for(L.workers, (int64_t)B * Hkv) + (size_t)L.workers;
     L.err = 0;
     L.segw = 256;
     L.ml = L.segw + align256((size_t)B * Hkv * 2 * sizeof(int));
     L.acc = L.ml + align256(slots * G * 2 * sizeof(float));
     L.plan = L.acc + align256(slots * G * D * sizeof(uint16_t));
-    L.total = L.plan + (with_plan && block_size >= kTile ? align256((size_t)L.workers * 64 * sizeof(int4)) : 0);
+    L.total = L.plan + (with_plan && block_size >= kTile ? align256((size_t)L.workers * kPlanStride * sizeof(int4)) : 0);
     return L;
 }
 
@@ -827,11 +875,12 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     // 13.4-13.5 us per call on MI355X. With 2048 workers, 4-wave workgroups measured 56.0 us against
     // 56.3 (2 waves) and 57.3 (1 wave).
     prm.wg_waves = prm.workers <= kSmallWorkers ? 2 : kWaves;
+    prm.seg_slots = seg_slots_for(prm.workers, (int64_t)B * prm.Hkv);
     const int blocks = (int)ceil_div(prm.workers, prm.wg_waves);
     hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16, false, PLANNED>), dim3(blocks),
                        dim3(prm.wg_waves * 64), 0, st, prm);
     const int64_t segs = (int64_t)B * prm.Hkv;
-    if (prm.workers > 10 * segs)
+    if (seg_slots_for(prm.workers, segs) == 32)
         hipLaunchKernelGGL((decode_merge_kernel<D, BS, G, BF16, 32>), dim3(prm.Hkv, B), dim3(merge_threads<D, G>()), 0,
                            st, prm);
     else

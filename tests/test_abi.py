@@ -36,12 +36,13 @@ def test_paged_attn_workspace_layout_is_host_computable():
     small = lib.mx_paged_attn_workspace_bytes(4, 8, 2, 64, 8, 16, 0)
     big = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 256, 16, 256)
     assert 0 < small < big
-    # One partial per worker + segment slot (fp32 m, l and a 16-bit output of D per head, G heads):
-    # 65536 tiles at the table width in ranges of 16 tiles -> 4096 workers, + 256 segments.
-    # Block size 16 also holds the tile plan of MX_PA_PLAN_WRITE / MX_PA_PLAN_READ: 64 entries of
-    # 16 bytes per worker; block sizes 4 and 8 have none.
-    slots = 4096 + 256
-    plan = 4096 * 64 * 16
+    # Partial slots (fp32 m, l and a 16-bit output of D per head, G heads): a window of U per
+    # segment and one overflow slot per worker. 65536 tiles at the table width in ranges of 16
+    # tiles -> 4096 workers over 256 segments, more than 10 per segment -> U = 32.
+    # Block size 16 also holds the tile plan of MX_PA_PLAN_WRITE / MX_PA_PLAN_READ: 64 entries and
+    # a header of 16 bytes per worker; block sizes 4 and 8 have none.
+    slots = 256 * 32 + 4096
+    plan = 4096 * 65 * 16
     assert big >= slots * 4 * (2 * 4 + 128 * 2) + plan
     assert big < slots * 4 * (2 * 4 + 128 * 4) + plan  # half the bytes of an fp32 accumulator
     w8 = lib.mx_paged_attn_workspace_bytes(32, 32, 8, 128, 512, 8, 256)  # same tiles and workers, no plan
