@@ -190,7 +190,7 @@ int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_st
  * such divisor of G; each reads its pool head's K/V, so K/V bytes are read vg times).
  * The workspace holds the split partials (per piece: fp32 m and l, and its
  * output normalised by l in the element type), the tile plan (16 bytes per tile
- * slot, 64 slots per wave, block_size >= 16) and the error word; zero it once at
+ * slot, 64 slots and a header per wave, block_size >= 16) and the error word; zero it once at
  * allocation so the error word starts clear. Concurrent calls must not share
  * a workspace. out rows must be 16-byte aligned (o_sb, o_sh multiples of 8).
  * ------------------------------------------------------------------------- */
@@ -216,7 +216,7 @@ int mx_paged_attn_decode(const uint16_t* q, int64_t q_sb, int64_t q_sh, const ui
  * The split partials live in a static device array of
  * MX_PA_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
  * until the process ends; shapes whose workspace without the tile plan
- * (mx_paged_attn_workspace_bytes less 1 KiB per wave) exceeds it are refused
+ * (mx_paged_attn_workspace_bytes less 1040 bytes per wave) exceeds it are refused
  * with MX_ERR_WORKSPACE, and the plan flags with MX_ERR_INVALID. The call
  * allocates nothing.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
