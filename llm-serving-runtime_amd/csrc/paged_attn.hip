@@ -507,8 +507,12 @@ __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t
 // PROBE = true: the calibration instance of mx_kv_gather_probe. The same partition and the same
 // K/V loads, with the math replaced by an xor of the loaded words (nothing is written unless
 // that checksum hits a magic value), so its duration is the gather alone.
-template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false, bool PLANNED = false>
+// PLAN: 0 a plain call, 1 a plain call that also records the tile plan (MX_PA_PLAN_WRITE), 2 a call
+// that starts from the plan (MX_PA_PLAN_READ). The record's stores are in their own instance: in the
+// plain one they pushed the D = 128 instances past their register budget (4-6 VGPRs of spills).
+template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false, int PLAN = 0>
 __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
+    constexpr bool PLANNED = PLAN == 2;
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
     constexpr int BPT = BS >= kTile ? 1 : kTile / BS;  // KV blocks per tile (block sizes 4, 8)
     constexpr int kMaxRange = kMaxRangeTiles / BPT;    // tiles whose block ids fit one vector
@@ -626,7 +630,7 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
     const int W = T < p.workers ? (int)T : p.workers;  // every worker gets >= 1 tile
     // MX_PA_PLAN_WRITE (block size >= 16): record every tile of the range for later calls; lanes
     // past the range (all of them for an idle worker) mark the end.
-    int4* const plan_w = (!PROBE && BPT == 1 && p.plan) ? p.plan + (int64_t)worker * kPlanStride : nullptr;
+    int4* const plan_w = (PLAN == 1 && !PROBE && BPT == 1) ? p.plan + (int64_t)worker * kPlanStride : nullptr;
     if (worker >= W) {
         if (plan_w) plan_w[lane] = int4{0, -1, 0, 0};
         return;
@@ -636,16 +640,33 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
     const int64_t x_first = x;
     if (plan_w && lane >= hi - x_first) plan_w[lane] = int4{0, -1, 0, 0};
 
-    while (x < hi) {
-        Seg sg;
+    // The segment holding global tile xx, from the lengths read above (or read again past 64 rows).
+    auto seg_at = [&](int64_t xx) {
         if (one_pass) {
             const int excl = incl_lane - n_lane;
-            const bool le = lane < p.B && (int64_t)excl * p.Hkv <= x;
+            const bool le = lane < p.B && (int64_t)excl * p.Hkv <= xx;
             const int bl = __builtin_popcountll(__builtin_amdgcn_ballot_w64(le)) - 1;
-            sg = Seg{bl, __builtin_amdgcn_readlane(n_lane, bl), (int64_t)__builtin_amdgcn_readlane(excl, bl) * p.Hkv};
-        } else {
-            sg = locate<BS>(p, x, lane);
+            return Seg{bl, __builtin_amdgcn_readlane(n_lane, bl), (int64_t)__builtin_amdgcn_readlane(excl, bl) * p.Hkv};
         }
+        return locate<BS>(p, xx, lane);
+    };
+    // Index of the worker's first piece within its segment: 0 when the range starts a segment;
+    // otherwise this worker minus the one holding the segment's first tile xs,
+    // floor(((xs + 1) W - 1) / T), the w with range_lo(w) <= xs < range_lo(w + 1). Every later
+    // piece starts its segment (index 0). Computed here, so that T and W are not held through
+    // the pieces (that pushed the D = 128 instances into spills).
+    int k_first = 0;
+    if (!PROBE) {
+        const Seg s0 = seg_at(x_first);
+        if (s0.ntiles > 0) {
+            const int64_t t00 = (x_first - s0.row_start) % s0.ntiles;
+            if (t00 > 0) k_first = (int)(worker - ((x_first - t00 + 1) * W - 1) / T);
+        }
+        if (plan_w && lane == 0) plan_w[64] = int4{k_first, 0, 0, 0};
+    }
+
+    while (x < hi) {
+        const Seg sg = seg_at(x);
         const int b = sg.b, nt = sg.ntiles;
         if (nt <= 0) {  // cannot happen for x < T; stop rather than divide by zero
             atomicOr(p.err, 4);
@@ -660,15 +681,6 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
             break;
         }
         int4* const plan_dst = plan_w ? plan_w + (x - x_first) : nullptr;
-        // The segment's k-th piece: 0 when the piece starts the segment; otherwise this worker
-        // minus the one holding the segment's first tile xs, floor(((xs + 1) W - 1) / T), the w
-        // with range_lo(w) <= xs < range_lo(w + 1).
-        int64_t k = 0;
-        if (t0 > 0) {
-            const int64_t xs = sg.row_start + (int64_t)kvh * nt;
-            k = worker - ((xs + 1) * W - 1) / T;
-        }
-        if (plan_w && x == x_first && lane == 0) plan_w[64] = int4{(int)k, 0, 0, 0};
         x += nj;
         int s_eff;
         if (one_pass) s_eff = __builtin_amdgcn_readlane(s_eff_lane, b);
@@ -677,7 +689,7 @@ __global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WA
         float4v acc[DPL];
         run_piece<D, BS, G, STREAM, BF16, PROBE>(p, b, kvh, t0, nj, s_eff, lane, m_run, l_run, acc, 0, plan_dst);
         if constexpr (PROBE) continue;
-        finish(b, kvh, t0, t1, nt, k, m_run, l_run, acc);
+        finish(b, kvh, t0, t1, nt, t0 > 0 ? k_first : 0, m_run, l_run, acc);
     }
 }
 
@@ -862,7 +874,7 @@ static int resident_waves() {
     return cache[dev];
 }
 
-template <int D, int BS, int G, bool STREAM, bool BF16, bool PLANNED = false>
+template <int D, int BS, int G, bool STREAM, bool BF16, int PLAN = 0>
 static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     // The worker count comes from the plain instance, so a MX_PA_PLAN_READ call has exactly the
     // workers whose plans the MX_PA_PLAN_WRITE call recorded.
@@ -877,7 +889,7 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
     prm.wg_waves = prm.workers <= kSmallWorkers ? 2 : kWaves;
     prm.seg_slots = seg_slots_for(prm.workers, (int64_t)B * prm.Hkv);
     const int blocks = (int)ceil_div(prm.workers, prm.wg_waves);
-    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16, false, PLANNED>), dim3(blocks),
+    hipLaunchKernelGGL((decode_split_kernel<D, BS, G, STREAM, BF16, false, PLAN>), dim3(blocks),
                        dim3(prm.wg_waves * 64), 0, st, prm);
     const int64_t segs = (int64_t)B * prm.Hkv;
     if (seg_slots_for(prm.workers, segs) == 32)
@@ -888,48 +900,45 @@ static void launch(Params prm, int B, hipStream_t st, int64_t floor_workers) {
                            st, prm);
 }
 
-template <int D, int BS, bool STREAM, bool BF16>
-static bool dispatch_g(int G, bool planned, const Params& prm, int B, hipStream_t st, int64_t fw) {
-    if (planned) {  // plan reads: block sizes >= 16 with streaming loads only
-        if constexpr (BS >= kTile && STREAM) {
-            switch (G) {
-                case 1: launch<D, BS, 1, STREAM, BF16, true>(prm, B, st, fw); return true;
-                case 2: launch<D, BS, 2, STREAM, BF16, true>(prm, B, st, fw); return true;
-                case 3: launch<D, BS, 3, STREAM, BF16, true>(prm, B, st, fw); return true;
-                case 4: launch<D, BS, 4, STREAM, BF16, true>(prm, B, st, fw); return true;
-                case 5: launch<D, BS, 5, STREAM, BF16, true>(prm, B, st, fw); return true;
-                case 6: launch<D, BS, 6, STREAM, BF16, true>(prm, B, st, fw); return true;
-                case 7: launch<D, BS, 7, STREAM, BF16, true>(prm, B, st, fw); return true;
-                case 8: launch<D, BS, 8, STREAM, BF16, true>(prm, B, st, fw); return true;
-                default: return false;
-            }
-        }
-        return false;
-    }
+template <int D, int BS, bool STREAM, bool BF16, int PLAN>
+static bool dispatch_plan_g(int G, const Params& prm, int B, hipStream_t st, int64_t fw) {
     switch (G) {
-        case 1: launch<D, BS, 1, STREAM, BF16>(prm, B, st, fw); return true;
-        case 2: launch<D, BS, 2, STREAM, BF16>(prm, B, st, fw); return true;
-        case 3: launch<D, BS, 3, STREAM, BF16>(prm, B, st, fw); return true;
-        case 4: launch<D, BS, 4, STREAM, BF16>(prm, B, st, fw); return true;
-        case 5: launch<D, BS, 5, STREAM, BF16>(prm, B, st, fw); return true;
-        case 6: launch<D, BS, 6, STREAM, BF16>(prm, B, st, fw); return true;
-        case 7: launch<D, BS, 7, STREAM, BF16>(prm, B, st, fw); return true;
-        case 8: launch<D, BS, 8, STREAM, BF16>(prm, B, st, fw); return true;
+        case 1: launch<D, BS, 1, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
+        case 2: launch<D, BS, 2, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
+        case 3: launch<D, BS, 3, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
+        case 4: launch<D, BS, 4, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
+        case 5: launch<D, BS, 5, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
+        case 6: launch<D, BS, 6, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
+        case 7: launch<D, BS, 7, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
+        case 8: launch<D, BS, 8, STREAM, BF16, PLAN>(prm, B, st, fw); return true;
         default: return false;
     }
 }
 
+// plan: 0 plain, 1 record the tile plan, 2 start from it (block sizes >= 16, streaming loads only).
+template <int D, int BS, bool STREAM, bool BF16>
+static bool dispatch_g(int G, int plan, const Params& prm, int B, hipStream_t st, int64_t fw) {
+    if (plan != 0) {
+        if constexpr (BS >= kTile && STREAM) {
+            return plan == 1 ? dispatch_plan_g<D, BS, STREAM, BF16, 1>(G, prm, B, st, fw)
+                             : dispatch_plan_g<D, BS, STREAM, BF16, 2>(G, prm, B, st, fw);
+        }
+        return false;
+    }
+    return dispatch_plan_g<D, BS, STREAM, BF16, 0>(G, prm, B, st, fw);
+}
+
 template <bool STREAM, bool BF16>
-static bool dispatch_d_bs(int D, int BS, int G, bool planned, const Params& prm, int B, hipStream_t st, int64_t fw) {
+static bool dispatch_d_bs(int D, int BS, int G, int plan, const Params& prm, int B, hipStream_t st, int64_t fw) {
     switch (D * 100 + BS) {
-        case 12804: return dispatch_g<128, 4, STREAM, BF16>(G, planned, prm, B, st, fw);
-        case 12808: return dispatch_g<128, 8, STREAM, BF16>(G, planned, prm, B, st, fw);
-        case 12816: return dispatch_g<128, 16, STREAM, BF16>(G, planned, prm, B, st, fw);
-        case 12832: return dispatch_g<128, 32, STREAM, BF16>(G, planned, prm, B, st, fw);
-        case 6404: return dispatch_g<64, 4, STREAM, BF16>(G, planned, prm, B, st, fw);
-        case 6408: return dispatch_g<64, 8, STREAM, BF16>(G, planned, prm, B, st, fw);
-        case 6416: return dispatch_g<64, 16, STREAM, BF16>(G, planned, prm, B, st, fw);
-        case 6432: return dispatch_g<64, 32, STREAM, BF16>(G, planned, prm, B, st, fw);
+        case 12804: return dispatch_g<128, 4, STREAM, BF16>(G, plan, prm, B, st, fw);
+        case 12808: return dispatch_g<128, 8, STREAM, BF16>(G, plan, prm, B, st, fw);
+        case 12816: return dispatch_g<128, 16, STREAM, BF16>(G, plan, prm, B, st, fw);
+        case 12832: return dispatch_g<128, 32, STREAM, BF16>(G, plan, prm, B, st, fw);
+        case 6404: return dispatch_g<64, 4, STREAM, BF16>(G, plan, prm, B, st, fw);
+        case 6408: return dispatch_g<64, 8, STREAM, BF16>(G, plan, prm, B, st, fw);
+        case 6416: return dispatch_g<64, 16, STREAM, BF16>(G, plan, prm, B, st, fw);
+        case 6432: return dispatch_g<64, 32, STREAM, BF16>(G, plan, prm, B, st, fw);
         default: return false;
     }
 }
@@ -1082,14 +1091,15 @@ static int launch_decode(const char* what, Params prm, const Layout& L, char* ws
     // Fewest workers that keep every range within one vector of block ids.
     const int64_t fw = ceil_div((int64_t)B * Hkv * ceil_div((int64_t)max_blocks * block_size, kTile),
                                 max_range_tiles(block_size));
-    const bool shared = flags & MX_PA_SHARED_BLOCKS, bf16 = flags & MX_PA_BF16, planned = flags & MX_PA_PLAN_READ;
+    const bool shared = flags & MX_PA_SHARED_BLOCKS, bf16 = flags & MX_PA_BF16;
+    const int plan = (flags & MX_PA_PLAN_READ) ? 2 : ((flags & MX_PA_PLAN_WRITE) ? 1 : 0);
     bool ok;
     if (bf16)
-        ok = shared ? dispatch_d_bs<false, true>(D, block_size, G, planned, prm, B, st, fw)
-                    : dispatch_d_bs<true, true>(D, block_size, G, planned, prm, B, st, fw);
+        ok = shared ? dispatch_d_bs<false, true>(D, block_size, G, plan, prm, B, st, fw)
+                    : dispatch_d_bs<true, true>(D, block_size, G, plan, prm, B, st, fw);
     else
-        ok = shared ? dispatch_d_bs<false, false>(D, block_size, G, planned, prm, B, st, fw)
-                    : dispatch_d_bs<true, false>(D, block_size, G, planned, prm, B, st, fw);
+        ok = shared ? dispatch_d_bs<false, false>(D, block_size, G, plan, prm, B, st, fw)
+                    : dispatch_d_bs<true, false>(D, block_size, G, plan, prm, B, st, fw);
     if (!ok) return fail(MX_ERR_UNSUPPORTED, "%s: unsupported configuration", what);
     return check_launch(what);
 }
