@@ -471,6 +471,30 @@ def test_tile_plan_matches_plain_calls(bsz, hq, hkv, d, bs, dtype):
         _check(read2, oracle_out(q2, k2, v2, tables, seq_lens, scale, grp), "plan read vs oracle")
 
 
+@pytest.mark.parametrize("bsz,hq,hkv,d", [(8, 16, 4, 128), (16, 14, 2, 64)])
+def test_tile_plan_with_many_pieces_per_segment(monkeypatch, bsz, hq, hkv, d):
+    """Ranges of one 16-token tile (chunk_tokens 16): segments are cut into far more pieces than
+    a merge window holds, so workers' first pieces reach the overflow slots, with and without the
+    tile plan. Plain, recording and reading calls agree bit for bit and match the oracle."""
+    from runtime_amd.phase2 import paged_attention_hip as pah
+
+    monkeypatch.setattr(pah, "_CHUNK_TOKENS", 16)
+    grp = hq // hkv
+    g = torch.Generator().manual_seed(bsz + d)
+    lens = torch.randint(200, 1500, (bsz,), generator=g).tolist()
+    print(f"[plan] many pieces B={bsz} Hq={hq} Hkv={hkv} D={d}", flush=True)
+    q, k, v, tables, seq_lens = _random_case(17, bsz, hkv, grp, d, 16, lens)
+    scale = d ** -0.5
+    plain = pah._decode(q, k, v, tables, seq_lens, scale, grp)
+    rec = pah._decode(q, k, v, tables, seq_lens, scale, grp, plan=pah.MX_PA_PLAN_WRITE)
+    read = pah._decode(q, k, v, tables, seq_lens, scale, grp, plan=pah.MX_PA_PLAN_READ)
+    torch.cuda.synchronize()
+    assert torch.equal(rec.view(torch.int16), plain.view(torch.int16))
+    assert torch.equal(read.view(torch.int16), plain.view(torch.int16))
+    assert (workspace_error_flag(q.device) & 8) == 0
+    _check(plain, oracle_out(q, k, v, tables, seq_lens, scale, grp), "one-tile ranges vs oracle")
+
+
 def test_tile_plan_flags_changed_lengths():
     """A MX_PA_PLAN_READ call whose lengths differ from the recording call: the pieces of the rows
     that changed are dropped and error bit 8 is set; nothing is read outside the pool (every
