@@ -107,8 +107,8 @@ constexpr int kMinDefaultTiles = 4;     // default ranges are at least this long
 // Default workers per segment on average, but never fewer than one worker per CU. Measured on
 // the Qwen2-0.5B shape (B 16, 2 kv-heads, contexts U[512, 2048]) with the 4-dims-per-thread
 // merge: a cap of 8 pieces 14.4 us per call, 16 pieces 13.8 us, 32 pieces 15.3 us; re-measured
-// with the unrolled short pieces, the tile plan and the merge windows: 8 pieces 13.3 us, 12
-// 13.05 us, 16 12.85 us, 24 15.2 us. At the Llama-3-8B bench shape (2048 workers) and for the
+// with the unrolled short pieces (before the tile plan and the merge windows): 8 pieces 13.3 us,
+// 12 13.05 us, 16 12.85 us, 24 15.2 us. At the Llama-3-8B bench shape (2048 workers) and for the
 // 128-row batch (the range floor) the cap is not reached.
 constexpr int kPiecesPerSegment = 16;
 constexpr int kMinWorkers = 256;
