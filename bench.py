@@ -84,7 +84,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="REPS",
                     help="instead of the bench: REPS rounds of one kernel family's launches of the headline step "
                          "and a 1 GiB copy, for rocprofv3 --pmc passes (see --probe-family)")
-    ap.add_argument("--probe-family", choices=["attn", "linears"], default="attn")
+    ap.add_argument("--probe-family", choices=["attn", "linears", "sweep"], default="attn",
+                    help="attn / linears: the headline step's attention or its four projections; sweep: "
+                         "int8_linear alone on config 4's shapes (and config 1's at --batch 1) at M = --batch")
     ap.add_argument("--stream-shared-kv", action="store_true",
                     help="config 5: read the aliased K/V with streaming loads (no MX_PA_SHARED_BLOCKS)")
     args = ap.parse_args()
@@ -830,6 +832,8 @@ def traffic_probe(args) -> int:
     from runtime_amd.phase2.roofline import attention_hbm_bytes
 
     _hip.load()
+    if args.probe_family == "sweep":
+        return sweep_probe(args)
     shape = LLAMA3_8B if args.model == "llama3-8b" else QWEN2_05B
     headroom = args.warmup + args.steps + args.kernel_steps + 2  # the bench's table width
     d = Decoder(shape, args.batch, args.ctx_lo, args.ctx_hi, args.pool_blocks, headroom, layers=args.layers)
@@ -852,6 +856,50 @@ def traffic_probe(args) -> int:
     print(json.dumps({"probe": args.probe_family, "launches_per_family": args.traffic_probe * d.n_layers + d.n_layers,
                       "bytes_per_launch": {n: per_launch[n] for n in names}, "copy_bytes": COPY_PROBE_BYTES}),
           flush=True)
+    return 0
+
+
+def sweep_probe(args) -> int:
+    """Counter-pass probe of configs 1 and 4: ``int8_linear`` alone at M = ``--batch`` on each
+    Llama-3-8B projection (and config 1's 4096x4096 at M = 1), as ``config14_linears`` times it:
+    one warm-up round and REPS rounds over enough distinct weight copies (> 600 MB) that no launch
+    finds its weights in the 256 MB MALL, shape after shape, then the 1 GiB calibration copy. Every
+    call is one GEMV/GEMM dispatch, followed by a ``reduce_kernel`` dispatch where K is split; the
+    printed manifest gives the calls per shape in dispatch order."""
+    import torch
+
+    from runtime_amd.phase2.int8_linear import int8_linear, linear_splits, pack_weight, quantize_weight
+    from runtime_amd.phase2.roofline import linear_hbm_bytes
+
+    dev, m = torch.device("cuda:0"), args.batch
+    shapes = ([("config1", 4096, 4096)] if m == 1 else []) + [("qkv", 4096, 6144), ("o", 4096, 4096),
+                                                             ("gate_up", 4096, 28672), ("down", 14336, 4096)]
+    cases = []
+    seeds = {"config1": 0, "qkv": 1000, "o": 1001, "gate_up": 1002, "down": 1003}  # config14_linears' seeds
+    for name, k, n in shapes:
+        g = torch.Generator(device=dev).manual_seed(seeds[name])
+        copies = max(4, math.ceil(600e6 / (n * k)))
+        weights = []
+        for _ in range(copies):
+            q, sc = quantize_weight(torch.randn(n, k, generator=g, device=dev) * 0.02)
+            weights.append((pack_weight(q), sc))
+        x = torch.randn(m, k, generator=g, device=dev).half()
+        y = torch.empty(m, n, dtype=torch.float16, device=dev)
+        cases.append((name, n, k, weights, x, y))
+    torch.cuda.synchronize()
+    manifest = []
+    for name, n, k, weights, x, y in cases:
+        for _ in range(1 + args.traffic_probe):
+            for packed, sc in weights:
+                int8_linear(x, packed, sc, None, n, out=y)
+        manifest.append({"shape": name, "m": m, "n": n, "k": k, "calls": (1 + args.traffic_probe) * len(weights),
+                         "splits": linear_splits(m, n, k), "bytes_per_call": linear_hbm_bytes(m, n, k)})
+    src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "sweep", "m": m, "manifest": manifest, "copy_bytes": COPY_PROBE_BYTES}), flush=True)
     return 0
 
 

@@ -37,6 +37,8 @@ projection weight is detected.
 from __future__ import annotations
 
 import copy
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
@@ -75,25 +77,56 @@ def random_qwen2(seed: int = 0, **overrides):
     return _random_model(Qwen2ForCausalLM, Qwen2Config(**kwargs), seed)
 
 
-def random_llama(seed: int = 0, **overrides):
-    """A random-init ``LlamaForCausalLM`` (Llama-3-8B shape unless overridden), as :func:`random_qwen2`."""
+def random_llama(seed: int = 0, parallel: bool = False, **overrides):
+    """A random-init ``LlamaForCausalLM`` (Llama-3-8B shape unless overridden), as :func:`random_qwen2`.
+
+    ``parallel`` draws the weights from independent seeded streams on several threads (same
+    distributions, other values): the Llama-3-8B widths hold ~2 G parameters at 4 layers, a minute
+    of single-stream sampling.
+    """
     from transformers import LlamaConfig, LlamaForCausalLM
 
     kwargs = dict(LLAMA3_8B)
     kwargs.update(overrides)
-    return _random_model(LlamaForCausalLM, LlamaConfig(**kwargs), seed)
+    return _random_model(LlamaForCausalLM, LlamaConfig(**kwargs), seed, parallel=parallel)
 
 
-def _random_model(model_cls, config, seed: int):
+_CHUNK = 1 << 24  # elements per independent stream in the parallel fills
+
+
+def _workers() -> int:
+    return max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else 1))
+
+
+def _normal_parallel(shape, seq: np.random.SeedSequence, pool) -> np.ndarray:
+    """N(0, 1) float32 of ``shape`` from ``ceil(numel / _CHUNK)`` child streams of ``seq``, filled by ``pool``."""
+    out = np.empty(int(np.prod(shape)), np.float32)
+    n_chunks = max(1, -(-out.size // _CHUNK))
+    seqs = seq.spawn(n_chunks)
+
+    def fill(i):
+        np.random.Generator(np.random.PCG64(seqs[i])).standard_normal(
+            out=out[i * _CHUNK:(i + 1) * _CHUNK], dtype=np.float32)
+
+    list(pool.map(fill, range(n_chunks)))
+    return out.reshape(shape)
+
+
+def _random_model(model_cls, config, seed: int, parallel: bool = False):
     from transformers.initialization import no_init_weights
 
     config._attn_implementation = "eager"
     with no_init_weights():
         model = model_cls(config)
     rng = np.random.default_rng(seed)
-    with torch.no_grad():
-        for name, p in model.named_parameters():
-            noise = rng.standard_normal(p.shape, dtype=np.float32)
+    params = list(model.named_parameters())
+    seqs = np.random.SeedSequence(seed).spawn(len(params))
+    with torch.no_grad(), ThreadPoolExecutor(_workers()) as pool:
+        for (name, p), seq in zip(params, seqs):
+            if parallel:
+                noise = _normal_parallel(tuple(p.shape), seq, pool)
+            else:
+                noise = rng.standard_normal(p.shape, dtype=np.float32)
             if name.endswith("norm.weight"):
                 p.copy_(torch.from_numpy(1.0 + 0.05 * noise))
             else:
@@ -130,6 +163,21 @@ def margin_controlled_(model: nn.Module, embed_scale: float = 200.0, successor: 
     return perm
 
 
+def _dequantized(w: np.ndarray) -> np.ndarray:
+    """``dequantize(quantize_per_channel(w))``, computed over row blocks on several threads (the
+    format is per row, so the blocks give the whole matrix's values bit for bit)."""
+    out = np.empty(w.shape, np.float32)
+    step = max(16, -(-w.shape[0] // (4 * _workers())))
+
+    def one(lo):
+        q, s = quantize_per_channel(w[lo:lo + step])
+        out[lo:lo + step] = dequantize(q, s)
+
+    with ThreadPoolExecutor(_workers()) as pool:
+        list(pool.map(one, range(0, w.shape[0], step)))
+    return out
+
+
 def _round_fp16_(t: torch.Tensor) -> None:
     t.copy_(t.to(torch.float16).to(torch.float32))
 
@@ -142,8 +190,7 @@ def quantized_reference(model: nn.Module, targets: tuple[str, ...] = PROJECTIONS
         for parent in ref.modules():
             for name, child in parent.named_children():
                 if isinstance(child, nn.Linear) and name in targets:
-                    q, s = quantize_per_channel(child.weight.detach().numpy())
-                    child.weight.copy_(torch.from_numpy(dequantize(q, s)))
+                    child.weight.copy_(torch.from_numpy(_dequantized(child.weight.detach().numpy())))
                     projected.add(id(child.weight))
         for p in ref.parameters():
             if id(p) not in projected:
@@ -204,6 +251,31 @@ def prefill_kv(model: nn.Module, prompt: torch.Tensor, past=None
     out = model(input_ids=prompt[skip:].view(1, -1), past_key_values=cache, use_cache=True, logits_to_keep=1)
     kv = [(layer.keys[0], layer.values[0]) for layer in out.past_key_values.layers]
     return kv, out.logits[0, -1].float()
+
+
+@torch.no_grad()
+def continue_logits(model: nn.Module, kv: list[tuple[torch.Tensor, torch.Tensor]], tokens: torch.Tensor
+                    ) -> torch.Tensor:
+    """Logits ``[len(tokens), V]`` (fp32, on the CPU) of a forward over ``tokens`` continuing a context
+    whose per-layer keys and values ``kv`` (``[Hkv, S, D]``, keys after RoPE, as :func:`prefill_kv`
+    returns them or as a paged pool holds them) are given: ``tokens[i]`` sits at position ``S + i``
+    and row ``i`` is the distribution of the token after it.
+
+    This is the decode step's view of a context: the native step reads K/V from the pool whatever
+    wrote them, so a context of random K/V (the bench's) is checked by handing those same values
+    here. The cache is built in the model's own device and dtype, so an fp16 copy of the model on
+    the GPU gives the fp16 yardstick of the same continuation.
+    """
+    from transformers import DynamicCache
+
+    p = next(model.parameters())
+    cache = DynamicCache(config=model.config)
+    for li, (k, v) in enumerate(kv):
+        cache.update(k.to(device=p.device, dtype=p.dtype).unsqueeze(0),
+                     v.to(device=p.device, dtype=p.dtype).unsqueeze(0), li)
+    ids = tokens.reshape(1, -1).to(device=p.device, dtype=torch.long)
+    out = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=int(ids.shape[1]))
+    return out.logits[0].float().cpu()
 
 
 @torch.no_grad()

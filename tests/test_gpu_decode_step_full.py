@@ -1,0 +1,246 @@
+"""The native decode step (``Int8DecodeModel.step``) at the sizes ``bench.py`` times it.
+
+The reference's contract for its decode step is the tokens of the path it serves
+(``runtime/phase2/worker_server.py:733-794``: greedy argmax of one batched forward;
+``tests/test_cuda_graph_decode.py:88-103``: graph replay tokens equal eager ones). Here the
+served path is the one the bench times: one eager step, then a HIP graph of the whole step
+captured once and replayed, attention at layer 0 recording the tile plan and every later
+layer reading it (``Int8DecodeModel.attn_plan``, on by default at block size 16), the fused
+qkv + RoPE + append, split-K consumers, the gate||up SwiGLU epilogue, int8 lm_head and the
+device argmax.
+
+Cases:
+
+* config 3 at full size: Qwen2-0.5B dims, 24 layers, vocabulary 151936, 16 rows, prompts
+  U[512, 2048] whose K/V the fp32 oracle computes (``oracle.model.prefill_kv``) and writes into
+  the pool, 64 greedy steps; once with plain random weights, once with the margin-controlled
+  init (``oracle.model.margin_controlled_``) where the north star's bar applies: every token
+  identical to the oracle's;
+* the headline: Llama-3-8B dims at batch 32 with the bench's own inputs: contexts U[128, 4096]
+  and block tables from ``make_contexts(32, 128, 4096, 16, 16384, seed=0)`` (the bench's call;
+  the lengths are the bench's, the tables hold 65 steps of headroom where the bench's hold 33),
+  a 16384-block pool of N(0, 1) K/V, vocabulary 128256, 64 steps from seeded random tokens. The
+  layer count is 4 (the bench's 32 only repeat the same launches over other weights) so that the
+  CPU oracle finishes in about a minute.
+
+Oracle: the HF model in fp32 on the CPU holding exactly the device weights
+(``oracle.model.quantized_reference``), continued from each row's K/V as the pool holds them
+(``oracle.model.continue_logits``) and teacher-forced on the native tokens, so every step of
+every row is compared on the same prefix. Yardstick: the same weights in torch fp16 on the GPU,
+continued from the same fp16 K/V the same way.
+
+Rules, as in the greedy-decode tests: per row ``max|dL| <= max(1e-2, 1.25 x torch fp16's
+error)``; a token that is not the oracle's argmax only where the oracle's top-1 gap is below
+twice that bar (a near tie that fp16 activations break either way), at most 2 % of all steps.
+Each test reports rows with every token identical, flips and errors (``ParityReport``).
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+
+import pytest
+import torch
+
+from conftest import report
+from oracle import glue as og
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+LOGIT_ATOL = 1e-2
+YARDSTICK_SLACK = 1.25
+MAX_TIE_FRACTION = 0.02
+MARGIN_MULTIPLE = 10.0
+BLOCK_SIZE = 16
+STEPS = 64
+
+
+def _drive(native, pool, tables_d, seq_lens, tokens):
+    """STEPS steps as bench.py runs them: one eager step, then a captured step graph replayed.
+    ``tokens`` holds each step's input and receives its output in place. Returns the input tokens
+    ``[B, STEPS]`` and the logits ``[B, STEPS, V]`` (fp16, CPU) of every step."""
+    assert native.attn_plan and pool.block_size_tokens >= 16, "the tile plan must be on, as in the bench"
+    seen_tokens, seen_logits = [tokens.cpu()], []
+    _, logits = native.step(tokens, pool, tables_d, seq_lens, return_logits=True, out=tokens)
+    seen_logits.append(logits.cpu())
+    seen_tokens.append(tokens.cpu())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _, logits_g = native.step(tokens, pool, tables_d, seq_lens, return_logits=True, out=tokens)
+    for _ in range(STEPS - 1):
+        graph.replay()
+        seen_logits.append(logits_g.cpu())
+        seen_tokens.append(tokens.cpu())
+    assert native.error_flag() == 0
+    return torch.stack(seen_tokens[:-1], dim=1), torch.stack(seen_logits, dim=1), torch.stack(seen_tokens[1:], dim=1)
+
+
+def _compare(ref, torch16, kv_rows, inputs, outputs, logits, label):
+    """Per row: oracle and yardstick continued from the row's K/V over its input tokens."""
+    results = []
+    for b, kv in enumerate(kv_rows):
+        ref_logits = om.continue_logits(ref, kv, inputs[b])
+        t16 = om.continue_logits(torch16, kv, inputs[b])
+        mine = logits[b].float()
+        err = float((mine - ref_logits).abs().max())
+        err16 = float((t16 - ref_logits).abs().max())
+        allowed = max(LOGIT_ATOL, YARDSTICK_SLACK * err16)
+        agree = om.greedy_agreement(ref_logits, outputs[b], tie_tol=2 * allowed)
+        top2 = ref_logits.topk(2, dim=-1).values
+        agree["min_margin"] = float((top2[:, 0] - top2[:, 1]).min())
+        yard = int((t16.argmax(dim=-1) != ref_logits.argmax(dim=-1)).sum())
+        results.append(dict(row=b, ctx=int(kv[0][0].shape[1]), err=err, err16=err16, allowed=allowed, yard=yard,
+                            **agree))
+        print(f"[{label}] row {b} ctx {results[-1]['ctx']}: max|dL| native {err:.3e} torch16 {err16:.3e}, "
+              f"mismatches {agree['mismatches']}/{agree['steps']} (torch16 {yard}), "
+              f"min oracle margin {agree['min_margin']:.3e}", flush=True)
+    return results
+
+
+def _summary(results, label):
+    steps = sum(r["steps"] for r in results)
+    flips = sum(r["mismatches"] for r in results)
+    identical = sum(r["mismatches"] == 0 for r in results)
+    return (f"[{label}] {identical}/{len(results)} rows with all {STEPS} tokens identical, {flips} near-tie flips "
+            f"in {steps} steps (torch fp16 {sum(r['yard'] for r in results)}), largest logit error "
+            f"{max(r['err'] for r in results):.3e} (torch fp16 {max(r['err16'] for r in results):.3e}), smallest "
+            f"oracle top-1 margin {min(r['min_margin'] for r in results):.3e}")
+
+
+def _check_tolerance(results, label):
+    summary = _summary(results, label)
+    for r in results:
+        assert r["err"] <= r["allowed"], f"row {r['row']}: logits off by {r['err']:.3e} (allowed " \
+                                         f"{r['allowed']:.3e}); {summary}"
+        assert r["ties_ok"], f"row {r['row']}: a mismatch outside the near-tie band {r}; {summary}"
+    assert sum(r["mismatches"] for r in results) <= MAX_TIE_FRACTION * sum(r["steps"] for r in results), summary
+    report(summary)
+
+
+def _config3(margin: bool):
+    from runtime_amd.phase2.decode_step import Int8DecodeModel
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    hf = om.random_qwen2(seed=0)
+    if margin:
+        om.margin_controlled_(hf, seed=0)
+    cfg = hf.config
+    assert (cfg.num_hidden_layers, cfg.vocab_size, cfg.hidden_size) == (24, 151936, 896)
+    ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
+    torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
+    native = Int8DecodeModel.from_hf(hf, device=DEV)
+    del hf
+    s = native.shape
+    batch = 16
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 2048 + 1, (batch,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g) for n in lens]
+    need = [math.ceil((n + STEPS + 1) / BLOCK_SIZE) for n in lens]
+    nb = sum(need) + 64
+    perm = torch.randperm(nb, generator=g)
+    tables = torch.zeros(batch, max(need), dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = perm[at:at + n].to(torch.int32)
+        at += n
+    print(f"[config3 native] margin={margin} prefill of {batch} prompts {min(lens)}..{max(lens)} on the CPU",
+          flush=True)
+    pool_k = torch.zeros(nb, s.layers, s.kv_heads, BLOCK_SIZE, s.head_dim, dtype=torch.float16)
+    pool_v = torch.zeros_like(pool_k)
+    kv_rows, first = [], []
+    for b, prompt in enumerate(prompts):
+        kv, last = om.prefill_kv(ref, prompt)
+        first.append(int(last.argmax()))
+        # The pool holds fp16; the oracle continues from exactly those values.
+        kv16 = [(k.half(), v.half()) for k, v in kv]
+        kv_rows.append([(k.float(), v.float()) for k, v in kv16])
+        for li, (k, v) in enumerate(kv16):
+            assert og.append_tokens(pool_k[:, li], pool_v[:, li], tables[b:b + 1], [0], k.unsqueeze(0),
+                                    v.unsqueeze(0)) == []
+    pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=BLOCK_SIZE, num_layers=s.layers, num_kv_heads=s.kv_heads,
+                          head_dim=s.head_dim, dtype=torch.float16, device=DEV)
+    pool._ensure_pools()
+    for li in range(s.layers):
+        pool.k_layer_view(li).copy_(pool_k[:, li])
+        pool.v_layer_view(li).copy_(pool_v[:, li])
+    del pool_k, pool_v
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    tokens = torch.tensor(first, dtype=torch.int64, device=DEV)
+    print(f"[config3 native] margin={margin} {STEPS} steps, 24 layers, graph replay with the tile plan", flush=True)
+    inputs, logits, outputs = _drive(native, pool, tables.to(DEV), seq_lens, tokens)
+    assert seq_lens.cpu().tolist() == [n + STEPS for n in lens]
+    return _compare(ref, torch16, kv_rows, inputs, outputs, logits, f"config3 native, margin={margin}")
+
+
+@pytest.mark.timeout(1200)
+def test_native_step_config3_full_size():
+    _check_tolerance(_config3(margin=False), "config3 native step")
+
+
+@pytest.mark.timeout(1200)
+def test_native_step_config3_full_size_margin_controlled_identical_tokens():
+    """The north star's bar on the path the bench times: every one of the 64 greedy tokens of
+    every row equals the oracle's, with the oracle's top-1 margin at least MARGIN_MULTIPLE times
+    the largest logit error (both measured here and printed)."""
+    results = _config3(margin=True)
+    summary = _summary(results, "config3 native step, margin-controlled")
+    max_err = max(r["err"] for r in results)
+    min_margin = min(r["min_margin"] for r in results)
+    for r in results:
+        assert r["err"] <= r["allowed"], f"row {r['row']}: logits off by {r['err']:.3e}; {summary}"
+    assert min_margin >= MARGIN_MULTIPLE * max_err, f"margin premise broken: {summary}"
+    assert sum(r["mismatches"] for r in results) == 0, summary
+    report(f"{summary} (margin / error {min_margin / max_err:.1f})")
+
+
+@pytest.mark.timeout(1200)
+def test_native_step_llama3_b32_bench_inputs():
+    from runtime_amd.phase2.decode_step import Int8DecodeModel, make_contexts
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    layers, batch, pool_blocks = 4, 32, 16384
+    print(f"[llama native] building the {layers}-layer Llama-3-8B-dims model (vocab 128256) on the CPU", flush=True)
+    hf = om.random_llama(seed=0, parallel=True, num_hidden_layers=layers)
+    cfg = hf.config
+    assert (cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_key_value_heads) == (4096, 14336,
+                                                                                                 128256, 8)
+    ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
+    native = Int8DecodeModel.from_hf(hf, device=DEV)
+    del hf
+    torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
+    s = native.shape
+    lens, tables = make_contexts(batch, 128, 4096, BLOCK_SIZE, pool_blocks, headroom=STEPS + 1, seed=0)
+    lens = lens.tolist()
+    # The bench's pool: every block of every layer N(0, 1) fp16, generated on the host here so the
+    # oracle reads the same values.
+    g = torch.Generator().manual_seed(1)
+    pool = GpuKVBlockPool(num_blocks=pool_blocks, block_size_tokens=BLOCK_SIZE, num_layers=layers,
+                          num_kv_heads=s.kv_heads, head_dim=s.head_dim, dtype=torch.float16, device=DEV)
+    pool._ensure_pools()
+    ctx = {}  # (layer, "k" | "v") -> per row [Hkv, S, D] fp32, gathered from the host copy
+    for li in range(layers):
+        for name, view in (("k", pool.k_layer_view(li)), ("v", pool.v_layer_view(li))):
+            host = torch.randn(view.shape, generator=g).half()
+            view.copy_(host)
+            ctx[li, name] = []
+            for b in range(batch):
+                blocks = host[tables[b, :math.ceil(lens[b] / BLOCK_SIZE)].long()]   # [nblk, Hkv, bs, D]
+                row = blocks.permute(1, 0, 2, 3).reshape(s.kv_heads, -1, s.head_dim)[:, :lens[b]]
+                ctx[li, name].append(row.float())
+            del host
+    kv_rows = [[(ctx[li, "k"][b], ctx[li, "v"][b]) for li in range(layers)] for b in range(batch)]
+    del ctx
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    tokens = torch.randint(0, cfg.vocab_size, (batch,), generator=torch.Generator().manual_seed(2)).to(DEV)
+    print(f"[llama native] {STEPS} steps, batch {batch}, contexts {min(lens)}..{max(lens)}, graph replay with the "
+          f"tile plan", flush=True)
+    inputs, logits, outputs = _drive(native, pool, tables.to(DEV), seq_lens, tokens)
+    assert seq_lens.cpu().tolist() == [n + STEPS for n in lens]
+    del pool
+    torch.cuda.empty_cache()
+    _check_tolerance(_compare(ref, torch16, kv_rows, inputs, outputs, logits, "llama3 native"),
+                     "llama3-8b dims native step, batch 32, bench contexts")

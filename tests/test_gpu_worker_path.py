@@ -143,17 +143,21 @@ def test_worker_persistent_slots_and_single_row_decode():
 
 @pytest.mark.timeout(600)
 def test_hip_graph_decode_matches_eager():
+    """Five rows for ``steps`` steps, then row 2 finishes and four rows decode ``tail`` more steps:
+    one graph per (rows, table width), each warming up eagerly, then captured and replayed. Tokens
+    and logits equal eager decoding over the same sequence, and every request's batch-1 cache ends
+    at its own length."""
     from runtime_amd.phase2.hf_decode import PagedDecoder
     from runtime_amd.phase2.hip_graph_decode import CudaGraphDecodeManager
 
     model, _, _ = _model(seed=22)
     g = torch.Generator().manual_seed(22)
-    # The longest row needs exactly 16 blocks, the power of two the graph bucket rounds the table
-    # width to, so eager and graph decode launch attention with the same table width (and split).
+    # The longest row needs 16 blocks: the persistent cache's table width, which both the eager
+    # dense step and the graph (keyed by that width) hand to attention.
     lens = [30, 100, 245, 57, 180]
     prompts = [torch.randint(0, 32768, (n,), generator=g) for n in lens]
-    steps = 10
-    need = [math.ceil((n + steps + 1) / BS) for n in lens]
+    steps, tail = 10, 5
+    need = [math.ceil((n + steps + tail + 1) / BS) for n in lens]
     assert max(need) == 16
     rows, at = [], 0
     for n in need:
@@ -169,17 +173,27 @@ def test_hip_graph_decode_matches_eager():
         for _ in range(steps):
             dec.decode_step(states)
             logits.append(dec.last_logits.float().cpu().clone())
-        runs[mode] = ([s.generated_token_ids for s in states], torch.stack(logits), mgr)
+        done = states.pop(2)
+        dec.release(done.req.request_id)
+        for _ in range(tail):
+            dec.decode_step(states)
+            logits.append(dec.last_logits.float().cpu().clone().view(-1))
+        lengths = [s.past_key_values.get_seq_length() for s in states]
+        assert lengths == [lens[i] + steps + tail for i in (0, 1, 3, 4)], lengths
+        runs[mode] = ([s.generated_token_ids for s in states + [done]], logits, mgr)
     mgr = runs["graph"][2]
     stats = mgr.stats()
-    assert not stats["disabled"], stats["disable_reason"]
-    (bucket,) = stats["buckets"]
-    assert bucket["captured"] and bucket["replays"] == steps - 2, stats
+    assert not stats["off_reason"], stats
+    five, four = stats["graphs"]
+    # Two eager warm-up steps each, then one capture + replay and a replay per later step.
+    assert (five["rows"], five["width"], four["rows"], four["width"]) == (5, 16, 4, 16), stats
+    assert five["state"] == "captured" and five["eager_steps"] == 2 and five["replays"] == steps - 2, stats
+    assert four["state"] == "captured" and four["eager_steps"] == 2 and four["replays"] == tail - 2, stats
     assert runs["graph"][0] == runs["eager"][0], "graph replay tokens differ from eager decode"
-    diff = float((runs["graph"][1] - runs["eager"][1]).abs().max())
+    diff = max(float((a.view(-1) - b.view(-1)).abs().max()) for a, b in zip(runs["graph"][1], runs["eager"][1]))
     assert diff <= 1e-3, f"graph vs eager logits differ by {diff:.3e}"
-    report(f"[hip graph] {len(lens)} rows x {steps} steps: tokens identical to eager, max |dlogits| {diff:.2e}, "
-           f"{bucket['replays']} replays of one captured step")
+    report(f"[hip graph] 5 rows x {steps} steps then 4 rows x {tail}: tokens identical to eager, max |dlogits| "
+           f"{diff:.2e}, {five['replays']} + {four['replays']} replays of two captured steps")
 
 
 def test_kv_write_overrun_raises_at_check():

@@ -127,3 +127,47 @@ def test_margin_controlled_init_pins():
     _, plain_logits = om.greedy_reference(plain, prompt, steps=24)
     plain_top2 = plain_logits.topk(2, dim=-1).values
     assert float((top2[:, 0] - top2[:, 1]).min()) > 10 * float((plain_top2[:, 0] - plain_top2[:, 1]).min())
+
+
+def test_continue_logits_from_given_kv(tiny_pair):
+    """continue_logits over a context's K/V equals teacher forcing over the whole sequence; K/V one
+    token short (positions shifted) or from the wrong layers are caught."""
+    _, ref = tiny_pair
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, TINY["vocab_size"], (41,), generator=g)
+    tokens, _ = om.greedy_reference(ref, prompt, steps=8)
+    full = om.teacher_forced_logits(ref, prompt, tokens)
+    kv, last = om.prefill_kv(ref, prompt)
+    torch.testing.assert_close(last, full[0], atol=1e-4, rtol=1e-4)
+    cont = om.continue_logits(ref, kv, tokens[:-1])
+    assert cont.shape == (8, TINY["vocab_size"])
+    torch.testing.assert_close(cont, full[1:], atol=1e-4, rtol=1e-4)
+    short = [(k[:, :-1], v[:, :-1]) for k, v in kv]
+    assert (om.continue_logits(ref, short, tokens[:-1]) - full[1:]).abs().max() > 1e-2
+    # The layers' K/V handed over in the wrong order (a layer-index slip in a layer-major pool).
+    swapped = [kv[1], kv[0]]
+    assert (om.continue_logits(ref, swapped, tokens[:-1]) - full[1:]).abs().max() > 1e-2
+    # The given tensors are not modified.
+    kv2, _ = om.prefill_kv(ref, prompt)
+    for (k, v), (k2, v2) in zip(kv, kv2):
+        assert torch.equal(k, k2) and torch.equal(v, v2)
+
+
+def test_parallel_init_is_seeded_and_distributed():
+    """random_llama(parallel=True): the same seed gives the same weights, another seed other ones,
+    and the draws have the stated distributions (matrices N(0, 0.02), norms 1 + N(0, 0.05))."""
+    small = dict(hidden_size=256, num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+                 intermediate_size=512, vocab_size=70000)  # embedding of 17.9 M elements: two streams
+    a = om.random_llama(seed=7, parallel=True, **small)
+    b = om.random_llama(seed=7, parallel=True, **small)
+    c = om.random_llama(seed=8, parallel=True, **small)
+    for (name, pa), (_, pb), (_, pc) in zip(a.named_parameters(), b.named_parameters(), c.named_parameters()):
+        assert torch.equal(pa, pb), name
+        assert not torch.equal(pa, pc), name
+    emb = a.model.embed_tokens.weight.detach()
+    assert abs(float(emb.std()) - 0.02) < 2e-4 and abs(float(emb.mean())) < 1e-4
+    # The two streams of the embedding are independent draws, not one stream repeated.
+    flat = emb.reshape(-1)
+    assert not torch.equal(flat[:1000], flat[1 << 24:(1 << 24) + 1000])
+    norm = a.model.layers[0].input_layernorm.weight.detach()
+    assert abs(float(norm.mean()) - 1.0) < 0.02 and abs(float(norm.std()) - 0.05) < 0.01
