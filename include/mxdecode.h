@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 14
+#define MX_ABI_VERSION 15
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -293,30 +293,33 @@ int mx_kv_append(const uint16_t* k_new, const uint16_t* v_new, int64_t new_sb, i
  * followed by BlockPagedBatchLayer.update's write (paged_kv_cache.py:121-157).
  * A position outside the table writes q = 0 and no K/V. lens_out (optional,
  * int32 [B]) receives positions[b] + 1, the KV length the attention call of
- * this token reads (seq_lens in paged_attention_triton.py:43-50). */
+ * this token reads (seq_lens in paged_attention_triton.py:43-50). used_blocks
+ * (nullable) is marked as by mx_kv_append. */
 int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
                        const float* rope, int32_t max_pos, const int32_t* positions, uint16_t* q_out,
                        int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
                        const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, int32_t block_size,
-                       int32_t num_pool_blocks, int32_t* err, int32_t* lens_out, void* stream);
+                       int32_t num_pool_blocks, int32_t* err, int32_t* lens_out, uint8_t* used_blocks,
+                       void* stream);
 
 /* mx_qkv_rope_append with the QKV projection given as split-K partials
  * (fp32 [splits][B][(Hq + 2*Hkv) * D], from mx_w8a16_linear_partials): each
  * element is fp16(sum over splits + bias), the value mx_w8a16_linear would
- * have written, then rotated and appended as above. bias may be NULL. */
+ * have written, then rotated and appended as above. bias may be NULL;
+ * partials and bias need 16-byte alignment. */
 int mx_qkv_rope_append_splits(const float* partials, int32_t splits, const uint16_t* bias, int32_t B, int32_t Hq,
                               int32_t Hkv, int32_t D, const float* rope, int32_t max_pos, const int32_t* positions,
                               uint16_t* q_out, int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk,
                               int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
                               int32_t block_size, int32_t num_pool_blocks, int32_t* err, int32_t* lens_out,
-                              void* stream);
+                              uint8_t* used_blocks, void* stream);
 
 /* The QKV projection and mx_qkv_rope_append_splits in one launch, for the
  * decode step's first two kernels per layer: q = the rotated q heads of
  * x[M, K] W^T (+ bias) (W the packed fused-QKV weight, N = (Hq + 2*Hkv) * D
  * rows in the order q, k, v), k rotated and v appended at position
  * positions[m], with everything else (q_out layout, pool slots, errors,
- * lens_out) as in mx_qkv_rope_append. The result is bit for bit that of
+ * lens_out, used_blocks) as in mx_qkv_rope_append. The result is bit for bit that of
  * mx_w8a16_linear_partials followed by mx_qkv_rope_append_splits whenever
  * mx_w8a16_splits(M, N, K) == 8 (the decode step's qkv at 5 <= M <= 32 on the
  * Llama-3-8B shape): each of the kernel's 8 waves accumulates one of those
@@ -329,7 +332,8 @@ int mx_w8a16_qkv_rope_append(const uint16_t* x, int64_t M, int64_t K, int64_t x_
                              const float* rope, int32_t max_pos, const int32_t* positions, uint16_t* q_out,
                              int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
                              const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, int32_t block_size,
-                             int32_t num_pool_blocks, int32_t* err, int32_t* lens_out, void* stream);
+                             int32_t num_pool_blocks, int32_t* err, int32_t* lens_out, uint8_t* used_blocks,
+                             void* stream);
 
 /* h = residual ? fp16(x + residual) : x;  residual_out (if not NULL) = h;
  * out = fp16(fp16(h * rsqrt(mean(h^2) + eps)) * weight), per row of H

@@ -123,6 +123,7 @@ struct RopeAppendParams {
     int max_blocks, bs, num_pool_blocks;
     int32_t* err;
     int32_t* lens_out;  // optional: lens_out[b] = positions[b] + 1 (the attention length)
+    uint8_t* used;      // optional [num_pool_blocks] map: 1 where a token was written
 };
 
 // Rotate-half RoPE (pairs i and i + D/2 share frequency i) on the q and k heads of one
@@ -189,6 +190,7 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_append_kernel(RopeAppendPar
         }
         *reinterpret_cast<uint2*>(p.k_pool + dst + j) = __builtin_bit_cast(uint2, o1);
         *reinterpret_cast<uint2*>(p.k_pool + dst + half + j) = __builtin_bit_cast(uint2, o2);
+        if (p.used && c == 0 && hs == p.Hq) p.used[p.bt[(int64_t)b * p.bt_sb + pos / p.bs]] = 1;
         return;
     }
     if (pos >= p.max_pos) return;  // flagged by the q/k threads of the row
@@ -611,7 +613,7 @@ extern "C" int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32
                                   uint16_t* q_out, int64_t q_stride, uint16_t* k_pool, uint16_t* v_pool,
                                   int64_t kv_sblk, int64_t kv_shead, const int32_t* block_tables, int64_t bt_sb,
                                   int32_t max_blocks, int32_t block_size, int32_t num_pool_blocks, int32_t* err,
-                                  int32_t* lens_out, void* stream) {
+                                  int32_t* lens_out, uint8_t* used_blocks, void* stream) {
     clear_error();
     if (B > 0 && !qkv) return fail(MX_ERR_NULL, "mx_qkv_rope_append: null pointer");
     if (B > 0 && (qkv_stride % 8 || !glue::a16(qkv)))
@@ -621,7 +623,7 @@ extern "C" int mx_qkv_rope_append(const uint16_t* qkv, int64_t qkv_stride, int32
     glue::RopeAppendParams p{qkv, qkv_stride, nullptr, 0, 0, nullptr, Hq, Hkv, D,
                              reinterpret_cast<const float2*>(rope), max_pos, positions, q_out, q_stride, k_pool,
                              v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, block_size, num_pool_blocks,
-                             err, lens_out};
+                             err, lens_out, used_blocks};
     return rope_append_common("mx_qkv_rope_append", p, B, stream);
 }
 
@@ -631,17 +633,18 @@ extern "C" int mx_qkv_rope_append_splits(const float* partials, int32_t splits, 
                                          uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
                                          const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
                                          int32_t block_size, int32_t num_pool_blocks, int32_t* err,
-                                         int32_t* lens_out, void* stream) {
+                                         int32_t* lens_out, uint8_t* used_blocks, void* stream) {
     clear_error();
     if (B > 0 && !partials) return fail(MX_ERR_NULL, "mx_qkv_rope_append_splits: null pointer");
     if (splits < 1) return fail(MX_ERR_INVALID, "mx_qkv_rope_append_splits: splits must be >= 1");
-    if (B > 0 && (!glue::a16(partials) || (bias && !aligned(bias, 8))))
-        return fail(MX_ERR_ALIGNMENT, "mx_qkv_rope_append_splits: partials need 16-byte alignment");
+    // The V heads' bias is read 8 halves (16 bytes) at a time, next to 16-byte partial loads.
+    if (B > 0 && (!glue::a16(partials) || (bias && !glue::a16(bias))))
+        return fail(MX_ERR_ALIGNMENT, "mx_qkv_rope_append_splits: partials and bias need 16-byte alignment");
     const int64_t width = (int64_t)(Hq + 2 * Hkv) * D;
     glue::RopeAppendParams p{nullptr, width, partials, splits, (int64_t)B * width, bias, Hq, Hkv, D,
                              reinterpret_cast<const float2*>(rope), max_pos, positions, q_out, q_stride, k_pool,
                              v_pool, kv_sblk, kv_shead, block_tables, bt_sb, max_blocks, block_size, num_pool_blocks,
-                             err, lens_out};
+                             err, lens_out, used_blocks};
     return rope_append_common("mx_qkv_rope_append_splits", p, B, stream);
 }
 

@@ -53,6 +53,7 @@ struct Params {
     int max_blocks, bs, num_pool_blocks;
     int32_t* err;
     int32_t* lens_out;  // optional: lens_out[m] = positions[m] + 1
+    uint8_t* used;      // optional [num_pool_blocks] map: 1 where a token was written
 };
 
 template <int MT, int D>
@@ -238,6 +239,7 @@ __global__ __launch_bounds__(kWaves * 64) void qkv_rope_kernel(Params p) {
             _Float16* k = reinterpret_cast<_Float16*>(p.k_pool) + dst[i] + c;
             k[0] = o[0];
             k[D / 2] = o[1];
+            if (p.used && flag_lane && head == p.Hq) p.used[p.bt[(int64_t)m * p.bt_sb + ps / p.bs]] = 1;
         } else {
             if (dst[i] < 0) continue;  // position or slot outside the tables: flagged by the q/k heads
             _Float16* v = reinterpret_cast<_Float16*>(p.v_pool) + dst[i] + c;
@@ -266,7 +268,7 @@ extern "C" int mx_w8a16_qkv_rope_append(const uint16_t* x, int64_t M, int64_t K,
                                         uint16_t* k_pool, uint16_t* v_pool, int64_t kv_sblk, int64_t kv_shead,
                                         const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks,
                                         int32_t block_size, int32_t num_pool_blocks, int32_t* err, int32_t* lens_out,
-                                        void* stream) {
+                                        uint8_t* used_blocks, void* stream) {
     const char* what = "mx_w8a16_qkv_rope_append";
     clear_error();
     if (M < 0) return fail(MX_ERR_INVALID, "%s: M must be >= 0", what);
@@ -310,6 +312,7 @@ extern "C" int mx_w8a16_qkv_rope_append(const uint16_t* x, int64_t M, int64_t K,
     p.num_pool_blocks = num_pool_blocks;
     p.err = err;
     p.lens_out = lens_out;
+    p.used = used_blocks;
     hipStream_t st = as_stream(stream);
     if (D == 128) qkvrope::launch<128>(p, st);
     else qkvrope::launch<64>(p, st);

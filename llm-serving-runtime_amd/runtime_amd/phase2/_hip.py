@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -67,7 +67,7 @@ SIGNATURES = {
     "mx_qkv_rope_append": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _i32, _i32,
-         _p, _p, _p],
+         _p, _p, _p, _p],
     ),
     "mx_add_rmsnorm": (
         ctypes.c_int,
@@ -80,12 +80,12 @@ SIGNATURES = {
     "mx_qkv_rope_append_splits": (
         ctypes.c_int,
         [_p, _i32, _p, _i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _i32, _i32,
-         _p, _p, _p],
+         _p, _p, _p, _p],
     ),
     "mx_w8a16_qkv_rope_append": (
         ctypes.c_int,
         [_p, _i64, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64,
-         _i32, _i32, _i32, _p, _p, _p],
+         _i32, _i32, _i32, _p, _p, _p, _p],
     ),
     "mx_add_rmsnorm_splits": (
         ctypes.c_int,

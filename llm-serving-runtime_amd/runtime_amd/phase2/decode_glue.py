@@ -55,6 +55,15 @@ def _lens_ptr(lens_out: torch.Tensor | None, b: int):
     return lens_out.data_ptr()
 
 
+def _used_ptr(used_blocks: torch.Tensor | None, nb: int, dev: torch.device):
+    if used_blocks is None:
+        return None
+    if (used_blocks.dtype != torch.uint8 or used_blocks.numel() < nb or not used_blocks.is_contiguous()
+            or used_blocks.device != dev):
+        raise ValueError("used_blocks must be a contiguous uint8 device tensor of num_blocks entries")
+    return used_blocks.data_ptr()
+
+
 _argmax_workspaces: dict[tuple, torch.Tensor] = {}
 
 
@@ -138,25 +147,23 @@ def kv_append(k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.
     if tables.dim() != 2 or tables.shape[0] != b:
         raise ValueError("block_tables must be [B, max_blocks]")
     starts = _i32(start_pos.reshape(-1), dev)
-    if used_blocks is not None and (used_blocks.dtype != torch.uint8 or used_blocks.numel() < nb
-                                    or not used_blocks.is_contiguous() or used_blocks.device != dev):
-        raise ValueError("used_blocks must be a contiguous uint8 device tensor of num_blocks entries")
+    used = _used_ptr(used_blocks, nb, dev)
     lib = _hip.load()
     _hip.check(lib.mx_kv_append(
         key_states.data_ptr(), value_states.data_ptr(), key_states.stride(0), key_states.stride(1),
         key_states.stride(2), b, t, hkv, d, tables.data_ptr(), tables.stride(0), int(tables.shape[1]),
         starts.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), bs, nb,
-        err.data_ptr() if err is not None else None, used_blocks.data_ptr() if used_blocks is not None else None,
-        _hip.stream_handle(dev)), "mx_kv_append")
+        err.data_ptr() if err is not None else None, used, _hip.stream_handle(dev)), "mx_kv_append")
 
 
 def qkv_rope_append(qkv: torch.Tensor, rope: torch.Tensor, positions: torch.Tensor, q_out: torch.Tensor,
                     k_layer: torch.Tensor, v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int,
                     num_kv_heads: int, err: torch.Tensor | None = None,
-                    lens_out: torch.Tensor | None = None) -> torch.Tensor:
+                    lens_out: torch.Tensor | None = None, used_blocks: torch.Tensor | None = None) -> torch.Tensor:
     """Rotate q, k of ``qkv [B, (Hq + 2 Hkv) * D]`` at ``positions [B]``; q -> ``q_out``, k, v -> the pool.
 
-    ``lens_out`` (int32 ``[B]``, optional) receives ``positions + 1``.
+    ``lens_out`` (int32 ``[B]``, optional) receives ``positions + 1``; ``used_blocks`` (uint8
+    ``[num_blocks]``, optional) gets 1 at every block a token was written to, as in :func:`kv_append`.
     """
     _hip.require_device_tensor(qkv, "qkv")
     dev = qkv.device
@@ -181,16 +188,18 @@ def qkv_rope_append(qkv: torch.Tensor, rope: torch.Tensor, positions: torch.Tens
         qkv2.data_ptr(), qkv2.stride(0), b, num_heads, num_kv_heads, d, rope.data_ptr(), int(rope.shape[0]),
         pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0),
         k_layer.stride(1), tables.data_ptr(), tables.stride(0), int(tables.shape[1]), bs, nb,
-        err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b), _hip.stream_handle(dev)),
-        "mx_qkv_rope_append")
+        err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b), _used_ptr(used_blocks, nb, dev),
+        _hip.stream_handle(dev)), "mx_qkv_rope_append")
     return q_out
 
 
 def qkv_rope_append_splits(partials: torch.Tensor, splits: int, bias: torch.Tensor | None, rope: torch.Tensor,
                            positions: torch.Tensor, q_out: torch.Tensor, k_layer: torch.Tensor,
                            v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,
-                           err: torch.Tensor | None = None, lens_out: torch.Tensor | None = None) -> torch.Tensor:
-    """:func:`qkv_rope_append` with the QKV projection as fp32 split partials ``[splits, B, width]``."""
+                           err: torch.Tensor | None = None, lens_out: torch.Tensor | None = None,
+                           used_blocks: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`qkv_rope_append` with the QKV projection as fp32 split partials ``[splits, B, width]``
+    (16-byte aligned, as is ``bias``)."""
     _hip.require_device_tensor(partials, "partials")
     dev = partials.device
     nb, hkv, bs, d = k_layer.shape
@@ -209,7 +218,7 @@ def qkv_rope_append_splits(partials: torch.Tensor, splits: int, bias: torch.Tens
         rope.data_ptr(), int(rope.shape[0]), pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(),
         v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), tables.data_ptr(), tables.stride(0),
         int(tables.shape[1]), bs, nb, err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b),
-        _hip.stream_handle(dev)), "mx_qkv_rope_append_splits")
+        _used_ptr(used_blocks, nb, dev), _hip.stream_handle(dev)), "mx_qkv_rope_append_splits")
     return q_out
 
 
@@ -219,7 +228,8 @@ QKV_ROPE_MAX_ROWS = 32
 def qkv_linear_rope_append(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
                            rope: torch.Tensor, positions: torch.Tensor, q_out: torch.Tensor, k_layer: torch.Tensor,
                            v_layer: torch.Tensor, block_tables: torch.Tensor, num_heads: int, num_kv_heads: int,
-                           err: torch.Tensor | None = None, lens_out: torch.Tensor | None = None) -> torch.Tensor:
+                           err: torch.Tensor | None = None, lens_out: torch.Tensor | None = None,
+                           used_blocks: torch.Tensor | None = None) -> torch.Tensor:
     """The int8 QKV projection of ``x [B, K]`` (packed fused-QKV weight, ``B <= 32``) and
     :func:`qkv_rope_append_splits` in one launch (``mx_w8a16_qkv_rope_append``)."""
     _hip.require_device_tensor(x, "x")
@@ -253,8 +263,8 @@ def qkv_linear_rope_append(x: torch.Tensor, packed: torch.Tensor, scale: torch.T
         bias.data_ptr() if bias is not None else None, num_heads, num_kv_heads, d, rope.data_ptr(),
         int(rope.shape[0]), pos.data_ptr(), q2.data_ptr(), q2.stride(0), k_layer.data_ptr(), v_layer.data_ptr(),
         k_layer.stride(0), k_layer.stride(1), tables.data_ptr(), tables.stride(0), int(tables.shape[1]), bs, nb,
-        err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b), _hip.stream_handle(dev)),
-        "mx_w8a16_qkv_rope_append")
+        err.data_ptr() if err is not None else None, _lens_ptr(lens_out, b), _used_ptr(used_blocks, nb, dev),
+        _hip.stream_handle(dev)), "mx_w8a16_qkv_rope_append")
     return q_out
 
 

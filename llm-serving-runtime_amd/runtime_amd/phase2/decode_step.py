@@ -17,7 +17,8 @@ current stream:
     a = paged_attention(q, pool)           mx_paged_attn_decode
     h += a Wo^T;  x = RMSNorm(h)           mx_w8a16_linear, mx_add_rmsnorm
     a = silu(x Wg^T) * (x Wu^T)            mx_w8a16_gateup_swiglu (gate and up rows
-                                           interleaved by 8, product in the epilogue)
+                                           interleaved by 8, product in the epilogue;
+                                           K is never split, the VALU GEMV takes <= 4 rows)
     h += a Wdown^T                         mx_w8a16_linear (+ the next add_rmsnorm)
     logits = RMSNorm(h) Wlm^T; argmax      mx_add_rmsnorm, mx_w8a16_linear, mx_argmax_rows_split
 
@@ -36,11 +37,11 @@ whole step can be captured in one HIP graph and replayed. Architecture is
 Llama / Qwen2 style (pre-norm, rotate-half RoPE, GQA, SwiGLU, untied int8
 lm_head); :meth:`Int8DecodeModel.from_hf` loads the weights of an HF
 ``LlamaForCausalLM`` / ``Qwen2ForCausalLM``. The gate||up weight is stored
-with gate and up rows interleaved in groups of 8 (``gateup_interleave``);
-where the fused epilogue does not apply (a gate||up GEMM that splits K, e.g.
-Qwen2-0.5B at batch 16), ``mx_swiglu_interleaved`` forms the product from the
-projection's split-K partials. At batches of at most 4 rows on such shapes the
-VALU GEMV takes the projection, with the SwiGLU product in its own epilogue.
+with gate and up rows interleaved in groups of 8 (``gateup_interleave``), and
+one ``mx_w8a16_gateup_swiglu`` launch per 128 rows writes ``silu(g) * u``
+whatever the batch: it never splits K (on shapes whose plain projection would,
+such as Qwen2-0.5B at batch 16, it runs unsplit), and at most 4 rows run on
+the VALU GEMV with the product in its own epilogue.
 """
 
 from __future__ import annotations
@@ -51,9 +52,9 @@ from dataclasses import dataclass
 import torch
 
 from .decode_glue import (QKV_ROPE_MAX_ROWS, add_rmsnorm, add_rmsnorm_splits, argmax_rows, qkv_linear_rope_append,
-                          qkv_rope_append, qkv_rope_append_splits, rope_table, swiglu_interleaved)
-from .int8_linear import (gateup_fusable, gateup_interleave, int8_gateup_swiglu, int8_linear,
-                          int8_linear_partials, linear_splits, pack_weight, quantize_weight)
+                          qkv_rope_append, qkv_rope_append_splits, rope_table)
+from .int8_linear import (gateup_interleave, int8_gateup_swiglu, int8_linear, int8_linear_partials, linear_splits,
+                          pack_weight, quantize_weight)
 from .paged_attention_hip import MX_PA_PLAN_READ, MX_PA_PLAN_WRITE
 from .paged_attention_hip import _decode as _paged_decode
 from .roofline import linear_hbm_bytes
@@ -105,13 +106,11 @@ class _Buffers:
     q: torch.Tensor       # rotated queries [B, heads * head_dim]
     attn: torch.Tensor    # attention output [B, heads, 1, head_dim]
     o: torch.Tensor       # [B, hidden]
-    gu: torch.Tensor      # [B, 2 * intermediate]
-    act: torch.Tensor     # [B, intermediate]
+    act: torch.Tensor     # [B, intermediate], silu(gate) * up
     mlp: torch.Tensor     # [B, hidden]
     logits: torch.Tensor  # [B, vocab]
-    part: torch.Tensor    # fp32 split partials of the current split projection
-    splits: dict          # projection name -> K splits at this batch size
-    gate_up_fused: bool   # gate||up with the SwiGLU epilogue in one launch (int8_gateup_swiglu)
+    part: torch.Tensor    # fp32 split partials of the current split projection (qkv, o, down)
+    splits: dict          # projection name -> K splits of its plain launch at this batch size
     attn_lens: torch.Tensor  # int32 [B]
     next: torch.Tensor    # int64 [B], greedy tokens
     err: torch.Tensor     # int32 [1], OR of the append kernels' error bits
@@ -249,15 +248,15 @@ class Int8DecodeModel:
                       "gate_up": (2 * s.intermediate, s.hidden), "down": (s.hidden, s.intermediate),
                       "lm_head": (s.vocab, s.hidden)}
             splits = {k: linear_splits(batch, n, kk) for k, (n, kk) in shapes.items()}
-            # The fused gate||up (SwiGLU epilogue) runs rows 128 at a time and needs no chunk split.
-            gate_up_fused = gateup_fusable(batch, *shapes["gate_up"])
-            part_elems = max([splits[k] * batch * shapes[k][0] for k in shapes if splits[k] > 1] + [4])
+            # gate||up runs unsplit with its SwiGLU epilogue and lm_head writes fp16 logits: only
+            # qkv (where not fused with RoPE), o and down write split partials.
+            part_elems = max([splits[k] * batch * shapes[k][0] for k in ("qkv", "o", "down") if splits[k] > 1]
+                             + [4])
             buf = _Buffers(h=e(batch, s.hidden), x=e(batch, s.hidden), qkv=e(batch, s.qkv_out),
                            q=e(batch, s.heads * s.head_dim), attn=e(batch, s.heads, 1, s.head_dim),
-                           o=e(batch, s.hidden), gu=e(batch, 2 * s.intermediate), act=e(batch, s.intermediate),
+                           o=e(batch, s.hidden), act=e(batch, s.intermediate),
                            mlp=e(batch, s.hidden), logits=e(batch, s.vocab),
                            part=torch.empty(part_elems, dtype=torch.float32, device=dev), splits=splits,
-                           gate_up_fused=gate_up_fused,
                            attn_lens=torch.zeros(batch, dtype=torch.int32, device=dev),
                            next=torch.zeros(batch, dtype=torch.int64, device=dev),
                            err=torch.zeros(1, dtype=torch.int32, device=dev))
@@ -294,20 +293,23 @@ class Int8DecodeModel:
             lens_out = buf.attn_lens if li == 0 else None
             k_layer = pool.k_layer_view(li)
             v_layer = pool.v_layer_view(li)
+            used = pool._used_map  # the pool's block-usage accounting, marked by the K/V append
             if self.uses_fused_qkv(bsz):
                 ev = self._tick(timers, "qkv")
                 packed, scale, _, bias = layer.qkv
                 qkv_linear_rope_append(buf.x, packed, scale, bias, self.rope, seq_lens, buf.q, k_layer, v_layer,
-                                       block_tables, s.heads, s.kv_heads, err=buf.err, lens_out=lens_out)
+                                       block_tables, s.heads, s.kv_heads, err=buf.err, lens_out=lens_out,
+                                       used_blocks=used)
                 self._tock(timers, "qkv", ev)
             elif sp["qkv"] > 1:
                 self._partials(buf.x, layer.qkv, buf.part, timers, "qkv")
                 qkv_rope_append_splits(buf.part, sp["qkv"], layer.qkv[3], self.rope, seq_lens, buf.q, k_layer,
-                                       v_layer, block_tables, s.heads, s.kv_heads, err=buf.err, lens_out=lens_out)
+                                       v_layer, block_tables, s.heads, s.kv_heads, err=buf.err, lens_out=lens_out,
+                                       used_blocks=used)
             else:
                 self._lin(buf.x, layer.qkv, buf.qkv, timers, "qkv")
                 qkv_rope_append(buf.qkv, self.rope, seq_lens, buf.q, k_layer, v_layer, block_tables, s.heads,
-                                s.kv_heads, err=buf.err, lens_out=lens_out)
+                                s.kv_heads, err=buf.err, lens_out=lens_out, used_blocks=used)
             ev = self._tick(timers, "attn")
             _paged_decode(buf.q.view(bsz, s.heads, 1, s.head_dim), k_layer, v_layer, block_tables, buf.attn_lens,
                           s.head_dim ** -0.5, s.group, out=buf.attn, shared_blocks=self.shared_kv_blocks,
@@ -344,18 +346,10 @@ class Int8DecodeModel:
             add_rmsnorm(buf.mlp, weight, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
 
     def _gate_up(self, buf: _Buffers, w, bsz: int, timers) -> None:
-        """act = silu(gate) * up from the interleaved gate||up weight."""
+        """act = silu(gate) * up from the interleaved gate||up weight, one launch per 128 rows."""
         packed, scale, n, bias = w
         ev = self._tick(timers, "gate_up")
-        if buf.gate_up_fused:
-            int8_gateup_swiglu(buf.x, packed, scale, bias, n // 2, out=buf.act)
-        elif buf.splits["gate_up"] > 1:  # split over K: the SwiGLU consumer sums the partials
-            int8_linear_partials(buf.x, packed, scale, n, buf.part)
-            swiglu_interleaved(None, n // 2, partials=buf.part, splits=buf.splits["gate_up"], bias=bias, rows=bsz,
-                               out=buf.act)
-        else:
-            int8_linear(buf.x, packed, scale, bias, n, out=buf.gu)
-            swiglu_interleaved(buf.gu, n // 2, out=buf.act)
+        int8_gateup_swiglu(buf.x, packed, scale, bias, n // 2, out=buf.act)
         self._tock(timers, "gate_up", ev)
 
     def _partials(self, x, w, part, timers, name):

@@ -32,12 +32,17 @@ MI355X-first differences:
   marks the blocks it writes in a device byte map. The ``IndexError`` the
   reference raises is raised by :meth:`check_write_errors` (one sync, called
   once per decode step by the decode loop), and ``allocated_block_count`` /
-  ``peak_allocated_block_count`` read the byte map when asked.
+  ``peak_allocated_block_count`` read the byte map when asked. A caller that
+  relies on the reference's raise at the write itself sets
+  ``sync_write_checks`` (or ``PHASE2_KV_SYNC_CHECKS=1`` before the pool is
+  built): every batched write then checks the word right away (one host sync
+  per call, skipped while a HIP graph is being captured).
 """
 
 from __future__ import annotations
 
 import math
+import os
 from dataclasses import dataclass
 
 import torch
@@ -69,6 +74,9 @@ class GpuKVBlockPool:
         self._peak_allocated_blocks = 0
         self._used_map: torch.Tensor | None = None    # uint8 [num_blocks]: blocks written on the device
         self._write_err: torch.Tensor | None = None   # int32 [1]: kv append error bits since the last check
+        # True: write_tokens_batch raises IndexError at the call, as the reference does (:221-222),
+        # at one host sync per call; False: at the next check_write_errors().
+        self.sync_write_checks = os.getenv("PHASE2_KV_SYNC_CHECKS", "0").strip() == "1"
 
     @property
     def block_size_tokens(self) -> int:
@@ -195,6 +203,8 @@ class GpuKVBlockPool:
 
             kv_append(k_layer, v_layer, block_tables, start_positions, key_states.to(self.dtype),
                       value_states.to(self.dtype), err=self._write_err, used_blocks=self._used_map)
+            if self.sync_write_checks and not torch.cuda.is_current_stream_capturing():
+                self.check_write_errors()
             return
         tables = block_tables.to(device=device, dtype=torch.int64)
         pos = start_positions.to(device=device, dtype=torch.int64).view(-1, 1) + torch.arange(

@@ -134,6 +134,30 @@ def _random_model(model_cls, config, seed: int, parallel: bool = False):
     return model.float().eval()
 
 
+# Buffers of HF's rotary embedding that ``nn.Module.to(dtype)`` would cast along with the weights.
+_ROPE_BUFFERS = ("inv_freq", "original_inv_freq")
+
+
+def to_device_dtype(model: nn.Module, device, dtype: torch.dtype) -> nn.Module:
+    """``model.to(device=device, dtype=dtype)`` with the rotary frequencies kept in fp32 (in place).
+
+    ``Module.to(dtype)`` casts every floating buffer, HF's ``inv_freq`` included. In fp16 the
+    frequencies carry a relative error of up to 2^-11, so the rotary angle ``pos * inv_freq`` is
+    off by ~1 rad at position 2000 for the fastest frequency: an error of the conversion, not of
+    fp16 arithmetic. A model loaded with ``from_pretrained(torch_dtype=fp16)`` (as the reference's
+    worker loads it, ``worker_server.py:176-186``) computes ``inv_freq`` in fp32 and keeps it; this
+    restores that for a model built in fp32 and converted afterwards. Used for the fp16/bf16
+    yardsticks and the HF device models of the GPU tests.
+    """
+    saved = {(mod_name, b): buf.detach().clone() for mod_name, mod in model.named_modules()
+             for b, buf in mod.named_buffers(recurse=False) if b in _ROPE_BUFFERS}
+    model.to(device=device, dtype=dtype)
+    modules = dict(model.named_modules())
+    for (mod_name, b), buf in saved.items():
+        setattr(modules[mod_name], b, buf.to(device=device, dtype=torch.float32))
+    return model
+
+
 def margin_controlled_(model: nn.Module, embed_scale: float = 200.0, successor: float = 0.2, seed: int = 0
                        ) -> torch.Tensor:
     """Give a random-init model a greedy top-1 margin far above fp16 activation error (in place).

@@ -44,7 +44,7 @@ def _run(hf, batch, lo, hi, seed, graph):
     dev = torch.device("cuda:0")
     cfg = hf.config
     ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
-    torch16 = copy.deepcopy(ref).to(device=dev, dtype=torch.float16).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), dev, torch.float16).eval()
     native = Int8DecodeModel.from_hf(hf, device=dev, max_positions=4096)
     s = native.shape
     assert (s.qkv_bias, s.group) == (cfg.model_type == "qwen2", cfg.num_attention_heads // cfg.num_key_value_heads)
@@ -99,6 +99,11 @@ def _run(hf, batch, lo, hi, seed, graph):
         tokens.copy_(nxt)
     assert native.error_flag() == 0
     assert seq_lens.cpu().tolist() == [n + STEPS for n in lens]
+    # The pool's block accounting: the prompts were copied in directly, so the device map holds
+    # exactly the blocks the decode steps' K/V appends wrote (positions lens[b] .. lens[b] + STEPS - 1).
+    decoded = {int(tables[b, p // BLOCK_SIZE]) for b in range(batch) for p in range(lens[b], lens[b] + STEPS)}
+    assert set(torch.nonzero(pool._used_map).flatten().tolist()) == decoded
+    assert pool.allocated_block_count() == len(decoded)
     toks = torch.stack(out_tokens, dim=1)  # [B, STEPS]: predictions of t1..tSTEPS
     logits = torch.stack(out_logits, dim=1)
 

@@ -31,7 +31,8 @@ continued from the same fp16 K/V the same way.
 
 Rules, as in the greedy-decode tests: per row ``max|dL| <= max(1e-2, 1.25 x torch fp16's
 error)``; a token that is not the oracle's argmax only where the oracle's top-1 gap is below
-twice that bar (a near tie that fp16 activations break either way), at most 2 % of all steps.
+twice that bar (a near tie that fp16 activations break either way), at most 2 % of all steps or
+torch fp16's own flips on the same prefixes plus one.
 Each test reports rows with every token identical, flips and errors (``ParityReport``).
 """
 
@@ -117,7 +118,9 @@ def _check_tolerance(results, label):
         assert r["err"] <= r["allowed"], f"row {r['row']}: logits off by {r['err']:.3e} (allowed " \
                                          f"{r['allowed']:.3e}); {summary}"
         assert r["ties_ok"], f"row {r['row']}: a mismatch outside the near-tie band {r}; {summary}"
-    assert sum(r["mismatches"] for r in results) <= MAX_TIE_FRACTION * sum(r["steps"] for r in results), summary
+    # At most 2 % of the steps, or as many as torch fp16 makes on the same prefixes plus one.
+    flips, yard = sum(r["mismatches"] for r in results), sum(r["yard"] for r in results)
+    assert flips <= max(MAX_TIE_FRACTION * sum(r["steps"] for r in results), yard + 1), summary
     report(summary)
 
 
@@ -131,7 +134,7 @@ def _config3(margin: bool):
     cfg = hf.config
     assert (cfg.num_hidden_layers, cfg.vocab_size, cfg.hidden_size) == (24, 151936, 896)
     ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
-    torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), DEV, torch.float16).eval()
     native = Int8DecodeModel.from_hf(hf, device=DEV)
     del hf
     s = native.shape
@@ -211,7 +214,7 @@ def test_native_step_llama3_b32_bench_inputs():
     ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
     native = Int8DecodeModel.from_hf(hf, device=DEV)
     del hf
-    torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), DEV, torch.float16).eval()
     s = native.shape
     lens, tables = make_contexts(batch, 128, 4096, BLOCK_SIZE, pool_blocks, headroom=STEPS + 1, seed=0)
     lens = lens.tolist()

@@ -67,10 +67,10 @@ def _case(layers: int, batch: int, lo: int, hi: int, seed: int, margin: bool = F
         om.margin_controlled_(model, seed=seed)
     cfg = model.config
     ref = om.quantized_reference(model)
-    torch16 = copy.deepcopy(ref).to(device=device, dtype=torch.float16).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), device, torch.float16).eval()
     w0 = model.model.layers[0].mlp.down_proj.weight.detach().numpy().copy()
     quantize_model_(model, device=device)
-    model.to(device=device, dtype=torch.float16)
+    om.to_device_dtype(model, device, torch.float16)
     enable_block_paged_attention(model)
     assert sum(isinstance(m, Int8Linear) for m in model.modules()) == 7 * layers
     packed0 = model.model.layers[0].mlp.down_proj.packed_weight.cpu().numpy()
@@ -194,8 +194,8 @@ def test_greedy_bf16_model_through_the_hook():
     model = om.random_qwen2(seed=11, num_hidden_layers=2, vocab_size=32768)
     cfg = model.config
     ref = copy.deepcopy(model).eval()
-    yard = copy.deepcopy(model).to(device=device, dtype=torch.bfloat16).eval()
-    model.to(device=device, dtype=torch.bfloat16)
+    yard = om.to_device_dtype(copy.deepcopy(model), device, torch.bfloat16).eval()
+    om.to_device_dtype(model, device, torch.bfloat16)
     enable_block_paged_attention(model)
     g = torch.Generator().manual_seed(11)
     lens = torch.randint(40, 160, (batch,), generator=g).tolist()

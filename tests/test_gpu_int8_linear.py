@@ -240,14 +240,16 @@ def test_swiglu_linear_equals_silu_mul_then_linear(m, n, k):
 
 @pytest.mark.parametrize("m,inter,k", [(32, 14336, 4096), (7, 4864, 896), (64, 1024, 256), (128, 1024, 256),
                                         (70, 4864, 896), (100, 14336, 4096), (1, 4864, 896), (3, 4864, 896),
-                                        (4, 4864, 896), (1, 14336, 4096), (4, 14336, 4096)])
+                                        (4, 4864, 896), (1, 14336, 4096), (4, 14336, 4096),
+                                        (49, 14336, 4096), (64, 14336, 4096)])
 def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     """gate||up with interleaved rows and the SwiGLU product in the epilogue equals the plain
     [gate | up] projection followed by mx_silu_mul, bit for bit where both take the same K
     accumulation (within fp16 rounding where the plain projection splits K). At M <= 4 on the Qwen2-0.5B
     MLP (a shape whose MFMA launch splits K) the VALU GEMV takes both, with the product in
     the GEMV's own epilogue; the Llama MLP at M <= 4 runs the unsplit MFMA kernel, and shapes whose
-    plain projection splits K (the Qwen2 MLP at 7 and 70 rows) run one unsplit MFMA launch."""
+    plain projection splits K (the Qwen2 MLP at 7 and 70 rows) run one unsplit MFMA launch. The Llama
+    MLP at 49-64 rows takes the instance with two m-tiles per wave and the SwiGLU epilogue."""
     from runtime_amd.phase2.decode_glue import silu_mul
     from runtime_amd.phase2.int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu,
                                                 linear_splits)

@@ -82,7 +82,7 @@ def test_native_step_shared_prefix_join_finish():
     hf = om.random_llama(seed=5, num_hidden_layers=2, vocab_size=32768)
     cfg = hf.config
     ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
-    torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), DEV, torch.float16).eval()
     native = Int8DecodeModel.from_hf(hf, device=DEV, max_positions=1024)
     native.shared_kv_blocks = True
     s = native.shape
@@ -200,7 +200,7 @@ def test_native_step_config5_rows_join_finish():
     hf = om.random_llama(seed=9, num_hidden_layers=2, vocab_size=32768)
     cfg = hf.config
     ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
-    torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), DEV, torch.float16).eval()
     native = Int8DecodeModel.from_hf(hf, device=DEV, max_positions=2048)
     native.shared_kv_blocks = True
     s = native.shape

@@ -43,9 +43,9 @@ def _model(seed: int):
 
     model = om.random_qwen2(seed=seed, num_hidden_layers=2, vocab_size=32768)
     ref = om.quantized_reference(model)
-    torch16 = copy.deepcopy(ref).to(device=DEV, dtype=torch.float16).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), DEV, torch.float16).eval()
     quantize_model_(model, device=DEV)
-    model.to(device=DEV, dtype=torch.float16)
+    om.to_device_dtype(model, DEV, torch.float16)
     enable_block_paged_attention(model)
     return model, ref, torch16
 
@@ -154,7 +154,7 @@ def test_hip_graph_decode_matches_eager():
     g = torch.Generator().manual_seed(22)
     # The longest row needs 16 blocks: the persistent cache's table width, which both the eager
     # dense step and the graph (keyed by that width) hand to attention.
-    lens = [30, 100, 245, 57, 180]
+    lens = [30, 100, 235, 57, 180]
     prompts = [torch.randint(0, 32768, (n,), generator=g) for n in lens]
     steps, tail = 10, 5
     need = [math.ceil((n + steps + tail + 1) / BS) for n in lens]
@@ -198,7 +198,8 @@ def test_hip_graph_decode_matches_eager():
 
 def test_kv_write_overrun_raises_at_check():
     """write_tokens_batch queues the write without a host sync; a slot past the table is skipped
-    and ``check_write_errors`` raises the reference's IndexError, once."""
+    and ``check_write_errors`` raises the reference's IndexError, once; with ``sync_write_checks`` the
+    write itself raises, as in the reference."""
     pool = _pool(8)
     table = torch.tensor([[3, 5]], dtype=torch.int32, device=DEV)
     k = torch.randn(1, 2, 4, 64, device=DEV).half()
@@ -208,3 +209,9 @@ def test_kv_write_overrun_raises_at_check():
     pool.check_write_errors()  # cleared
     assert pool.allocated_block_count() == 1  # block 5 holds positions 30, 31
     torch.testing.assert_close(pool.k_layer_view(0)[5, :, 14:16], k[0, :, :2])
+    # Opt-in: the reference's raise at the write itself (one host sync per call).
+    pool.sync_write_checks = True
+    with pytest.raises(IndexError):
+        pool.write_tokens_batch(0, table, torch.tensor([31], device=DEV), k, k)
+    pool.write_tokens_batch(0, table, torch.tensor([0], device=DEV), k, k)  # in range: no raise
+    assert pool.allocated_block_count() == 2

@@ -7,6 +7,8 @@ agreement rule used by the GPU greedy-decode tests.
 
 from __future__ import annotations
 
+import copy
+
 import numpy as np
 import pytest
 import torch
@@ -171,3 +173,29 @@ def test_parallel_init_is_seeded_and_distributed():
     assert not torch.equal(flat[:1000], flat[1 << 24:(1 << 24) + 1000])
     norm = a.model.layers[0].input_layernorm.weight.detach()
     assert abs(float(norm.mean()) - 1.0) < 0.02 and abs(float(norm.std()) - 0.05) < 0.01
+
+
+def test_to_device_dtype_keeps_rotary_frequencies_fp32():
+    """A model converted to a 16-bit dtype keeps HF's rotary frequencies in fp32 (as a model loaded in
+    that dtype has them): its (cos, sin) at long positions are the fp32 ones rounded once. Converted
+    with a plain ``.to(dtype)`` the frequencies round and the angles drift by up to radians."""
+    cfg = dict(hidden_size=128, num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+               intermediate_size=256, vocab_size=512, max_position_embeddings=8192)
+    ref = om.random_llama(seed=9, **cfg)
+    fixed = om.to_device_dtype(copy.deepcopy(ref), "cpu", torch.bfloat16)
+    naive = copy.deepcopy(ref).to(dtype=torch.bfloat16)
+    rot = fixed.model.rotary_emb
+    assert rot.inv_freq.dtype == rot.original_inv_freq.dtype == torch.float32
+    assert torch.equal(rot.inv_freq, ref.model.rotary_emb.inv_freq)
+    assert naive.model.rotary_emb.inv_freq.dtype == torch.bfloat16
+    assert fixed.model.layers[0].mlp.down_proj.weight.dtype == torch.bfloat16
+    pos = torch.arange(2000, 4096, 7).view(1, -1)
+    x = torch.zeros(1, pos.shape[1], 128)
+    with torch.no_grad():
+        cos_ref, sin_ref = ref.model.rotary_emb(x, pos)
+        cos_f, sin_f = rot(x.to(torch.bfloat16), pos)
+        cos_n, sin_n = naive.model.rotary_emb(x.to(torch.bfloat16), pos)
+    err_fixed = max(float((cos_f.float() - cos_ref).abs().max()), float((sin_f.float() - sin_ref).abs().max()))
+    err_naive = max(float((cos_n.float() - cos_ref).abs().max()), float((sin_n.float() - sin_ref).abs().max()))
+    assert err_fixed <= 2.0 ** -8, err_fixed   # one bf16 rounding of a value in [-1, 1]
+    assert err_naive > 0.5, err_naive
