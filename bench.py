@@ -58,6 +58,7 @@ LM_HEAD_REPEATS = 8
 COPY_PROBE_BYTES = 1 << 30
 ATTN_TRAFFIC_PROFILE = os.path.join(HERE, "profiles", "paged_attn_traffic_llama3_8b_b32.md")
 GEMM_COUNTER_PROFILE = os.path.join(HERE, "profiles", "int8_gemm_counters_llama3_8b_b32.md")
+SWEEP_COUNTER_PROFILE = os.path.join(HERE, "profiles", "int8_linear_sweep_counters_configs1_4.md")
 PREFIX_GROUPS, PREFIX_TOKENS, ROTATE_EVERY = 16, 1024, 16
 
 
@@ -87,6 +88,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--probe-family", choices=["attn", "linears", "sweep"], default="attn",
                     help="attn / linears: the headline step's attention or its four projections; sweep: "
                          "int8_linear alone on config 4's shapes (and config 1's at --batch 1) at M = --batch")
+    ap.add_argument("--kv-layout", choices=["split", "interleaved"], default="interleaved",
+                    help="KV pool layout (GpuKVBlockPool kv_layout) of the headline, config 2 and config 5 pools")
     ap.add_argument("--stream-shared-kv", action="store_true",
                     help="config 5: read the aliased K/V with streaming loads (no MX_PA_SHARED_BLOCKS)")
     args = ap.parse_args()
@@ -178,9 +181,9 @@ def committed_figures(path: str, prefix: str) -> dict[str, dict]:
 
 
 def fill_normal(t, gen) -> None:
-    flat = t.view(-1)
-    for i in range(0, flat.numel(), 1 << 28):
-        flat[i:i + (1 << 28)].normal_(generator=gen)
+    """N(0, 1) in place, one leading slice at a time (the pool tensors may be strided views)."""
+    for i in range(t.shape[0]):
+        t[i].normal_(generator=gen)
 
 
 CPU_SAMPLE_S = 10.0  # seconds of CPU work per baseline sample (a bounded sample of the workload)
@@ -290,7 +293,8 @@ def time_step(step, steps: int, warmup: int, use_graph: bool = True):
 class Decoder:
     """A random-init int8 decoder, its paged pool (random K/V) and a batch of seeded contexts."""
 
-    def __init__(self, shape, batch: int, lo: int, hi: int, pool_blocks: int, headroom: int, layers=None, seed=0):
+    def __init__(self, shape, batch: int, lo: int, hi: int, pool_blocks: int, headroom: int, layers=None, seed=0,
+                 kv_layout: str = "interleaved"):
         import torch
 
         from runtime_amd.phase2.decode_step import Int8DecodeModel, make_contexts
@@ -304,7 +308,7 @@ class Decoder:
         self.model = Int8DecodeModel(shape, device=self.dev, seed=seed, layers=self.n_layers)
         self.pool = GpuKVBlockPool(num_blocks=pool_blocks, block_size_tokens=self.bs, num_layers=self.n_layers,
                                    num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16,
-                                   device=self.dev)
+                                   device=self.dev, kv_layout=kv_layout)
         self.pool._ensure_pools()
         gk = torch.Generator(device=self.dev).manual_seed(seed + 1)
         fill_normal(self.pool._k_pool, gk)
@@ -577,7 +581,7 @@ def config14_linears(args) -> tuple[dict, dict]:
                                                 ("down", 14336, 4096))]
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    counters = committed_figures(GEMM_COUNTER_PROFILE, "gemm-counters")
+    counters = committed_figures(SWEEP_COUNTER_PROFILE, "gemm-counters")
     rows = []
     for idx, (name, k, n, ms) in enumerate(shapes):
         g = torch.Generator(device=dev).manual_seed(0 if name == "config1" else 1000 + idx - 1)
@@ -625,6 +629,8 @@ def config14_linears(args) -> tuple[dict, dict]:
         "workload": "int8 linear x [1,4096] @ W [4096,4096] (seed 0)",
         "avg_us": c1["avg_us"], "bytes_per_call": c1["bytes"], "gbps": c1["gbps"], "frac": c1["frac"],
     }
+    if "counters" in c1:
+        config1["counters"] = dict(c1["counters"], profile=os.path.relpath(SWEEP_COUNTER_PROFILE, HERE))
     if "cpu_baseline" in c1:
         config1["cpu_baseline"] = dict(cpu_note, value=c1["cpu_baseline"]["gbps"], us_per_call=c1["cpu_baseline"]["us"])
     sweep_rows = rows[1:]
@@ -706,7 +712,8 @@ def config5_prefix(args, model, bsz: int = 128) -> dict:
     shared_before = model.shared_kv_blocks
     model.shared_kv_blocks = not args.stream_shared_kv
     pool = GpuKVBlockPool(num_blocks=num_blocks, block_size_tokens=bs, num_layers=n_layers,
-                          num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16, device=dev)
+                          num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16, device=dev,
+                          kv_layout=args.kv_layout)
     pool._ensure_pools()
     gk = torch.Generator(device=dev).manual_seed(1)
     fill_normal(pool._k_pool, gk)
@@ -836,7 +843,8 @@ def traffic_probe(args) -> int:
         return sweep_probe(args)
     shape = LLAMA3_8B if args.model == "llama3-8b" else QWEN2_05B
     headroom = args.warmup + args.steps + args.kernel_steps + 2  # the bench's table width
-    d = Decoder(shape, args.batch, args.ctx_lo, args.ctx_hi, args.pool_blocks, headroom, layers=args.layers)
+    d = Decoder(shape, args.batch, args.ctx_lo, args.ctx_hi, args.pool_blocks, headroom, layers=args.layers,
+                kv_layout=args.kv_layout)
     fams = family_launches(d)
     names = ["attn"] if args.probe_family == "attn" else ["qkv", "o", "gate_up", "down"]
     for name in names:
@@ -949,7 +957,8 @@ def main() -> int:
                               config={"workload": c5["workload"]}, **c5)), flush=True)
         return 0
     headroom = args.warmup + 1 + GRAPH_WARMUP + args.steps + args.kernel_steps + 2
-    d = Decoder(shape, args.batch, args.ctx_lo, args.ctx_hi, args.pool_blocks, headroom, layers=args.layers)
+    d = Decoder(shape, args.batch, args.ctx_lo, args.ctx_hi, args.pool_blocks, headroom, layers=args.layers,
+                kv_layout=args.kv_layout)
     if args.workload == "attention":
         c2 = config2_attention(args, d.pool, d.n_layers)
         print(json.dumps({"metric": "paged decode attention algorithmic HBM GB/s (config 2)", "value": c2["gbps"],

@@ -34,11 +34,12 @@ def test_reference_roundtrip_kat_product_pool():
     assert pool.allocated_block_count() == 1  # both tokens land in block 0 (bs=2)
 
 
-def test_product_pool_matches_oracle_layout():
+@pytest.mark.parametrize("layout", ["split", "interleaved"])
+def test_product_pool_matches_oracle_layout(layout):
     g = torch.Generator().manual_seed(0)
     nb, layers, hkv, bs, d = 12, 3, 2, 4, 8
     pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=bs, num_layers=layers, num_kv_heads=hkv, head_dim=d,
-                          dtype=torch.float32, device="cpu")
+                          dtype=torch.float32, device="cpu", kv_layout=layout)
     ok, ov = kv_pool.empty_pool(nb, layers, hkv, bs, d)
     tables = torch.tensor([[3, 7, 1, 0], [9, 2, 11, 5]], dtype=torch.int32)
     starts = torch.tensor([0, 5])
@@ -51,8 +52,13 @@ def test_product_pool_matches_oracle_layout():
     for layer in range(layers):  # same per-layer contents; layer-major storage
         assert torch.equal(pool.k_layer_view(layer), ok[:, layer])
         assert torch.equal(pool.v_layer_view(layer), ov[:, layer])
-    assert pool.k_layer_view(1).stride() == (hkv * bs * d, bs * d, d, 1)
-    assert pool.k_layer_view(1).is_contiguous()
+    k1v, v1v = pool.k_layer_view(1), pool.v_layer_view(1)
+    if layout == "split":
+        assert k1v.stride() == (hkv * bs * d, bs * d, d, 1) and k1v.is_contiguous()
+    else:  # one (block, kv-head) holds its K run, then its V run
+        assert k1v.stride() == v1v.stride() == (hkv * 2 * bs * d, 2 * bs * d, d, 1)
+        assert v1v.data_ptr() - k1v.data_ptr() == bs * d * k1v.element_size()
+        assert k1v[5, 1].data_ptr() - k1v.data_ptr() == (5 * hkv * 2 + 2) * bs * d * k1v.element_size()
     keys, vals = pool.gather_layer(2, tables[1].tolist(), 11)
     ok_k, ok_v = kv_pool.gather_layer(ok, ov, 2, tables[1].tolist(), 11)
     assert torch.equal(keys, ok_k) and torch.equal(vals, ok_v)
