@@ -512,7 +512,12 @@ __device__ __forceinline__ void run_piece(const Params& p, int b, int kvh, int t
 // that starts from the plan (MX_PA_PLAN_READ). The record's stores are in their own instance: in the
 // plain one they pushed the D = 128 instances past their register budget (4-6 VGPRs of spills).
 template <int D, int BS, int G, bool STREAM, bool BF16, bool PROBE = false, int PLAN = 0>
-__global__ __launch_bounds__(kWaves * 64, (D == 64 && !PROBE) ? 2 : MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
+// The instance that records the tile plan (PLAN = 1, layer 0 of a decode step) and the block-size 4
+// and 8 instances need more than the 168 VGPRs of 3 waves per SIMD (they spilled 12-28 bytes per
+// lane there); at 2 waves per SIMD (256 VGPRs) they hold 171 without scratch and still keep the
+// default 2048 workers resident in one round. The recording call at the bench shape: 60.7-61.6
+// -> 56.8-56.9 us on MI355X (three interleaved pairs).
+__global__ __launch_bounds__(kWaves * 64, ((D == 64 && !PROBE) || PLAN == 1 || BS < kTile) ? 2 : MX_PA_MIN_WAVES) void decode_split_kernel(Params p) {
     constexpr bool PLANNED = PLAN == 2;
     constexpr int DPL = D / 16;      // dims per lane in P.V: one MFMA per dim offset
     constexpr int BPT = BS >= kTile ? 1 : kTile / BS;  // KV blocks per tile (block sizes 4, 8)

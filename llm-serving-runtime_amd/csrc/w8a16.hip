@@ -688,8 +688,17 @@ static WideShape wide_shape(int NT, bool npw1_only) {
 template <int MT, int NPW, int WAVES, bool SW, bool GU, int KW = 1, int MW = 1, int NJX = 0>
 static void launch_shape(const uint16_t* x, int64_t xs, int M, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                          uint16_t* y, int64_t ys, int NT, int KT, int KS, float* partial, hipStream_t st) {
-    // Pipeline depth: 6 for the M-split shape spilled (24 VGPRs at 4 m-tiles); 4 fits.
-    constexpr int P = MW > 1 ? 4 : (NPW == 1 ? mfma_depth(MT) : (NPW == 2 ? 6 : 4));
+    // Pipeline depth (k-tiles of loads in flight per wave), the deepest that fits 256 VGPRs
+    // without scratch: 6 for the M-split shape spilled (24 VGPRs at 4 m-tiles), 4 fits. The wide
+    // shapes (two or four n-tiles) and the SwiGLU-input instances at three or more m-tiles spilled
+    // 36-216 bytes per lane at depths 4-6; at the depths below none does, and on MI355X lm_head
+    // (128256 x 4096) went 99.3-102.6 -> 84.4-85.3 us at 33 rows and 100.5-103.9 -> 86.7-87.4 us at
+    // 48, the SwiGLU-input down (4096 x 14336) 42.0-42.4 -> 37.5-37.7 us at 48 rows and
+    // 49.1-49.5 -> 37.5-37.8 us at 64 (three interleaved pairs each).
+    constexpr int P = MW > 1 ? 4
+                      : NPW == 1 ? (SW && MT >= 3 ? 3 : mfma_depth(MT))
+                      : NPW == 2 ? (MT == 1 ? 6 : (MT == 2 ? 4 : 3))
+                                 : (MT <= 2 ? 4 : 2);
     const int groups = ceil_div(NT, (WAVES / (KW * MW)) * NPW);
     hipLaunchKernelGGL((gemm_mfma_kernel<MT, NPW, WAVES, P, SW, GU, KW, MW, NJX>), dim3(groups, KS), dim3(WAVES * 64), 0,
                        st, x, xs, M, w, s, b, y, ys, KT, NT, partial);
