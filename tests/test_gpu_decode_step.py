@@ -164,3 +164,42 @@ def test_native_step_more_than_64_rows(batch):
 def test_native_step_llama3_shape_graph_replay():
     hf = om.random_llama(seed=2, num_hidden_layers=2, vocab_size=32768)
     _run(hf, batch=32, lo=48, hi=160, seed=2, graph=True)
+
+
+def test_native_step_same_bits_on_both_pool_layouts():
+    """The native step (fused qkv + RoPE append, tile-planned attention, graph replays) on a pool of
+    each layout holding the same K/V: identical logits, tokens and K/V after 8 steps."""
+    from runtime_amd.phase2.decode_step import QWEN2_05B, Int8DecodeModel, make_contexts
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    dev = torch.device("cuda:0")
+    native = Int8DecodeModel(QWEN2_05B, device=dev, seed=5, layers=2)
+    s = native.shape
+    lens, tables = make_contexts(8, 100, 600, BLOCK_SIZE, 512, headroom=9, seed=5)
+    g = torch.Generator(device=dev).manual_seed(6)
+    init_k = torch.randn(2, 512, s.kv_heads, BLOCK_SIZE, s.head_dim, generator=g, device=dev).half()
+    init_v = torch.randn_like(init_k)
+    runs = {}
+    for layout in ("split", "interleaved"):
+        pool = GpuKVBlockPool(num_blocks=512, block_size_tokens=BLOCK_SIZE, num_layers=2, num_kv_heads=s.kv_heads,
+                              head_dim=s.head_dim, dtype=torch.float16, device=dev, kv_layout=layout)
+        pool._ensure_pools()
+        pool._k_pool.copy_(init_k)
+        pool._v_pool.copy_(init_v)
+        seq = lens.to(dev).clone()
+        tok = torch.arange(8, device=dev, dtype=torch.int64) * 101
+        tdev = tables.to(dev)
+        native.step(tok, pool, tdev, seq, out=tok)  # eager: sizes the buffers
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            _, logits = native.step(tok, pool, tdev, seq, return_logits=True, out=tok)
+        seen = []
+        for _ in range(8):
+            graph.replay()
+            seen.append((logits.clone(), tok.clone()))
+        runs[layout] = (seen, pool._k_pool.clone(), pool._v_pool.clone(), seq.clone())
+    (a, ka, va, sa), (b, kb, vb, sb) = runs["split"], runs["interleaved"]
+    assert torch.equal(sa, sb) and sa.tolist() == [n + 9 for n in lens.tolist()]
+    for (la, ta), (lb, tb) in zip(a, b):
+        assert torch.equal(la, lb) and torch.equal(ta, tb)
+    assert torch.equal(ka, kb) and torch.equal(va, vb)

@@ -525,3 +525,22 @@ def test_tile_plan_flags_changed_lengths():
         ws[off:off + 4].zero_()
     torch.cuda.synchronize()
     assert workspace_error_flag(dev) == 0
+
+
+@pytest.mark.parametrize("d,bs,grp", [(128, 16, 4), (64, 16, 7), (128, 4, 4), (64, 32, 2)])
+def test_interleaved_pool_layout_is_bit_identical(d, bs, grp):
+    """The pool's default layout keeps each (block, kv-head)'s K and V runs adjacent in one tensor
+    ([nb, Hkv, 2, bs, D]); the kernel reads strided views of it. The same K/V in that layout and in two
+    separate tensors give the same bits, and the oracle's answer."""
+    q, k, v, tables, lens = _random_case(21, 5, 2, grp, d, bs, [1, 40, 300, 2049, 0])
+    kv = torch.empty(k.shape[0], k.shape[1], 2, bs, d, dtype=k.dtype, device=k.device)
+    kv[:, :, 0] = k
+    kv[:, :, 1] = v
+    ki, vi = kv[:, :, 0], kv[:, :, 1]
+    assert ki.stride() == vi.stride() == (k.shape[1] * 2 * bs * d, 2 * bs * d, d, 1)
+    scale = d ** -0.5
+    split = _decode(q, k, v, tables, lens, scale, grp)
+    inter = _decode(q, ki, vi, tables, lens, scale, grp)
+    assert torch.equal(split, inter)
+    _check(inter, oracle_out(q, ki, vi, tables, lens, scale, grp))
+    assert workspace_error_flag() == 0
