@@ -18,8 +18,12 @@ Modules:
                         (torch fp32 on the CPU).
 * ``kv_pool``         - the paged KV pool layout and its write/gather
                         (torch on the CPU).
-* ``model``           - a small fp32 decoder-step oracle used by the greedy
-                        decode tests.
+* ``model``           - the fp32 HF decoder (Qwen2 / Llama) holding exactly the
+                        device's int8 weights: teacher-forced logits, prefill K/V,
+                        continuation from given K/V, greedy decode; used by the
+                        greedy-decode and native-step tests.
+* ``glue``            - RoPE, RMSNorm + residual, SwiGLU and the KV append of the
+                        decode step (torch on the CPU).
 
 Parity status of each function is stated in its module header.
 """
