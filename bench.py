@@ -1,6 +1,6 @@
 """Decode-step benchmark on one MI355X: int8 (W8A16) linears + paged-attention decode.
 
-Headline workload: a Llama-3-8B-shaped int8 weight-only decoder
+Headline workload (the benchmark's north star): a Llama-3-8B-shaped int8 weight-only decoder
 (32 layers, hidden 4096, 32 q / 8 kv heads, head_dim 128, intermediate 14336, vocab 128256),
 batch 32, one token per row per step, paged fp16 KV with block_size 16 in a 16384-block pool,
 contexts ~ U[128, 4096] drawn with seed 0 (config-2-like), block tables from one randperm of
@@ -17,8 +17,9 @@ latency lands inside the interval (the single lm_head launch is repeated 8 times
 oracle on a bounded sample (one decoder layer at the same batch and contexts, plus an lm_head
 slice), extrapolated to the full step. ``hbm_copy`` is a timed 1 GiB device-to-device copy.
 
-``configs`` carries every other BASELINE config in the same run, each with its algorithmic
-bytes, achieved GB/s, roofline fraction and (where BASELINE.md lists one) a CPU baseline:
+``configs`` carries every other benchmark configuration in the same run, each with its
+algorithmic bytes, achieved GB/s, roofline fraction and (where the configuration asks for one) a
+CPU baseline:
 
 * ``config1_linear`` and ``config4_linear_sweep``: the single 4096x4096 int8 linear at M=1 and
   the Llama-3-8B projections at M in {1, 8, 32, 64}, each timed over enough distinct weight
@@ -818,8 +819,8 @@ def config5_prefix(args, model, bsz: int = 128) -> dict:
                  "gbps_unique": round(final_uniq / attn_s / 1e9, 1),
                  "gbps_logical": round(final_logical / attn_s / 1e9, 1)},
         "setup_s": round(setup_s, 1),
-        "cpu_baseline": None, "cpu_baseline_note": "not CPU-timed (68 GB of logical K/V per step); BASELINE.md "
-                                                   "lists none",
+        "cpu_baseline": None, "cpu_baseline_note": "not CPU-timed (68 GB of logical K/V per step); the "
+                                                   "configuration asks for none",
     }
 
 

@@ -145,7 +145,7 @@ def test_reference_batched_ragged():
 
 
 def _config2(seed=0):
-    """B=32, Hq=32, Hkv=8, D=128, bs=16, ctx ~ U[128, 4096], one randperm(16384) pool."""
+    """Benchmark config 2: B=32, Hq=32, Hkv=8, D=128, bs=16, ctx ~ U[128, 4096], one randperm(16384) pool."""
     g = torch.Generator().manual_seed(seed)
     bsz, hkv, grp, d, bs, nb = 32, 8, 4, 128, 16, 16384
     lens = torch.randint(128, 4097, (bsz,), generator=g)
@@ -395,7 +395,7 @@ def test_block_ids_outside_the_pool(d, bs):
 
 
 def _config5_attention_case(seed=0):
-    """BASELINE config 5's attention shape: 128 rows in 16 groups of 8, each group's rows longer than
+    """Benchmark config 5's attention shape: 128 rows in 16 groups of 8, each group's rows longer than
     1024 tokens aliasing the group's 1024-token prefix blocks; contexts U[1, 8192]; Llama-3-8B heads
     (Hq 32, Hkv 8, D 128), block 16, a 40960-block pool with seeded block ids."""
     from runtime_amd.phase2.prefix_batch import PrefixBatch

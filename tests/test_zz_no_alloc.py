@@ -65,7 +65,7 @@ def _noalloc(q, k, v, tables, lens, err=None, flags=0):
 
 
 def test_noalloc_equals_workspace_entry_two_calls():
-    # Call 1: BASELINE config 2 (32 rows, GQA 4, D 128, contexts U[128, 4096], 16384-block pool).
+    # Call 1: benchmark config 2 (32 rows, GQA 4, D 128, contexts U[128, 4096], 16384-block pool).
     g = torch.Generator().manual_seed(0)
     lens1 = torch.randint(128, 4097, (32,), generator=g).tolist()
     big = _case(0, lens1, 8, 4, 128, 16, num_blocks=16384)
