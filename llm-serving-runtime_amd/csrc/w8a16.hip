@@ -508,16 +508,57 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     }
 }
 
-// y[m, n] = fp16(sum over splits of partial[ks][m][n] + bias[n]).
-__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ partial, int KS, int M, int N,
+// y[m, n] = fp16(bias[n] + the splits' partial[ks][m][n] in split order), one fp32 add each. A
+// thread owns 8 consecutive outputs (N % 16 == 0). KS > 0 is the split count known at compile time:
+// every split's two 16-byte loads go out before the first add, one memory round trip in all; KS == 0
+// loops over `splits`. A runtime loop of one element per thread made the compiler wait for each
+// split's load before issuing the next: one round trip per split.
+template <int KS>
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ partial, int splits, int M, int N,
                                                      const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
                                                      int64_t ys) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)M * N) return;
-    const int m = (int)(idx / N), n = (int)(idx % N);
-    float v = bias ? h2f(bias, n) : 0.0f;
-    for (int k = 0; k < KS; ++k) v += partial[(int64_t)k * M * N + idx];
-    y[(int64_t)m * ys + n] = f2h_bits(pin_f32(v));
+    const int G8 = N / 8;
+    if (idx >= (int64_t)M * G8) return;
+    const int m = (int)(idx / G8), n = (int)(idx % G8) * 8;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bias ? h2f(bias, n + e) : 0.0f;
+    const float* p = partial + (int64_t)m * N + n;
+    const int64_t stride = (int64_t)M * N;
+    if constexpr (KS > 0) {
+        float4v a[KS][2];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            a[k][0] = *reinterpret_cast<const float4v*>(p + k * stride);
+            a[k][1] = *reinterpret_cast<const float4v*>(p + k * stride + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] += a[k][e / 4][e % 4];
+    } else {
+        for (int k = 0; k < splits; ++k) {
+            const float4v a0 = *reinterpret_cast<const float4v*>(p + k * stride);
+            const float4v a1 = *reinterpret_cast<const float4v*>(p + k * stride + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] += a0[e];
+                v[4 + e] += a1[e];
+            }
+        }
+    }
+    uint16_t* yr = y + (int64_t)m * ys + n;
+    if ((reinterpret_cast<uintptr_t>(yr) & 15) == 0) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = (uint32_t)f2h_bits(pin_f32(v[2 * e])) | ((uint32_t)f2h_bits(pin_f32(v[2 * e + 1])) << 16);
+        *reinterpret_cast<uint4*>(yr) = uint4{w[0], w[1], w[2], w[3]};
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) yr[e] = f2h_bits(pin_f32(v[e]));
+    }
 }
 
 // Largest M handled by the VALU GEMV; above it the MFMA kernel runs.
@@ -783,9 +824,14 @@ static void launch_mfma_mt(int MT, const uint16_t* x, int64_t xs, int M, const u
 
 static void launch_reduce(const float* partial, int KS, int M, int N, const uint16_t* b, uint16_t* y, int64_t ys,
                           hipStream_t st) {
-    const int64_t total = (int64_t)M * N;
-    hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, partial, KS, M, N, b, y,
-                       ys);
+    const dim3 grid((unsigned)ceil_div((int64_t)M * (N / 8), 256)), block(256);
+    switch (KS) {
+        case 2: hipLaunchKernelGGL(reduce_kernel<2>, grid, block, 0, st, partial, KS, M, N, b, y, ys); break;
+        case 4: hipLaunchKernelGGL(reduce_kernel<4>, grid, block, 0, st, partial, KS, M, N, b, y, ys); break;
+        case 8: hipLaunchKernelGGL(reduce_kernel<8>, grid, block, 0, st, partial, KS, M, N, b, y, ys); break;
+        case 16: hipLaunchKernelGGL(reduce_kernel<16>, grid, block, 0, st, partial, KS, M, N, b, y, ys); break;
+        default: hipLaunchKernelGGL(reduce_kernel<0>, grid, block, 0, st, partial, KS, M, N, b, y, ys); break;
+    }
 }
 
 }  // namespace w8a16
