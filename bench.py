@@ -69,7 +69,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=None, help="rows (default 32; 128 for --workload prefix-batch)")
-    ap.add_argument("--workload", choices=["all", "decode", "prefix-batch", "linear-sweep", "attention", "qwen"],
+    ap.add_argument("--workload", choices=["all", "decode", "prefix-batch", "linear-sweep", "attention", "qwen",
+                                           "probes"],
                     default="all",
                     help="all: the headline step with every config in 'configs' (default). decode: the headline "
                          "step alone. prefix-batch: config 5. linear-sweep: configs 1 and 4. attention: config 2 "
@@ -652,6 +653,64 @@ def config14_linears(args) -> tuple[dict, dict]:
 
 
 # ---------------------------------------------------------------------------------------------
+# Calibration probes: what one CU streams, and what a launch costs inside a graph
+# ---------------------------------------------------------------------------------------------
+STREAM_PROBE_SHAPES = ((1, 64 << 10), (1, 1 << 20), (32, 256 << 10), (256, 64 << 10), (256, 256 << 10),
+                       (512, 256 << 10), (512, 1 << 20))
+LAUNCH_PROBE_SHAPES = ((0, 256), (16 * 256, 256), (4 << 20, 256), (16 << 20, 256), (64 << 20, 1024))
+
+
+def calibration_probes(args) -> dict:
+    """The tables the kernels' shapes were chosen from, measured on this GPU.
+
+    * stream: G workgroups of T threads each read their own contiguous run of B bytes
+      (``mx_stream_probe``: non-temporal 16-byte loads, 4 in flight per thread), 20 launches per graph
+      at distinct offsets of a 2 GiB buffer (a run is not re-read until 2 GiB later, past the 256 MB
+      MALL); per launch us and GB/s.
+    * launch: a graph of 100 launches of ``mx_launch_probe`` that do nothing or write the given bytes
+      (equal shares per workgroup); per launch us.
+    """
+    import torch
+
+    from runtime_amd.phase2 import _hip
+
+    lib = _hip.load()
+    dev = torch.device("cuda:0")
+    span_total = 2 << 30
+    buf = torch.empty(span_total, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    launches = 20
+    stream = []
+    for wgs, per in STREAM_PROBE_SHAPES:
+        span = wgs * per
+        n_off = max(1, min(launches, span_total // span))
+        for threads in (256, 512, 1024):
+            def run(wgs=wgs, per=per, span=span, n_off=n_off, threads=threads):
+                st = _hip.stream_handle(dev)
+                for i in range(launches):
+                    _hip.check(lib.mx_stream_probe(buf.data_ptr(), span_total, (i % n_off) * span, per, wgs, threads,
+                                                   sink.data_ptr(), st), "mx_stream_probe")
+            t = graph_time(run, launches)
+            stream.append({"workgroups": wgs, "bytes_per_workgroup": per, "threads": threads,
+                           "us": round(t * 1e6, 2), "gbps": round(span / t / 1e9, 1)})
+    del buf
+    torch.cuda.empty_cache()
+    dst = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    launch = []
+    for nbytes, wgs in LAUNCH_PROBE_SHAPES:
+        def run(nbytes=nbytes, wgs=wgs):
+            st = _hip.stream_handle(dev)
+            for _ in range(100):
+                _hip.check(lib.mx_launch_probe(dst.data_ptr(), dst.numel(), nbytes, wgs, st), "mx_launch_probe")
+        t = graph_time(run, 100)
+        launch.append({"bytes_written": nbytes, "workgroups": wgs, "us": round(t * 1e6, 2)})
+    return {"stream": stream, "launch": launch,
+            "what": "mx_stream_probe (per-workgroup contiguous runs, 20 launches per graph over 2 GiB) and "
+                    "mx_launch_probe (graphs of 100 launches)"}
+
+
+# ---------------------------------------------------------------------------------------------
 # Config 3: the Qwen2-0.5B-shaped step
 # ---------------------------------------------------------------------------------------------
 def config3_qwen(args) -> dict:
@@ -942,6 +1001,11 @@ def main() -> int:
                           "value": c1["gbps"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
                           "dtype": DTYPE, "data": DATA, "config": {"workload": c1["workload"]},
                           "config1": c1, "config4": c4}), flush=True)
+        return 0
+    if args.workload == "probes":
+        pr = calibration_probes(args)
+        print(json.dumps({"metric": "calibration probes (per-CU streaming, launch floor in a HIP graph)", "n_gpus": 1,
+                          "data": DATA, **pr}), flush=True)
         return 0
     if args.workload == "qwen":
         c3 = config3_qwen(args)

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 15
+#define MX_ABI_VERSION 16
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -245,6 +245,24 @@ int mx_kv_gather_probe(const uint16_t* k, const uint16_t* v, int64_t kv_sblk, in
                        const int32_t* block_tables, int64_t bt_sb, int32_t max_blocks, const int32_t* seq_lens,
                        int32_t B, int32_t Hkv, int32_t D, int32_t block_size, int32_t num_pool_blocks, int32_t mode,
                        int32_t* sink, void* stream);
+
+/* Calibration probe (no reference counterpart; used by bench.py --workload
+ * probes): `workgroups` workgroups of `threads` threads (256, 512 or 1024) each
+ * read their own contiguous run of bytes_per_wg bytes of src, starting at
+ * byte `offset` (runs back to back), with non-temporal 16-byte loads, 4 in
+ * flight per thread. The runs must lie inside the src_bytes-byte buffer; sizes
+ * and offset are multiples of 16. Nothing is written except, with negligible
+ * odds, a checksum to sink[0] (one int32 of device memory). */
+int mx_stream_probe(const void* src, int64_t src_bytes, int64_t offset, int64_t bytes_per_wg, int32_t workgroups,
+                    int32_t threads, int32_t* sink, void* stream);
+
+/* Calibration probe (no reference counterpart; used by bench.py --workload
+ * probes): one launch of `workgroups` workgroups of 256 threads that does
+ * nothing (bytes == 0; dst may be NULL) or writes `bytes` bytes of dst, an
+ * equal contiguous share per workgroup (bytes a multiple of 16 x workgroups,
+ * at most dst_bytes). Its cost inside a HIP graph is the floor under every
+ * small launch of the decode step. */
+int mx_launch_probe(void* dst, int64_t dst_bytes, int64_t bytes, int32_t workgroups, void* stream);
 
 /* Byte offset of the int32 error word inside a paged-attention workspace
  * (nonzero after a call that met an out-of-range block id). Reading it needs a

@@ -20,7 +20,7 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "runtime_amd", "libmxdecode.so")
-SOURCES = ["status.hip", "w8a16.hip", "paged_attn.hip", "decode_glue.hip", "qkv_rope.hip"]
+SOURCES = ["status.hip", "w8a16.hip", "paged_attn.hip", "decode_glue.hip", "qkv_rope.hip", "probes.hip"]
 ARCH = os.environ.get("MX_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in generated code.

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -92,6 +92,8 @@ SIGNATURES = {
         [_p, _i32, _p, _p, _i64, _p, _i32, _i32, ctypes.c_float, _p, _i64, _p, _i64, _p],
     ),
     "mx_silu_mul": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _i64, _p]),
+    "mx_stream_probe": (ctypes.c_int, [_p, _i64, _i64, _i64, _i32, _i32, _p, _p]),
+    "mx_launch_probe": (ctypes.c_int, [_p, _i64, _i64, _i32, _p]),
 }
 
 _lib = None

@@ -161,3 +161,19 @@ def test_python_wrappers_refuse_cpu_tensors():
         Int8Linear(100, 64)
     with pytest.raises(ValueError):
         Int8Linear.from_linear(torch.nn.Linear(64, 16), device="cpu")
+
+
+def test_calibration_probes_reject_bad_arguments():
+    """The probes check every range on the host before a launch (nothing here reaches the device)."""
+    lib = _hip.load()
+    fake = ctypes.c_void_p(1 << 20)
+    _status(lib.mx_stream_probe(None, 1 << 20, 0, 4096, 1, 256, fake, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_stream_probe(fake, 1 << 20, 0, 4096, 1, 256, None, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_stream_probe(fake, 1 << 20, 0, 4008, 1, 256, fake, None), _hip.MX_ERR_INVALID)  # not 16-byte
+    _status(lib.mx_stream_probe(fake, 1 << 20, 16, 1 << 20, 1, 256, fake, None), _hip.MX_ERR_INVALID)  # past the end
+    _status(lib.mx_stream_probe(fake, 1 << 20, 0, 4096, 0, 256, fake, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_stream_probe(fake, 1 << 20, 0, 4096, 1, 128, fake, None), _hip.MX_ERR_UNSUPPORTED)
+    _status(lib.mx_launch_probe(fake, 1 << 20, 100, 2, None), _hip.MX_ERR_INVALID)  # not 16 x workgroups
+    _status(lib.mx_launch_probe(fake, 1 << 20, 2 << 20, 2, None), _hip.MX_ERR_INVALID)  # past the end
+    _status(lib.mx_launch_probe(None, 1 << 20, 4096, 2, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_launch_probe(None, 0, 0, 0, None), _hip.MX_ERR_INVALID)
