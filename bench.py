@@ -705,9 +705,89 @@ def calibration_probes(args) -> dict:
                 _hip.check(lib.mx_launch_probe(dst.data_ptr(), dst.numel(), nbytes, wgs, st), "mx_launch_probe")
         t = graph_time(run, 100)
         launch.append({"bytes_written": nbytes, "workgroups": wgs, "us": round(t * 1e6, 2)})
-    return {"stream": stream, "launch": launch,
-            "what": "mx_stream_probe (per-workgroup contiguous runs, 20 launches per graph over 2 GiB) and "
-                    "mx_launch_probe (graphs of 100 launches)"}
+    del dst
+    torch.cuda.empty_cache()
+    gather = gather_sweep(args)
+    return {"stream": stream, "launch": launch, "gather": gather,
+            "what": "mx_stream_probe (per-workgroup contiguous runs, 20 launches per graph over 2 GiB), "
+                    "mx_launch_probe (graphs of 100 launches), mx_run_gather_probe / mx_kv_gather_probe over "
+                    "config 2's K/V runs (one call per layer of a 32-layer pool)"}
+
+
+# (waves, runs in flight, streaming, load pattern: 0 1 KiB contiguous, 1/2 the attention kernel's operand loads)
+GATHER_SWEEP = ((1024, 2, 1, 0), (1024, 3, 1, 0), (2048, 1, 1, 0), (2048, 2, 1, 0), (2048, 3, 1, 0), (4096, 2, 1, 0),
+                (4096, 4, 1, 0), (2048, 2, 0, 0), (1024, 3, 0, 0), (2048, 2, 1, 1), (2048, 2, 1, 2), (1024, 2, 1, 2))
+
+
+def gather_sweep(args) -> dict:
+    """Config 2's K/V reads (torch.manual_seed(0) contexts and tables, the bench's interleaved 16384-block
+    pool of 32 layers) without the math: each (block, kv-head)'s K and V runs are one 8 KiB run of the
+    pool. W waves take equal shares of a layer's runs, R runs in flight per wave, streaming or default
+    loads (``mx_run_gather_probe``), one call per layer; beside it the attention kernel's own partition
+    and loads (``mx_kv_gather_probe`` mode 0) and whole-block workgroups (mode 1)."""
+    import torch
+
+    from runtime_amd.phase2 import _hip
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    lib = _hip.load()
+    dev = torch.device("cuda:0")
+    B, Hkv, D, bs, nb, layers = 32, 8, 128, 16, 16384, 32
+    pool = GpuKVBlockPool(num_blocks=nb, block_size_tokens=bs, num_layers=layers, num_kv_heads=Hkv, head_dim=D,
+                          dtype=torch.float16, device=dev)
+    pool._ensure_pools()
+    k0 = pool.k_layer_view(0)
+    if pool.v_layer_view(0).data_ptr() - k0.data_ptr() != bs * D * 2:
+        raise RuntimeError("the gather sweep needs the interleaved pool (K and V runs of a block adjacent)")
+    torch.manual_seed(0)
+    lens = torch.randint(128, 4097, (B,))
+    perm = torch.randperm(nb)
+    nblk = [math.ceil(int(x) / bs) for x in lens]
+    tables = torch.zeros(B, max(nblk), dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(nblk):
+        tables[b, :n] = perm[used:used + n].to(torch.int32)
+        used += n
+    ids = torch.cat([tables[b, :n] for b, n in enumerate(nblk)]).long()  # row-major, as the segments run
+    base = pool._k_pool.data_ptr()
+    base_bytes = pool._k_pool.untyped_storage().nbytes()  # the whole pool (K and V of every layer)
+    sblk, shead = k0.stride(0) * 2, k0.stride(1) * 2
+    offs = []
+    for li in range(layers):
+        lo = pool.k_layer_view(li).data_ptr() - base
+        heads = torch.arange(Hkv, dtype=torch.long) * shead
+        offs.append((lo + ids[:, None] * sblk + heads[None, :]).flatten().to(dev))
+    n_runs = int(offs[0].numel())
+    run_bytes = 2 * bs * D * 2
+    sink = torch.zeros(2, dtype=torch.int32, device=dev)
+    kv_bytes = n_runs * run_bytes
+    rows = []
+    for waves, r, streaming, pattern in GATHER_SWEEP:
+        def run(waves=waves, r=r, streaming=streaming, pattern=pattern):
+            st = _hip.stream_handle(dev)
+            for li in range(layers):
+                _hip.check(lib.mx_run_gather_probe(base, base_bytes, offs[li].data_ptr(), n_runs, run_bytes, waves, r,
+                                                   streaming, pattern, sink.data_ptr(), st), "mx_run_gather_probe")
+        t = graph_time(run, layers, reps=max(2, args.kernel_steps))
+        rows.append({"waves": waves, "runs_in_flight": r, "loads": "streaming" if streaming else "default",
+                     "pattern": ("1 KiB contiguous", "attention operands, streaming",
+                                 "attention operands, K first halves default")[pattern],
+                     "us": round(t * 1e6, 2), "gbps": round(kv_bytes / t / 1e9, 1), "frac": frac(kv_bytes / t / 1e9)})
+    td, ld = tables.to(dev), lens.to(device=dev, dtype=torch.int32)
+    kernel = {}
+    for mode, name in ((0, "attention_partition"), (1, "whole_blocks")):
+        def probe(mode=mode):
+            for li in range(layers):
+                k, v = pool.k_layer_view(li), pool.v_layer_view(li)
+                _hip.check(lib.mx_kv_gather_probe(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), td.data_ptr(),
+                                                  td.stride(0), td.shape[1], ld.data_ptr(), B, Hkv, D, bs, nb, mode,
+                                                  sink.data_ptr(), _hip.stream_handle(dev)), "mx_kv_gather_probe")
+        t = graph_time(probe, layers, reps=max(2, args.kernel_steps))
+        kernel[name] = {"us": round(t * 1e6, 2), "gbps": round(kv_bytes / t / 1e9, 1), "frac": frac(kv_bytes / t / 1e9)}
+    del pool
+    torch.cuda.empty_cache()
+    return {"runs_per_call": n_runs, "run_bytes": run_bytes, "kv_bytes_per_call": kv_bytes, "sweep": rows,
+            "kv_gather_probe": kernel}
 
 
 # ---------------------------------------------------------------------------------------------

@@ -264,6 +264,23 @@ int mx_stream_probe(const void* src, int64_t src_bytes, int64_t offset, int64_t 
  * small launch of the decode step. */
 int mx_launch_probe(void* dst, int64_t dst_bytes, int64_t bytes, int32_t workgroups, void* stream);
 
+/* Calibration probe (no reference counterpart; used by bench.py --workload
+ * probes): the gather of paged attention without its math. `waves` waves split
+ * the n_runs byte offsets (int64 device array) into equal contiguous shares; a
+ * wave reads each run of run_bytes (4096 or 8192) bytes from base as coalesced
+ * 1 KiB loads, in_flight runs at a time (8192: 1, 2, 3, 4 or 6; 4096: 2 or 4),
+ * non-temporal when `streaming` is nonzero (pattern 0). Patterns 1 and 2
+ * (8192-byte runs, 2 in flight, streaming) read each run as the paged-attention
+ * kernel reads a 16-token K tile of head_dim 128 and its V tile: K as 4 load
+ * instructions of 16 rows x 64 bytes, V as 4 of 4 rows x 256 bytes; pattern 2
+ * loads the first half of each K line with the default policy, as the kernel
+ * does. An offset outside [0, base_bytes - run_bytes] reads run 0 instead
+ * (offsets round down to 16 bytes), so no list reads outside the buffer.
+ * Nothing is written except, with negligible odds, a checksum to sink[0]. */
+int mx_run_gather_probe(const void* base, int64_t base_bytes, const int64_t* offsets, int64_t n_runs,
+                        int32_t run_bytes, int32_t waves, int32_t in_flight, int32_t streaming, int32_t pattern,
+                        int32_t* sink, void* stream);
+
 /* Byte offset of the int32 error word inside a paged-attention workspace
  * (nonzero after a call that met an out-of-range block id). Reading it needs a
  * device-to-host copy by the caller; clearing it is the caller's choice. */

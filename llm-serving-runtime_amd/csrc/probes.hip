@@ -44,6 +44,63 @@ __global__ __launch_bounds__(256) void write_kernel(uint4* __restrict__ dst, int
     for (int64_t i = threadIdx.x; i < chunks_per_wg; i += 256) p[i] = uint4{v, v, v, v};
 }
 
+// Wave w of `waves` reads the runs [w * n / waves, (w + 1) * n / waves) of a list of byte offsets
+// into base, each run RUN16 16-byte chunks read as RUN16 / 64 coalesced 1 KiB loads (lane l reads
+// chunks l, l + 64, ...), R runs in flight per wave; STREAM selects non-temporal loads. The gather
+// pattern of paged attention without its math: which runs, how many in flight, what policy.
+// An offset outside [0, base_bytes - run bytes] reads run 0 instead, and offsets are rounded down to
+// 16 bytes, so no offset list makes the probe read outside the buffer.
+// PATTERN 0: 1 KiB contiguous per load instruction. PATTERN 1 and 2 (8 KiB runs: a 16-token K tile of
+// head_dim 128 followed by its V tile, the interleaved pool): the paged-attention kernel's operand
+// loads, K as 4 instructions of 16 token rows x 64 bytes (lane (r, g) = (l % 16, l / 16) reads row r,
+// bytes 64 kk + 16 g) and V as 4 instructions of 4 token rows x 256 bytes (row 4 g + jj, bytes 16 r);
+// 1 streams every load, 2 loads the first half of each K line with the default policy, as the kernel.
+template <int RUN16, int R, bool STREAM, int PATTERN = 0>
+__global__ __launch_bounds__(256) void run_gather_kernel(const u32x4v* __restrict__ base, int64_t base_bytes,
+                                                         const int64_t* __restrict__ offsets, int64_t n_runs,
+                                                         int waves, int32_t* __restrict__ sink) {
+    static_assert(PATTERN == 0 || RUN16 == 512, "operand patterns: 8 KiB runs");
+    constexpr int L = RUN16 / 64;  // load instructions per run
+    const int wave = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    if (wave >= waves) return;
+    const int64_t lo = n_runs * wave / waves, hi = n_runs * (wave + 1) / waves;
+    uint32_t acc = 0;
+    for (int64_t r0 = lo; r0 < hi; r0 += R) {
+        u32x4v v[R][L];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t ri = r0 + r < hi ? r0 + r : hi - 1;
+            int64_t off = offsets[ri];
+            if ((uint64_t)off > (uint64_t)(base_bytes - RUN16 * 16)) off = 0;
+            if constexpr (PATTERN == 0) {
+                const u32x4v* p = base + (off >> 4) + lane;
+#pragma unroll
+                for (int j = 0; j < L; ++j) {
+                    if constexpr (STREAM) v[r][j] = __builtin_nontemporal_load(p + 64 * j);
+                    else v[r][j] = p[64 * j];
+                }
+            } else {
+                const int rr = lane & 15, g = lane >> 4;
+                const u32x4v* k = base + (off >> 4) + rr * 16 + g;         // row rr, 16-byte chunk g
+                const u32x4v* vv = base + (off >> 4) + 256 + g * 64 + rr;  // V tile: row 4 g, chunk rr
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    if (PATTERN == 2 && (kk & 1) == 0) v[r][kk] = k[4 * kk];
+                    else v[r][kk] = __builtin_nontemporal_load(k + 4 * kk);
+                }
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) v[r][4 + jj] = __builtin_nontemporal_load(vv + 16 * jj);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < L; ++j) acc ^= v[r][j].x ^ v[r][j].y ^ v[r][j].z ^ v[r][j].w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = (int32_t)acc;
+}
+
 }  // namespace probe
 }  // namespace mx
 
@@ -89,4 +146,43 @@ extern "C" int mx_launch_probe(void* dst, int64_t dst_bytes, int64_t bytes, int3
                            bytes / 16 / workgroups);
     }
     return check_launch(what);
+}
+
+extern "C" int mx_run_gather_probe(const void* base, int64_t base_bytes, const int64_t* offsets, int64_t n_runs,
+                                   int32_t run_bytes, int32_t waves, int32_t in_flight, int32_t streaming,
+                                   int32_t pattern, int32_t* sink, void* stream) {
+    const char* what = "mx_run_gather_probe";
+    clear_error();
+    if (!base || !offsets || !sink) return fail(MX_ERR_NULL, "%s: null pointer", what);
+    if (n_runs <= 0 || waves <= 0 || base_bytes < run_bytes)
+        return fail(MX_ERR_INVALID, "%s: need runs, waves > 0 and a buffer of at least one run", what);
+    if (run_bytes != 4096 && run_bytes != 8192) return fail(MX_ERR_UNSUPPORTED, "%s: run_bytes 4096 or 8192", what);
+    if (!aligned(base, 16)) return fail(MX_ERR_ALIGNMENT, "%s: base must be 16-byte aligned", what);
+    hipStream_t st = as_stream(stream);
+    const auto* b = static_cast<const probe::u32x4v*>(base);
+    const dim3 grid((unsigned)ceil_div(waves, 4)), block(256);
+    if (pattern == 1 || pattern == 2) {
+        if (run_bytes != 8192) return fail(MX_ERR_UNSUPPORTED, "%s: the operand patterns take 8192-byte runs", what);
+        if (in_flight != 2) return fail(MX_ERR_UNSUPPORTED, "%s: the operand patterns take 2 runs in flight", what);
+        if (pattern == 1)
+            hipLaunchKernelGGL((probe::run_gather_kernel<512, 2, true, 1>), grid, block, 0, st, b, base_bytes, offsets,
+                               n_runs, waves, sink);
+        else
+            hipLaunchKernelGGL((probe::run_gather_kernel<512, 2, true, 2>), grid, block, 0, st, b, base_bytes, offsets,
+                               n_runs, waves, sink);
+        return check_launch(what);
+    }
+    if (pattern != 0) return fail(MX_ERR_INVALID, "%s: pattern must be 0, 1 or 2", what);
+#define MX_RG(RB, R, S)                                                                                          \
+    if (run_bytes == RB && in_flight == R && (streaming != 0) == S) {                                           \
+        hipLaunchKernelGGL((probe::run_gather_kernel<RB / 16, R, S>), grid, block, 0, st, b, base_bytes, offsets,  \
+                           n_runs, waves, sink);                                                                \
+        return check_launch(what);                                                                              \
+    }
+    MX_RG(8192, 1, true) MX_RG(8192, 2, true) MX_RG(8192, 3, true) MX_RG(8192, 4, true) MX_RG(8192, 6, true)
+    MX_RG(8192, 1, false) MX_RG(8192, 2, false) MX_RG(8192, 3, false) MX_RG(8192, 4, false) MX_RG(8192, 6, false)
+    MX_RG(4096, 2, true) MX_RG(4096, 4, true) MX_RG(4096, 2, false) MX_RG(4096, 4, false)
+#undef MX_RG
+    return fail(MX_ERR_UNSUPPORTED, "%s: in_flight %d not built for %d-byte runs (8192: 1, 2, 3, 4, 6; 4096: 2, 4)",
+                what, in_flight, run_bytes);
 }

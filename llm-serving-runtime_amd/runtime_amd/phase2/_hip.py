@@ -94,6 +94,7 @@ SIGNATURES = {
     "mx_silu_mul": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _i64, _p]),
     "mx_stream_probe": (ctypes.c_int, [_p, _i64, _i64, _i64, _i32, _i32, _p, _p]),
     "mx_launch_probe": (ctypes.c_int, [_p, _i64, _i64, _i32, _p]),
+    "mx_run_gather_probe": (ctypes.c_int, [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p]),
 }
 
 _lib = None
