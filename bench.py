@@ -716,7 +716,8 @@ def calibration_probes(args) -> dict:
 
 # (waves, runs in flight, streaming, load pattern: 0 1 KiB contiguous, 1/2 the attention kernel's operand loads)
 GATHER_SWEEP = ((1024, 2, 1, 0), (1024, 3, 1, 0), (2048, 1, 1, 0), (2048, 2, 1, 0), (2048, 3, 1, 0), (4096, 2, 1, 0),
-                (4096, 4, 1, 0), (2048, 2, 0, 0), (1024, 3, 0, 0), (2048, 2, 1, 1), (2048, 2, 1, 2), (1024, 2, 1, 2))
+                (4096, 4, 1, 0), (2048, 2, 0, 0), (1024, 3, 0, 0), (2048, 2, 1, 1), (2048, 2, 1, 2), (1024, 2, 1, 2),
+                (2048, 2, 1, 3), (1024, 2, 1, 3), (2048, 2, 1, 4), (1024, 2, 1, 4))
 
 
 def gather_sweep(args) -> dict:
@@ -771,7 +772,9 @@ def gather_sweep(args) -> dict:
         t = graph_time(run, layers, reps=max(2, args.kernel_steps))
         rows.append({"waves": waves, "runs_in_flight": r, "loads": "streaming" if streaming else "default",
                      "pattern": ("1 KiB contiguous", "attention operands, streaming",
-                                 "attention operands, K first halves default")[pattern],
+                                 "attention operands, K first halves default",
+                                 "attention operands, K staged through LDS in whole rows",
+                                 "K staged through LDS, rows permuted so V loads are 1 KiB contiguous")[pattern],
                      "us": round(t * 1e6, 2), "gbps": round(kv_bytes / t / 1e9, 1), "frac": frac(kv_bytes / t / 1e9)})
     td, ld = tables.to(dev), lens.to(device=dev, dtype=torch.int32)
     kernel = {}

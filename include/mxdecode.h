@@ -274,7 +274,10 @@ int mx_launch_probe(void* dst, int64_t dst_bytes, int64_t bytes, int32_t workgro
  * kernel reads a 16-token K tile of head_dim 128 and its V tile: K as 4 load
  * instructions of 16 rows x 64 bytes, V as 4 of 4 rows x 256 bytes; pattern 2
  * loads the first half of each K line with the default policy, as the kernel
- * does. An offset outside [0, base_bytes - run_bytes] reads run 0 instead
+ * does. Pattern 3 stages K through LDS with global->LDS loads of 4 whole token
+ * rows each, then reads pattern 1's K operand layout back from LDS; pattern 4
+ * also permutes the operand rows so that each V load reads 4 consecutive token
+ * rows (1 KiB contiguous). An offset outside [0, base_bytes - run_bytes] reads run 0 instead
  * (offsets round down to 16 bytes), so no list reads outside the buffer.
  * Nothing is written except, with negligible odds, a checksum to sink[0]. */
 int mx_run_gather_probe(const void* base, int64_t base_bytes, const int64_t* offsets, int64_t n_runs,

@@ -55,6 +55,11 @@ __global__ __launch_bounds__(256) void write_kernel(uint4* __restrict__ dst, int
 // loads, K as 4 instructions of 16 token rows x 64 bytes (lane (r, g) = (l % 16, l / 16) reads row r,
 // bytes 64 kk + 16 g) and V as 4 instructions of 4 token rows x 256 bytes (row 4 g + jj, bytes 16 r);
 // 1 streams every load, 2 loads the first half of each K line with the default policy, as the kernel.
+// PATTERN 3: K through LDS, V as in 1: 4 streaming global->LDS loads per K tile, each 4 whole token rows
+// (1 KiB, lane l of load i carries row 4 i + l / 16, 16-byte chunk (l % 16) ^ (row % 16)), then the
+// operand layout of 1 read back from LDS (the xor makes the 16 rows of a read hit distinct banks).
+// PATTERN 4: K as in 3, with operand row r holding token 4 (r % 4) + r / 4, so that the tokens a V load
+// needs (4 jj + g for lane group g) are 4 consecutive rows: each V load reads 1 KiB contiguous.
 template <int RUN16, int R, bool STREAM, int PATTERN = 0>
 __global__ __launch_bounds__(256) void run_gather_kernel(const u32x4v* __restrict__ base, int64_t base_bytes,
                                                          const int64_t* __restrict__ offsets, int64_t n_runs,
@@ -63,6 +68,8 @@ __global__ __launch_bounds__(256) void run_gather_kernel(const u32x4v* __restric
     constexpr int L = RUN16 / 64;  // load instructions per run
     const int wave = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
+    // PATTERN 3, 4: each wave's K tiles (R of 256 16-byte chunks); unused by the other patterns.
+    __shared__ u32x4v k_lds[PATTERN >= 3 ? 4 * R * 256 : 1];
     if (wave >= waves) return;
     const int64_t lo = n_runs * wave / waves, hi = n_runs * (wave + 1) / waves;
     uint32_t acc = 0;
@@ -80,6 +87,21 @@ __global__ __launch_bounds__(256) void run_gather_kernel(const u32x4v* __restric
                     if constexpr (STREAM) v[r][j] = __builtin_nontemporal_load(p + 64 * j);
                     else v[r][j] = p[64 * j];
                 }
+            } else if constexpr (PATTERN >= 3) {
+                u32x4v* kw = k_lds + ((threadIdx.x >> 6) * R + r) * 256;
+                const int row_in = lane >> 4, ch = lane & 15;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 4 * i + row_in;
+                    __builtin_amdgcn_global_load_lds(static_cast<const void*>(base + (off >> 4) + row * 16 + (ch ^ row)),
+                                                     (__attribute__((address_space(3))) void*)(kw + 64 * i),
+                                                     16, 0, 2);
+                }
+                const int rr = lane & 15, g = lane >> 4;
+                // V row 4 g + jj (3) or 4 jj + g (4), chunk rr
+                const u32x4v* vv = base + (off >> 4) + 256 + (PATTERN == 3 ? g * 64 : g * 16) + rr;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) v[r][4 + jj] = __builtin_nontemporal_load(vv + (PATTERN == 3 ? 16 : 64) * jj);
             } else {
                 const int rr = lane & 15, g = lane >> 4;
                 const u32x4v* k = base + (off >> 4) + rr * 16 + g;         // row rr, 16-byte chunk g
@@ -93,10 +115,27 @@ __global__ __launch_bounds__(256) void run_gather_kernel(const u32x4v* __restric
                 for (int jj = 0; jj < 4; ++jj) v[r][4 + jj] = __builtin_nontemporal_load(vv + 16 * jj);
             }
         }
+        if constexpr (PATTERN >= 3) {
+            // The global->LDS loads are not tracked by the compiler's waits: wait for every load of
+            // the round (vmcnt(0)) before reading K back; the reads of a round finish (their values
+            // are consumed below) before the next round's loads overwrite the buffers.
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __builtin_amdgcn_sched_barrier(0);
+            const int rr = lane & 15, g = lane >> 4;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const u32x4v* kw = k_lds + ((threadIdx.x >> 6) * R + r) * 256;
+                const int t = PATTERN == 3 ? rr : 4 * (rr & 3) + (rr >> 2);  // the token of operand row rr
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) v[r][kk] = kw[64 * (t >> 2) + 16 * (t & 3) + ((g + 4 * kk) ^ t)];
+            }
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int j = 0; j < L; ++j) acc ^= v[r][j].x ^ v[r][j].y ^ v[r][j].z ^ v[r][j].w;
+        if constexpr (PATTERN >= 3) __builtin_amdgcn_sched_barrier(0);
     }
     if (acc == 0x9e3779b9u) sink[0] = (int32_t)acc;
 }
@@ -161,18 +200,24 @@ extern "C" int mx_run_gather_probe(const void* base, int64_t base_bytes, const i
     hipStream_t st = as_stream(stream);
     const auto* b = static_cast<const probe::u32x4v*>(base);
     const dim3 grid((unsigned)ceil_div(waves, 4)), block(256);
-    if (pattern == 1 || pattern == 2) {
+    if (pattern >= 1 && pattern <= 4) {
         if (run_bytes != 8192) return fail(MX_ERR_UNSUPPORTED, "%s: the operand patterns take 8192-byte runs", what);
         if (in_flight != 2) return fail(MX_ERR_UNSUPPORTED, "%s: the operand patterns take 2 runs in flight", what);
         if (pattern == 1)
             hipLaunchKernelGGL((probe::run_gather_kernel<512, 2, true, 1>), grid, block, 0, st, b, base_bytes, offsets,
+                               n_runs, waves, sink);
+        else if (pattern == 3)
+            hipLaunchKernelGGL((probe::run_gather_kernel<512, 2, true, 3>), grid, block, 0, st, b, base_bytes, offsets,
+                               n_runs, waves, sink);
+        else if (pattern == 4)
+            hipLaunchKernelGGL((probe::run_gather_kernel<512, 2, true, 4>), grid, block, 0, st, b, base_bytes, offsets,
                                n_runs, waves, sink);
         else
             hipLaunchKernelGGL((probe::run_gather_kernel<512, 2, true, 2>), grid, block, 0, st, b, base_bytes, offsets,
                                n_runs, waves, sink);
         return check_launch(what);
     }
-    if (pattern != 0) return fail(MX_ERR_INVALID, "%s: pattern must be 0, 1 or 2", what);
+    if (pattern != 0) return fail(MX_ERR_INVALID, "%s: pattern must be 0 to 4", what);
 #define MX_RG(RB, R, S)                                                                                          \
     if (run_bytes == RB && in_flight == R && (streaming != 0) == S) {                                           \
         hipLaunchKernelGGL((probe::run_gather_kernel<RB / 16, R, S>), grid, block, 0, st, b, base_bytes, offsets,  \

@@ -37,7 +37,7 @@ def test_stream_and_gather_probes_write_nothing():
     offs = (torch.randperm(1000, device=DEV)[:300] * 8192).to(torch.int64)
     offs[0] = -1  # out of range: read as run 0
     offs[1] = 1 << 40
-    for pattern, inflight, streaming in ((0, 1, 1), (0, 2, 0), (0, 3, 1), (0, 6, 1), (1, 2, 1), (2, 2, 1)):
+    for pattern, inflight, streaming in ((0, 1, 1), (0, 2, 0), (0, 3, 1), (0, 6, 1), (1, 2, 1), (2, 2, 1), (3, 2, 1), (4, 2, 1)):
         _hip.check(lib.mx_run_gather_probe(src.data_ptr(), src.numel(), offs.data_ptr(), offs.numel(), 8192, 64,
                                            inflight, streaming, pattern, sink.data_ptr(), st), "mx_run_gather_probe")
     torch.cuda.synchronize()
