@@ -83,6 +83,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-steps", type=int, default=5, help="graph replays per kernel family for kernel timing")
     ap.add_argument("--prefix-steps", type=int, default=40, help="timed steps of config 5")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--fuse-mlp", action="store_true",
+                    help="run gate||up and down as one launch where the shape takes it (Int8DecodeModel.fuse_mlp)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="REPS",
                     help="instead of the bench: REPS rounds of one kernel family's launches of the headline step "
@@ -296,7 +298,7 @@ class Decoder:
     """A random-init int8 decoder, its paged pool (random K/V) and a batch of seeded contexts."""
 
     def __init__(self, shape, batch: int, lo: int, hi: int, pool_blocks: int, headroom: int, layers=None, seed=0,
-                 kv_layout: str = "interleaved"):
+                 kv_layout: str = "interleaved", fuse_mlp: bool = False):
         import torch
 
         from runtime_amd.phase2.decode_step import Int8DecodeModel, make_contexts
@@ -308,6 +310,7 @@ class Decoder:
         t0 = time.perf_counter()
         self.lens, self.tables = make_contexts(batch, lo, hi, self.bs, pool_blocks, headroom=headroom, seed=seed)
         self.model = Int8DecodeModel(shape, device=self.dev, seed=seed, layers=self.n_layers)
+        self.model.fuse_mlp = fuse_mlp
         self.pool = GpuKVBlockPool(num_blocks=pool_blocks, block_size_tokens=self.bs, num_layers=self.n_layers,
                                    num_kv_heads=shape.kv_heads, head_dim=shape.head_dim, dtype=torch.float16,
                                    device=self.dev, kv_layout=kv_layout)
@@ -344,7 +347,7 @@ def family_launches(d: Decoder) -> dict:
     import torch
 
     from runtime_amd.phase2.decode_glue import qkv_linear_rope_append
-    from runtime_amd.phase2.int8_linear import int8_linear, int8_linear_partials
+    from runtime_amd.phase2.int8_linear import int8_linear, int8_linear_partials, int8_mlp_fused_partials
     from runtime_amd.phase2.paged_attention_hip import MX_PA_PLAN_READ, MX_PA_PLAN_WRITE, _decode
 
     model, pool, bsz, dev, s = d.model, d.pool, d.batch, d.dev, d.shape
@@ -390,6 +393,12 @@ def family_launches(d: Decoder) -> dict:
             model._gate_up(buf, layer.gate_up, bsz, None)
     out["gate_up"] = (gate_up, nl)
     out["down"] = (lin("down", buf.act), nl)
+    if model.fuse_mlp and buf.mlp_fused:
+        def mlp():
+            # As the step runs it at this batch: gate||up and down's split partials in one launch.
+            for layer in model.layers:
+                int8_mlp_fused_partials(x_h, layer.gate_up, layer.down, buf.act, buf.part, buf.mlp_sync)
+        out["mlp"] = (mlp, nl)
 
     # As the step calls it: layer 0 records the tile plan, the later layers start from it.
     planned = model.attn_plan and not model.shared_kv_blocks and pool.block_size_tokens >= 16
@@ -419,9 +428,13 @@ def family_table(d: Decoder, args, lens_after) -> tuple[dict, dict, dict, dict]:
     from runtime_amd.phase2.roofline import attention_hbm_bytes
 
     s = d.shape
-    kdur = {name: graph_time(run, launches, args.kernel_steps) for name, (run, launches) in family_launches(d).items()}
+    fams = family_launches(d)
+    if "mlp" in fams:  # the step runs gate||up and down as one launch: time that, not the two apart
+        del fams["gate_up"], fams["down"]
+    kdur = {name: graph_time(run, launches, args.kernel_steps) for name, (run, launches) in fams.items()}
+    lin = d.model.linear_bytes(d.batch)
     per_launch = {"attn": attention_hbm_bytes([x + 1 for x in lens_after], s.kv_heads, s.head_dim, s.heads, d.bs),
-                  **d.model.linear_bytes(d.batch)}
+                  **lin, "mlp": lin["gate_up"] + lin["down"]}
     per_step = {k: (d.n_layers if k != "lm_head" else 1) for k in kdur}
     kernels = {}
     for k in kdur:
@@ -446,7 +459,7 @@ def headline(args, d: Decoder) -> dict:
             if k in counters:
                 kernels[k]["counters"] = counters[k]
     layer_linear_b = sum(lin[k] for k in ("qkv", "o", "gate_up", "down"))
-    layer_linear_s = sum(kdur[k] for k in ("qkv", "o", "gate_up", "down"))
+    layer_linear_s = sum(kdur[k] for k in (("qkv", "o", "mlp") if "mlp" in kdur else ("qkv", "o", "gate_up", "down")))
     achieved = per_launch[dominant] / kdur[dominant] / 1e9
     traffic = None
     if dominant == "attn" and args.model == "llama3-8b" and bsz == 32 and d.n_layers == s.layers:
@@ -461,7 +474,8 @@ def headline(args, d: Decoder) -> dict:
             "batch": bsz, "layers": d.n_layers, "hidden": s.hidden, "heads": s.heads, "kv_heads": s.kv_heads,
             "head_dim": s.head_dim, "intermediate": s.intermediate, "vocab": s.vocab,
             "contexts": f"U[{args.ctx_lo},{args.ctx_hi}] seed 0", "block_size": d.bs,
-            "pool_blocks": args.pool_blocks, "hip_graph": not args.no_graph, "parallelism": "none (1 GPU)",
+            "pool_blocks": args.pool_blocks, "hip_graph": not args.no_graph, "fused_mlp": "mlp" in kdur,
+            "parallelism": "none (1 GPU)",
         },
         "step_hbm_bytes": step_bytes,
         "step_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
@@ -1106,7 +1120,7 @@ def main() -> int:
         return 0
     headroom = args.warmup + 1 + GRAPH_WARMUP + args.steps + args.kernel_steps + 2
     d = Decoder(shape, args.batch, args.ctx_lo, args.ctx_hi, args.pool_blocks, headroom, layers=args.layers,
-                kv_layout=args.kv_layout)
+                kv_layout=args.kv_layout, fuse_mlp=args.fuse_mlp)
     if args.workload == "attention":
         c2 = config2_attention(args, d.pool, d.n_layers)
         print(json.dumps({"metric": "paged decode attention algorithmic HBM GB/s (config 2)", "value": c2["gbps"],

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 16
+#define MX_ABI_VERSION 17
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -125,6 +125,31 @@ int mx_w8a16_linear_partials_swiglu(const uint16_t* gate_up, int64_t M, int64_t 
 int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride, const uint8_t* packed,
                            const uint16_t* scale, const uint16_t* bias, uint16_t* y, int64_t I, int64_t y_stride,
                            void* stream);
+
+/* The whole int8 MLP in one launch: act = mx_w8a16_gateup_swiglu(x) (fp16
+ * [M, I], row stride act_stride) and partials = the split-K partials of
+ * act Wd^T exactly as mx_w8a16_linear_partials(act, ..., N) writes them
+ * (mx_w8a16_splits(M, N, I) slices of [M, N]), both bit-identical to those two
+ * calls. Replaces transformers' down_proj(act_fn(gate_proj(x)) * up_proj(x))
+ * (reached from worker_server.py:771-775, its linears in the quantized slots
+ * of worker_server.py:194-205), which launches each projection in turn; here
+ * down's first weight loads overlap the end of gate||up. Takes 4 < M <= 32
+ * where gate||up runs unsplit and down splits K in k parts
+ * (mx_w8a16_mlp_fused_supported: the Llama-3-8B MLP at batch 32), with act
+ * 128-byte aligned and act_stride a multiple of 64; MX_ERR_UNSUPPORTED
+ * otherwise, or where the device cannot hold every workgroup of the launch at
+ * once. sync: 64 int32 words of device memory, zero before the first call;
+ * every call leaves words 0-32 zero again and ORs error bits into word 33
+ * (1: a wait for the activations gave up after tens of milliseconds, the
+ * outputs then undefined). One call at a time per sync buffer. Measured on
+ * MI355X at the Llama-3-8B MLP's 32 rows it is slower than the two calls
+ * (48-50 against 39.6-41.3 us): down waits for gate||up's slowest workgroups. */
+int mx_w8a16_mlp_fused_supported(int64_t M, int64_t K, int64_t I, int64_t N);
+int mx_w8a16_mlp_fused_partials(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride,
+                                const uint8_t* gu_packed, const uint16_t* gu_scale, const uint16_t* gu_bias,
+                                int64_t I, uint16_t* act, int64_t act_stride, const uint8_t* down_packed,
+                                const uint16_t* down_scale, int64_t N, float* partials, size_t partials_bytes,
+                                int32_t* sync, void* stream);
 
 /* ----------------------------------------------------------------------------
  * Paged-attention decode.

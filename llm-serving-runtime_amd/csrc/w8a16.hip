@@ -235,13 +235,63 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_valu_kernel(const uint16_t* _
 // reads fragments at the k-tile's column offset and meets no barrier. Results are identical to the
 // per-k-tile staging. Measured on MI355X: a barrier per k-tile cost the Qwen2-0.5B step (k ranges
 // of 5-14 tiles) about 9 % of its time.
-template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false, int KW = 1, int MW = 1, int NJX = 0>
-__global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 && MW == 1) ? MX_GEMM_MIN_WAVES : 1) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
-                                                               const uint8_t* __restrict__ w,
-                                                               const uint16_t* __restrict__ scale,
-                                                               const uint16_t* __restrict__ bias,
-                                                               uint16_t* __restrict__ y, int64_t ys, int KT, int NT,
-                                                               float* __restrict__ partial) {
+//
+// The body takes its workgroup's grid coordinates (gx, ks) and the split count KS as arguments, so
+// that the fused MLP launch (mlp_fused_kernel) can run it twice. FUSE: 0 a plain launch; 1 the
+// gate||up phase of the fused launch, whose SwiGLU outputs are stored as whole lines written through
+// the XCD's L2 (sc1), so that workgroups on the other XCDs can read them in the same launch; 2 its
+// down phase, which issues its first P stages of weight loads, waits for the activations of its k
+// range (mlp_wait) and then reads them.
+struct MlpWait {
+    int* sync = nullptr;  // per-chunk arrival counters, then kMlpDone and kMlpErr
+    int chunk_ch = 0;     // activation channels per chunk: one k part of one split of down
+    int group_ch = 0;     // activation channels per gate||up workgroup
+    int groups = 0;       // gate||up workgroups
+};
+constexpr int kMlpMaxChunks = 32, kMlpDone = 32, kMlpErr = 33, kMlpSyncWords = 64;
+// Polls of the arrival counter before a wait gives up (each a device-coherent load of about a
+// microsecond plus a short sleep): a wait that should last tens of microseconds ends after tens of
+// milliseconds at most, sets kMlpErr bit 1 and goes on with whatever the activations hold.
+constexpr int kMlpSpinLimit = 1 << 15;
+
+// Gate||up workgroups whose activation channels overlap chunk c.
+__device__ __forceinline__ int mlp_chunk_arrivals(const MlpWait& wt, int c) {
+    const int lo = c * wt.chunk_ch / wt.group_ch;
+    int hi = ((c + 1) * wt.chunk_ch - 1) / wt.group_ch;
+    if (hi > wt.groups - 1) hi = wt.groups - 1;
+    return hi - lo + 1;
+}
+
+// Thread 0 waits until every gate||up workgroup that writes the chunks of k parts [0, KW) of split
+// ks has arrived; the workgroup's barrier then releases every wave.
+template <int KW>
+__device__ __forceinline__ void mlp_wait(const MlpWait& wt, int ks) {
+    if (threadIdx.x == 0) {
+        for (int kw = 0; kw < KW; ++kw) {
+            const int c = ks * KW + kw;
+            const int want = mlp_chunk_arrivals(wt, c);
+            int polls = 0;
+            while (__hip_atomic_load(wt.sync + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
+                if (++polls > kMlpSpinLimit) {
+                    atomicOr(wt.sync + kMlpErr, 1);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int MT, int NPW, int WAVES, int P, bool SW, bool GU, int KW, int MW, int NJX, int FUSE>
+__device__ __forceinline__ void gemm_body(const int gx, const int ks, const int KS, const uint16_t* __restrict__ x,
+                                          int64_t xs, int M, const uint8_t* __restrict__ w,
+                                          const uint16_t* __restrict__ scale, const uint16_t* __restrict__ bias,
+                                          uint16_t* __restrict__ y, int64_t ys, int KT, int NT,
+                                          float* __restrict__ partial, const MlpWait& wt) {
+    static_assert(FUSE == 0 || (NJX == 0 && !SW && MW == 1 && NPW == 1), "fused phases: plain 1-n-tile shapes");
+    static_assert(FUSE != 1 || GU, "the fused gate||up phase has the SwiGLU epilogue");
+    static_assert(FUSE != 2 || !GU, "the fused down phase writes partials");
     constexpr int ROWS = MW * MT * 16;  // x rows staged per k-tile (MW waves along M, MT m-tiles each)
     constexpr int RS = kTileK + 8;  // LDS row stride (halfs): 144 bytes, rows start 4 banks apart
     constexpr int WN = WAVES / (KW * MW);  // waves along N per k part, each owning NPW n-tiles
@@ -254,7 +304,6 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     constexpr int XF = NJX > 0 ? (ROWS * NJX * 8 + WP * 64 - 1) / (WP * 64) : 1;  // chunks per thread
     __shared__ __attribute__((aligned(16))) _Float16 xl[KW][NJX > 0 ? 1 : 2][NJX > 0 ? ROWS * RSX : ROWS * RS];
 
-    const int ks = blockIdx.y, KS = gridDim.y;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kw = wave / WP, wm = wave - kw * WP;
@@ -265,7 +314,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     const int ltid = tid - kw * WP * 64;  // thread index within the k part
     const int lane = tid & 63;
     const int g = lane >> 4, r = lane & 15;
-    const int nt_w = (blockIdx.x * WN + wn) * NPW;
+    const int nt_w = (gx * WN + wn) * NPW;
     const bool valid = nt_w < NT;                 // NT % NPW == 0: a wave is all in or all out
     const int nt_c = valid ? nt_w : NT - NPW;     // out-of-range waves load (and drop) the last tiles
     const uint4* wbase = reinterpret_cast<const uint4*>(w) + (int64_t)nt_c * 64;  // tile (nt_c + p, kt): + (kt*NT + p)*64
@@ -289,17 +338,28 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
         uint4 up[SW ? XC : 1];
     };
     const int up_off = KT * kTileK;  // SW: the up half of a gate_up row
-    auto load = [&](int j, St& st) {
+    auto load_w = [&](int j, St& st) {
         const int kt = kt_lo + (j < nj ? j : nj - 1);
 #pragma unroll
         for (int p = 0; p < NPW; ++p) st.w[p] = load_wtile<MW == 1>(wbase + ((int64_t)kt * NT + p) * 64 + lane);
+    };
+    auto load_x = [&](int j, St& st) {
+        const int kt = kt_lo + (j < nj ? j : nj - 1);
         if constexpr (NJX == 0) {
 #pragma unroll
             for (int u = 0; u < XC; ++u) {
+                // FUSE == 2: plain loads of activations written in this launch. Each line of them has
+                // one writer, which wrote it through to memory before counting itself, and no cache of
+                // this CU or XCD holds it before its chunk's wait ends (caches start the launch clean and
+                // nothing reads the activations earlier), so the first load fetches the final line.
                 st.x[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + kt * kTileK);
                 if (SW) st.up[u] = *reinterpret_cast<const uint4*>(xbase + xsrc[u] + up_off + kt * kTileK);
             }
         }
+    };
+    auto load = [&](int j, St& st) {
+        load_w(j, st);
+        load_x(j, st);
     };
     // NJX: chunk c = ltid + u * WP * 64 of the part's ROWS x (nj * 64) range (rows past M read row
     // M - 1; chunks past the range load chunk 0 and are stored to row 0's padding, which no fragment
@@ -395,7 +455,7 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
     uint16_t sc_raw[NPW], bi_raw[NPW];
     auto convert_epilogue = [&]() {
         __builtin_amdgcn_sched_barrier(0);
-        const bool with_bias = gridDim.y == 1 && bias;
+        const bool with_bias = KS == 1 && bias;
 #pragma unroll
         for (int p = 0; p < NPW; ++p) {
             sc_pre[p] = (float)__builtin_bit_cast(_Float16, sc_raw[p]);
@@ -409,10 +469,10 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
             const int64_t n = (int64_t)(nt_c + p) * kTileN + r;
             if constexpr (kRaw) {  // unconditional loads (no bias: read the scale, use 0)
                 sc_raw[p] = scale[n];
-                bi_raw[p] = ((gridDim.y == 1 && bias) ? bias : scale)[n];
+                bi_raw[p] = ((KS == 1 && bias) ? bias : scale)[n];
             } else {
                 sc_pre[p] = h2f(scale, n);
-                bi_pre[p] = (gridDim.y == 1 && bias) ? h2f(bias, n) : 0.0f;
+                bi_pre[p] = (KS == 1 && bias) ? h2f(bias, n) : 0.0f;
             }
         }
     };
@@ -440,7 +500,18 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
                 if (j < nj) compute(st[j]);
         } else {
             St st[P];
-            PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), MX_NJX_HOOK)
+            if constexpr (FUSE == 2) {
+                // The first stages' weights go out before the wait, their activations after it.
+#pragma unroll
+                for (int s = 0; s < P; ++s) load_w(s, st[s]);
+                mlp_wait<KW>(wt, ks);
+#pragma unroll
+                for (int s = 0; s < P; ++s) load_x(s, st[s]);
+                MX_NJX_HOOK
+                PIPELINE_REST(P, nj, st, load, compute(st[s]))
+            } else {
+                PIPELINE_BODY_HOOK(P, nj, st, load, compute(st[s]), MX_NJX_HOOK)
+            }
         }
     } else {
         load_epilogue();
@@ -449,6 +520,9 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
 #undef MX_NJX_HOOK
     const int N = NT * kTileN;
     if (GU) {
+        // FUSE == 1: the workgroup's [ROWS, 64] activation tile is gathered in LDS first and stored
+        // as whole 128-byte lines of each row (write-through, see below).
+        __shared__ __attribute__((aligned(16))) uint16_t act_tile[FUSE == 1 ? ROWS : 1][FUSE == 1 ? WN * 8 : 1];
         // Every lane takes part in the swap; out-of-range waves just do not store.
 #pragma unroll
         for (int p = 0; p < NPW; ++p) {
@@ -465,9 +539,27 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
                     const int m = (mw * MT + mt) * 16 + 4 * g + i;
                     if (valid && r < 8 && m < M) {
                         const _Float16 sg = (_Float16)silu_f32(v);
-                        y[(int64_t)m * ys + c] = f2h_bits((float)sg * other);
+                        if constexpr (FUSE == 1)
+                            act_tile[m][wn * 8 + (r & 7)] = f2h_bits((float)sg * other);
+                        else
+                            y[(int64_t)m * ys + c] = f2h_bits((float)sg * other);
                     }
                 }
+        }
+        if constexpr (FUSE == 1) {
+            // 16 threads per row, 8 bytes each: every store instruction covers whole lines. The
+            // stores are device-coherent (sc1, written through the XCD's L2), so that a workgroup on
+            // another XCD that waits for this one's arrival reads them from memory; the group's
+            // channels are whole lines of each row (the caller checks the alignment), so no line of
+            // the activations is written from two XCDs.
+            static_assert(FUSE != 1 || (WN * 8 * 2 == 128 && ROWS * 16 <= WAVES * 64), "one line per row, one store each");
+            __syncthreads();
+            const int row = tid >> 4, q = tid & 15;
+            if (row < ROWS && row < M && nt_w - wn * NPW < NT) {
+                const uint64_t v = *reinterpret_cast<const uint64_t*>(&act_tile[row][q * 4]);
+                __hip_atomic_store(reinterpret_cast<uint64_t*>(y + (int64_t)row * ys + (int64_t)gx * WN * 8) + q, v,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         return;
     }
@@ -506,6 +598,17 @@ __global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 
                 else partial[((int64_t)ks * M + m) * N + n] = acc[p][mt][i] * sc;
             }
     }
+}
+
+template <int MT, int NPW, int WAVES, int P, bool SW = false, bool GU = false, int KW = 1, int MW = 1, int NJX = 0>
+__global__ __launch_bounds__(WAVES * 64, (NPW == 1 && !SW && MT <= 2 && KW == 1 && MW == 1) ? MX_GEMM_MIN_WAVES : 1) void gemm_mfma_kernel(const uint16_t* __restrict__ x, int64_t xs, int M,
+                                                               const uint8_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ scale,
+                                                               const uint16_t* __restrict__ bias,
+                                                               uint16_t* __restrict__ y, int64_t ys, int KT, int NT,
+                                                               float* __restrict__ partial) {
+    gemm_body<MT, NPW, WAVES, P, SW, GU, KW, MW, NJX, 0>(blockIdx.x, blockIdx.y, gridDim.y, x, xs, M, w, scale, bias, y,
+                                                         ys, KT, NT, partial, MlpWait{});
 }
 
 // y[m, n] = fp16(bias[n] + the splits' partial[ks][m][n] in split order), one fp32 add each. A
@@ -834,6 +937,108 @@ static void launch_reduce(const float* partial, int KS, int M, int N, const uint
     }
 }
 
+// ---------------------------------------------------------------------------
+// Fused MLP launch (mx_w8a16_mlp_fused_partials): silu(x Wg^T) * (x Wu^T) and the split partials of
+// down in one persistent launch, so that down's first weight loads overlap the end of gate||up
+// instead of waiting behind a launch boundary. Workgroup i first computes gate||up group i (8 waves
+// of one n-tile each: 64 activation channels, whole 128-byte lines of every row) if i < groups1,
+// stores it device-coherent and counts itself in the arrival counter of each down chunk its
+// channels overlap (a chunk: the k range of one k part of one split of down). It then runs down's
+// workgroup (i % groups2, split i / groups2), which issues its first P stages of weights, waits for
+// its chunks and reads the activations with device-coherent loads. The last workgroup to finish
+// clears the counters for the next launch. Every workgroup must be resident at once (checked on the
+// host from the occupancy), or a wait could stall on a workgroup that has not started; the waits
+// are bounded in any case (kMlpSpinLimit). Both phases run the standalone launches' code with the
+// same k order per output, so act and the partials are bit-identical to gate||up + down run apart.
+// Measured on MI355X (Llama-3-8B MLP, 32 rows) it is slower than the two launches, 48-50 against
+// 39.6-41.3 us: down's chunks wait for gate||up's slowest workgroups, which end 4-6 us after the
+// median, and the hand-off (counter, poll, first activation loads) costs about what the launch
+// boundary did. The decode step keeps the two launches unless asked (Int8DecodeModel.fuse_mlp).
+constexpr int kMlpWaves = 8;
+constexpr int kMlpGroupCh = kMlpWaves * kTileN / 2;  // activation channels per gate||up workgroup
+constexpr int kMlpDownWn = kMlpWaves / kKParts;      // down: waves along N per k part, one n-tile each
+
+// One 8-wave workgroup per CU at 2 or 3 waves per SIMD alike. At 2 (256 VGPRs) the kernel holds
+// everything in registers; at 3 (168) gate||up streamed faster, as in its own launch (phase 1 ended
+// at a median of 22 against 25 us per workgroup, the launch 45.9 against 48.5 us on MI355X at the
+// Llama-3-8B MLP's 32 rows), but this build spills 20 bytes per lane there.
+template <int MT>
+__global__ __launch_bounds__(kMlpWaves * 64, 2) void mlp_fused_kernel(
+    const uint16_t* __restrict__ x, int64_t xs, int M, const uint8_t* __restrict__ wgu,
+    const uint16_t* __restrict__ sgu, const uint16_t* __restrict__ bgu, uint16_t* __restrict__ act, int64_t as,
+    int KT1, int NT1, const uint8_t* __restrict__ wd, const uint16_t* __restrict__ sd, int KT2, int NT2, int KS2,
+    int groups2, float* __restrict__ partial, MlpWait wt) {
+    constexpr int P = mfma_depth(MT);
+    const int wg = blockIdx.x;
+    if (wg < wt.groups) {
+        gemm_body<MT, 1, kMlpWaves, P, false, true, 1, 1, 0, 1>(wg, 0, 1, x, xs, M, wgu, sgu, bgu, act, as, KT1, NT1,
+                                                                nullptr, wt);
+        // Every wave's stores have completed (vmcnt 0) before the workgroup counts itself.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int lo = wg * wt.group_ch, hi = lo + wt.group_ch - 1, chunks = KS2 * kKParts;
+            for (int c = lo / wt.chunk_ch; c <= hi / wt.chunk_ch && c < chunks; ++c)
+                __hip_atomic_fetch_add(wt.sync + c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    gemm_body<MT, 1, kMlpWaves, P, false, false, kKParts, 1, 0, 2>(wg % groups2, wg / groups2, KS2, act, as, M, wd, sd,
+                                                                   nullptr, nullptr, 0, KT2, NT2, partial, wt);
+    // Thread 0 has passed its workgroup's wait: the last one to get here clears the counters.
+    if (threadIdx.x == 0) {
+        const int done = __hip_atomic_fetch_add(wt.sync + kMlpDone, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == (int)gridDim.x - 1) {
+            for (int c = 0; c < KS2 * kKParts; ++c)
+                __hip_atomic_store(wt.sync + c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(wt.sync + kMlpDone, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+struct MlpPlan {
+    int MT, KS2, groups1, groups2, grid;
+};
+
+// Workgroups of the fused kernel that fit on the current device at once, cached per device and
+// instance; 0 if the runtime cannot say.
+template <int MT>
+static int mlp_resident() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cache[dev] == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mlp_fused_kernel<MT>, kMlpWaves * 64, 0) != hipSuccess)
+            return 0;
+        cache[dev] = cus * per_cu;
+    }
+    return cache[dev];
+}
+
+// The fused launch takes M = 5..32 rows (one or two m-tiles) where gate||up alone would run as one
+// unsplit MFMA launch and down as a split one with k parts (the Llama-3-8B MLP at batch 32), and
+// where all of its workgroups fit on the device at once. shape_only: skip the device check.
+static bool mlp_plan(int64_t M, int64_t K, int64_t I, int64_t N, MlpPlan& mp, bool shape_only = false) {
+    if (M <= kValuMaxM || M > 32 || K <= 0 || I <= 0 || N <= 0) return false;
+    if (K % kTileK || I % kMlpGroupCh || N % (kTileN * kMlpDownWn)) return false;
+    if (K / kTileK > (1 << 20) || 2 * I / kTileN > (1 << 24) || N / kTileN > (1 << 24) || I * 64 > 0x7fffffff)
+        return false;
+    const int NT1 = (int)(2 * I / kTileN), KT1 = (int)(K / kTileK);
+    const int NT2 = (int)(N / kTileN), KT2 = (int)(I / kTileK);
+    const Plan p1 = plan_for((int)M, NT1, KT1), p2 = plan_for((int)M, NT2, KT2);
+    if (p1.valu || p1.KS != 1 || p2.valu || p2.KS < 2 || p2.KW != kKParts || p2.MT != p1.MT || p2.MT > 2) return false;
+    if (KT2 % (p2.KS * kKParts) != 0 || p2.KS * kKParts > kMlpMaxChunks) return false;
+    mp.MT = p2.MT;
+    mp.KS2 = p2.KS;
+    mp.groups1 = NT1 / kMlpWaves;
+    mp.groups2 = NT2 / kMlpDownWn;
+    mp.grid = mp.groups2 * mp.KS2;
+    if (mp.groups1 > mp.grid || mp.grid > 65535) return false;
+    if (shape_only) return true;
+    return (mp.MT == 1 ? mlp_resident<1>() : mlp_resident<2>()) >= mp.grid;
+}
+
 }  // namespace w8a16
 }  // namespace mx
 
@@ -1037,4 +1242,54 @@ extern "C" int mx_w8a16_gateup_swiglu(const uint16_t* x, int64_t M, int64_t K, i
         }
     }
     return check_launch("mx_w8a16_gateup_swiglu");
+}
+
+extern "C" int mx_w8a16_mlp_fused_supported(int64_t M, int64_t K, int64_t I, int64_t N) {
+    w8a16::MlpPlan mp{};
+    return w8a16::mlp_plan(M, K, I, N, mp) ? 1 : 0;
+}
+
+extern "C" int mx_w8a16_mlp_fused_partials(const uint16_t* x, int64_t M, int64_t K, int64_t x_stride,
+                                           const uint8_t* gu_packed, const uint16_t* gu_scale,
+                                           const uint16_t* gu_bias, int64_t I, uint16_t* act, int64_t act_stride,
+                                           const uint8_t* down_packed, const uint16_t* down_scale, int64_t N,
+                                           float* partials, size_t partials_bytes, int32_t* sync, void* stream) {
+    const char* what = "mx_w8a16_mlp_fused_partials";
+    if (!x || !gu_packed || !gu_scale || !act || !down_packed || !down_scale || !partials || !sync)
+        return fail(MX_ERR_NULL, "%s: null pointer", what);
+    w8a16::MlpPlan mp{};
+    if (!w8a16::mlp_plan(M, K, I, N, mp, true))
+        return fail(MX_ERR_UNSUPPORTED, "%s: shape M=%lld K=%lld I=%lld N=%lld does not take the fused launch", what,
+                    (long long)M, (long long)K, (long long)I, (long long)N);
+    if (!w8a16::mlp_plan(M, K, I, N, mp))
+        return fail(MX_ERR_UNSUPPORTED, "%s: the %d workgroups of the fused launch do not fit on this device at once",
+                    what, mp.grid);
+    if (x_stride < K || act_stride < I) return fail(MX_ERR_INVALID, "%s: row strides must cover K and I", what);
+    if (!aligned(x, 16) || (x_stride % 8) != 0 || !aligned(gu_packed, 16) || !aligned(down_packed, 16) ||
+        !aligned(partials, 16) || !aligned(sync, 4))
+        return fail(MX_ERR_ALIGNMENT, "%s: x rows, weights and partials must be 16-byte aligned", what);
+    // Each gate||up workgroup writes whole 128-byte lines of every activation row, so that no line is
+    // written from two XCDs.
+    if (!aligned(act, 128) || (act_stride * 2) % 128 != 0)
+        return fail(MX_ERR_ALIGNMENT, "%s: act must be 128-byte aligned with a row stride of a multiple of 64", what);
+    if (partials_bytes < (size_t)mp.KS2 * M * N * sizeof(float))
+        return fail(MX_ERR_WORKSPACE, "%s: partials need %zu bytes, got %zu", what,
+                    (size_t)mp.KS2 * M * N * sizeof(float), partials_bytes);
+    w8a16::MlpWait wt;
+    wt.sync = sync;
+    wt.chunk_ch = (int)(I / (mp.KS2 * w8a16::kKParts));
+    wt.group_ch = w8a16::kMlpGroupCh;
+    wt.groups = mp.groups1;
+    const int NT1 = (int)(2 * I / w8a16::kTileN), KT1 = (int)(K / w8a16::kTileK);
+    const int NT2 = (int)(N / w8a16::kTileN), KT2 = (int)(I / w8a16::kTileK);
+    hipStream_t st = as_stream(stream);
+    if (mp.MT == 1)
+        hipLaunchKernelGGL(w8a16::mlp_fused_kernel<1>, dim3(mp.grid), dim3(w8a16::kMlpWaves * 64), 0, st, x, x_stride,
+                           (int)M, gu_packed, gu_scale, gu_bias, act, act_stride, KT1, NT1, down_packed, down_scale, KT2,
+                           NT2, mp.KS2, mp.groups2, partials, wt);
+    else
+        hipLaunchKernelGGL(w8a16::mlp_fused_kernel<2>, dim3(mp.grid), dim3(w8a16::kMlpWaves * 64), 0, st, x, x_stride,
+                           (int)M, gu_packed, gu_scale, gu_bias, act, act_stride, KT1, NT1, down_packed, down_scale, KT2,
+                           NT2, mp.KS2, mp.groups2, partials, wt);
+    return check_launch(what);
 }

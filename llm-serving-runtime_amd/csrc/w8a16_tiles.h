@@ -87,6 +87,10 @@ __device__ __forceinline__ float h2f(const uint16_t* p, int64_t i) {
 #define PIPELINE_BODY_HOOK(P, nj, st, load, COMPUTE, HOOK)         \
     _Pragma("unroll") for (int s = 0; s < P; ++s) load(s, st[s]); \
     HOOK;                                                           \
+    PIPELINE_REST(P, nj, st, load, COMPUTE)
+
+// Everything after the prologue: for callers that issue the first P stages themselves.
+#define PIPELINE_REST(P, nj, st, load, COMPUTE)                     \
     int j0 = 0;                                                     \
     for (; j0 + 2 * P <= nj; j0 += P) {                             \
         _Pragma("unroll") for (int s = 0; s < P; ++s) {             \

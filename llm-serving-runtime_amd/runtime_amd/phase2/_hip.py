@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -44,6 +44,9 @@ SIGNATURES = {
     "mx_w8a16_linear_swiglu": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _sz, _p]),
     "mx_w8a16_linear_partials_swiglu": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _sz, _p]),
     "mx_w8a16_gateup_swiglu": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p]),
+    "mx_w8a16_mlp_fused_supported": (ctypes.c_int, [_i64, _i64, _i64, _i64]),
+    "mx_w8a16_mlp_fused_partials": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _p, _p, _i64, _p,
+                                                   _sz, _p, _p]),
     "mx_paged_attn_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "mx_paged_attn_error_offset": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "mx_paged_attn_decode": (

@@ -53,7 +53,8 @@ import torch
 
 from .decode_glue import (QKV_ROPE_MAX_ROWS, add_rmsnorm, add_rmsnorm_splits, argmax_rows, qkv_linear_rope_append,
                           qkv_rope_append, qkv_rope_append_splits, rope_table)
-from .int8_linear import (gateup_interleave, int8_gateup_swiglu, int8_linear, int8_linear_partials, linear_splits,
+from .int8_linear import (MLP_SYNC_ERR, MLP_SYNC_WORDS, gateup_interleave, int8_gateup_swiglu, int8_linear,
+                          int8_linear_partials, int8_mlp_fused_partials, linear_splits, mlp_fusable,
                           pack_weight, quantize_weight)
 from .paged_attention_hip import MX_PA_PLAN_READ, MX_PA_PLAN_WRITE
 from .paged_attention_hip import _decode as _paged_decode
@@ -114,6 +115,8 @@ class _Buffers:
     attn_lens: torch.Tensor  # int32 [B]
     next: torch.Tensor    # int64 [B], greedy tokens
     err: torch.Tensor     # int32 [1], OR of the append kernels' error bits
+    mlp_sync: torch.Tensor  # int32 [MLP_SYNC_WORDS], the fused MLP launch's counters and error word
+    mlp_fused: bool       # gate||up and down run as one launch at this batch size
 
 
 def _quantize(w: torch.Tensor, device: torch.device) -> tuple:
@@ -147,6 +150,11 @@ class Int8DecodeModel:
         # whose lengths and block tables are the same, start from that record (MX_PA_PLAN_READ):
         # one dependent memory round trip less per layer. Needs block size >= 16 and no aliasing.
         self.attn_plan = True
+        # True: gate||up and down as one launch where the shape and device take it (mlp_fusable:
+        # the Llama-3-8B MLP at batch 32), bit-identical to the two launches. Off: measured on
+        # MI355X at batch 32 it took 48-50 us per layer against 39.6-41.3 us for the two launches
+        # (bench.py --fuse-mlp); down cannot start before gate||up's slowest workgroups finish.
+        self.fuse_mlp = False
         self._buffers: dict[int, _Buffers] = {}
         self.layers: list[_Layer] = []
         if not init:
@@ -259,15 +267,20 @@ class Int8DecodeModel:
                            part=torch.empty(part_elems, dtype=torch.float32, device=dev), splits=splits,
                            attn_lens=torch.zeros(batch, dtype=torch.int32, device=dev),
                            next=torch.zeros(batch, dtype=torch.int64, device=dev),
-                           err=torch.zeros(1, dtype=torch.int32, device=dev))
+                           err=torch.zeros(1, dtype=torch.int32, device=dev),
+                           mlp_sync=torch.zeros(MLP_SYNC_WORDS, dtype=torch.int32, device=dev),
+                           mlp_fused=mlp_fusable(batch, s.hidden, s.intermediate, s.hidden))
             self._buffers[batch] = buf
         return buf
 
     def error_flag(self) -> int:
-        """OR of the KV-append error bits since the buffers were created (one host sync)."""
+        """OR of the KV-append error bits since the buffers were created (one host sync each), with
+        bit 16 set if a fused MLP launch gave up waiting for its activations."""
         flag = 0
         for buf in self._buffers.values():
             flag |= int(buf.err.item())
+            if int(buf.mlp_sync[MLP_SYNC_ERR].item()):
+                flag |= 16
         return flag
 
     def step(self, tokens: torch.Tensor, pool, block_tables: torch.Tensor, seq_lens: torch.Tensor,
@@ -322,11 +335,16 @@ class Int8DecodeModel:
             else:
                 self._lin(buf.attn.view(bsz, -1), layer.o, buf.o, timers, "o")
                 add_rmsnorm(buf.o, layer.ln_post, eps, residual=buf.h, out=buf.x, residual_out=buf.h)
-            self._gate_up(buf, layer.gate_up, bsz, timers)
-            if sp["down"] > 1:
-                self._partials(buf.act, layer.down, buf.part, timers, "down")
+            if self.fuse_mlp and buf.mlp_fused:
+                ev = self._tick(timers, "mlp")
+                int8_mlp_fused_partials(buf.x, layer.gate_up, layer.down, buf.act, buf.part, buf.mlp_sync)
+                self._tock(timers, "mlp", ev)
             else:
-                self._lin(buf.act, layer.down, buf.mlp, timers, "down")
+                self._gate_up(buf, layer.gate_up, bsz, timers)
+                if sp["down"] > 1:
+                    self._partials(buf.act, layer.down, buf.part, timers, "down")
+                else:
+                    self._lin(buf.act, layer.down, buf.mlp, timers, "down")
         self._norm_after_down(buf, self.ln_final)
         self._lin(buf.x, self.lm_head, buf.logits, timers, "lm_head")
         nxt = argmax_rows(buf.logits, out=buf.next if out is None else out, seq_lens=seq_lens)

@@ -241,6 +241,45 @@ def int8_gateup_swiglu(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tenso
     return y
 
 
+MLP_SYNC_WORDS = 64  # int32 words of a fused MLP launch's sync buffer
+MLP_SYNC_ERR = 33    # the word holding its error bits
+
+
+def mlp_fusable(m: int, hidden: int, inter: int, out_features: int) -> bool:
+    """Whether :func:`int8_mlp_fused_partials` takes ``m`` rows of this MLP on the current device."""
+    return bool(_hip.load().mx_w8a16_mlp_fused_supported(m, hidden, inter, out_features))
+
+
+def int8_mlp_fused_partials(x: torch.Tensor, gate_up: tuple, down: tuple, act: torch.Tensor, partials: torch.Tensor,
+                            sync: torch.Tensor) -> int:
+    """:func:`int8_gateup_swiglu` into ``act`` and :func:`int8_linear_partials` of ``act`` with the down
+    weight into ``partials``, as one launch (``mx_w8a16_mlp_fused_partials``); bit-identical to the two
+    calls. ``gate_up`` = (packed, scale, 2 * inter, bias) with interleaved rows, ``down`` = (packed, scale,
+    out_features, ...); ``act`` fp16 [M, inter] with 128-byte aligned rows; ``sync`` int32 [64] zeros,
+    kept between calls. Returns down's split count."""
+    _hip.require_device_tensor(x, "x")
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise ValueError("int8_mlp_fused_partials expects fp16 x [M, K]")
+    if x.stride(-1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    m, k = (int(v) for v in x.shape)
+    gpk, gsc, gn, gbias = gate_up[0], gate_up[1], int(gate_up[2]), gate_up[3]
+    dpk, dsc, n = down[0], down[1], int(down[2])
+    inter = gn // 2
+    if act.dtype != torch.float16 or act.dim() != 2 or tuple(act.shape) != (m, inter) or act.stride(-1) != 1:
+        raise ValueError(f"act must be fp16 [{m}, {inter}] with unit column stride")
+    if partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous fp32 tensor")
+    if sync.dtype != torch.int32 or sync.numel() < MLP_SYNC_WORDS or not sync.is_contiguous():
+        raise ValueError(f"sync must be a contiguous int32 tensor of at least {MLP_SYNC_WORDS} words")
+    lib = _hip.load()
+    _hip.check(lib.mx_w8a16_mlp_fused_partials(
+        x.data_ptr(), m, k, x.stride(0), gpk.data_ptr(), gsc.data_ptr(), gbias.data_ptr() if gbias is not None else None,
+        inter, act.data_ptr(), act.stride(0), dpk.data_ptr(), dsc.data_ptr(), n, partials.data_ptr(),
+        partials.numel() * 4, sync.data_ptr(), _hip.stream_handle(x.device)), "mx_w8a16_mlp_fused_partials")
+    return int(lib.mx_w8a16_splits(m, n, inter))
+
+
 class Int8Linear(nn.Module):
     """Drop-in for ``nn.Linear`` on the decode path with int8 weights and fp16 scales."""
 

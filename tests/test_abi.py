@@ -177,3 +177,26 @@ def test_calibration_probes_reject_bad_arguments():
     _status(lib.mx_launch_probe(fake, 1 << 20, 2 << 20, 2, None), _hip.MX_ERR_INVALID)  # past the end
     _status(lib.mx_launch_probe(None, 1 << 20, 4096, 2, None), _hip.MX_ERR_NULL)
     _status(lib.mx_launch_probe(None, 0, 0, 0, None), _hip.MX_ERR_INVALID)
+
+
+def test_fused_mlp_rejects_bad_arguments():
+    """mx_w8a16_mlp_fused_partials refuses null pointers and shapes outside its plan on the host,
+    before anything reaches the device."""
+    lib = _hip.load()
+    f = ctypes.c_void_p(1 << 20)
+    k, i, n = 4096, 14336, 4096  # the Llama-3-8B MLP, which the fused launch takes at 5..32 rows
+
+    def call(x=f, m=32, kk=k, ii=i, nn=n, act=f, part=f, sync=f):
+        return lib.mx_w8a16_mlp_fused_partials(x, m, kk, kk, f, f, None, ii, act, ii, f, f, nn, part, 1 << 30, sync,
+                                               None)
+
+    _status(call(x=None), _hip.MX_ERR_NULL)
+    _status(call(sync=None), _hip.MX_ERR_NULL)
+    _status(call(part=None), _hip.MX_ERR_NULL)
+    _status(call(m=4), _hip.MX_ERR_UNSUPPORTED)   # the VALU GEMV's rows
+    _status(call(m=33), _hip.MX_ERR_UNSUPPORTED)  # three m-tiles
+    _status(call(kk=4000), _hip.MX_ERR_UNSUPPORTED)
+    _status(call(ii=14336 + 32), _hip.MX_ERR_UNSUPPORTED)  # gate||up groups of 64 channels
+    _status(call(kk=1024, ii=4096, nn=1024), _hip.MX_ERR_UNSUPPORTED)  # gate||up would split K there
+    assert lib.mx_w8a16_mlp_fused_supported(4, k, i, n) == 0
+    assert lib.mx_w8a16_mlp_fused_supported(48, k, i, n) == 0
