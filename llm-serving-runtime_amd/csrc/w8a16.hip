@@ -667,7 +667,15 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
 // Largest M handled by the VALU GEMV; above it the MFMA kernel runs.
 constexpr int kValuMaxM = 4;
 constexpr int kMaxRows = 128;  // rows per MFMA launch (8 m-tiles); larger M runs in chunks
-constexpr int kGemvWaves = 8;
+// Waves per GEMV workgroup (one workgroup per n-tile, the waves taking interleaved k-tiles): 4
+// where the grid alone covers the chip (more than 256 n-tiles) or K is short or long (at most 32
+// or at least 128 k-tiles), else 8 (few workgroups that must each pull a middling K: the
+// Qwen2-0.5B down projection, 56 n-tiles x 76 k-tiles). 16 spilled. Measured on MI355X, 40-50
+// distinct weight copies per graph, 8 -> 4 waves, M = 1..4: Llama-3-8B qkv 9.4-15.9 ->
+// 8.5-14.4 us, down 16.0-23.8 -> 14.0-23.5 us; Qwen2-0.5B qkv 3.8-4.6 -> 3.2-3.9 us, o 3.7-4.5 ->
+// 3.2-3.9 us, gate||up (9728 x 896) 9.0-11.8 -> 5.5-7.5 us; the Llama o / config-1 shape (256 x 64
+// tiles) 6.1-9.0 either way, 7.5 against 8.1 us at M = 2, so it keeps 8.
+static int gemv_waves(int NT, int KT) { return (NT > 256 || KT <= 32 || KT >= 128) ? 4 : 8; }
 constexpr int kMfmaWaves = 4;
 constexpr int kWideGrid = 256;    // at least this many n-groups: no K split
 constexpr int kSplitGrid = 512;   // otherwise split K until the grid reaches this many workgroups
@@ -792,8 +800,12 @@ static size_t workspace_for(int M, int NT, int KT) {
 template <int M, bool GU = false>
 static void launch_gemv(const uint16_t* x, int64_t xs, const uint8_t* w, const uint16_t* s, const uint16_t* b,
                         uint16_t* y, int64_t ys, int NT, int KT, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_valu_kernel<M, kGemvWaves, gemv_depth(M), GU>), dim3(NT), dim3(kGemvWaves * 64), 0, st,
-                       x, xs, w, s, b, y, ys, KT);
+    if (gemv_waves(NT, KT) == 4)
+        hipLaunchKernelGGL((gemv_valu_kernel<M, 4, gemv_depth(M), GU>), dim3(NT), dim3(4 * 64), 0, st, x, xs, w, s, b, y,
+                           ys, KT);
+    else
+        hipLaunchKernelGGL((gemv_valu_kernel<M, 8, gemv_depth(M), GU>), dim3(NT), dim3(8 * 64), 0, st, x, xs, w, s, b, y,
+                           ys, KT);
 }
 
 template <bool GU = false>
