@@ -73,6 +73,29 @@ def test_fused_mlp_bit_identical_on_calls_in_a_row(mlp):
         assert words[:MLP_SYNC_ERR] == [0] * MLP_SYNC_ERR  # counters cleared for the next call
 
 
+def test_fused_mlp_with_gate_up_bias(mlp):
+    """A gate||up bias (interleaved like the weight rows) enters the fused launch's epilogue exactly as
+    it enters mx_w8a16_gateup_swiglu's."""
+    gu, dn = mlp
+    _require_fusable(16)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    bias = gateup_interleave(torch.randn(I, generator=g, device=DEV) * 0.1,
+                             torch.randn(I, generator=g, device=DEV) * 0.1).half()
+    gub = (gu[0], gu[1], gu[2], bias)
+    m = 16
+    x = _x(m, 55)
+    act = torch.empty(m, I, dtype=torch.float16, device=DEV)
+    ks = linear_splits(m, N, I)
+    part = torch.empty(ks * m * N, dtype=torch.float32, device=DEV)
+    sync = torch.zeros(MLP_SYNC_WORDS, dtype=torch.int32, device=DEV)
+    assert int8_mlp_fused_partials(x, gub, dn, act, part, sync) == ks
+    want_act, want_part, _ = _apart(x, gub, dn)
+    torch.cuda.synchronize()
+    assert torch.equal(act, want_act)
+    assert torch.equal(part, want_part)
+    assert sync.tolist() == [0] * MLP_SYNC_WORDS
+
+
 def test_fused_mlp_graph_replays(mlp):
     """Captured once, replayed with new inputs copied in between and the two-launch reference run
     eagerly between the replays: every replay equals it."""
