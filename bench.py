@@ -710,6 +710,7 @@ def calibration_probes(args) -> dict:
                            "us": round(t * 1e6, 2), "gbps": round(span / t / 1e9, 1)})
     del buf
     torch.cuda.empty_cache()
+    print("[probes] stream done", file=sys.stderr, flush=True)
     dst = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
     launch = []
     for nbytes, wgs in LAUNCH_PROBE_SHAPES:
@@ -721,11 +722,109 @@ def calibration_probes(args) -> dict:
         launch.append({"bytes_written": nbytes, "workgroups": wgs, "us": round(t * 1e6, 2)})
     del dst
     torch.cuda.empty_cache()
+    print("[probes] launch done", file=sys.stderr, flush=True)
+    handoff, barrier, chain = handoff_probes()
     gather = gather_sweep(args)
-    return {"stream": stream, "launch": launch, "gather": gather,
+    print("[probes] gather done", file=sys.stderr, flush=True)
+    return {"stream": stream, "launch": launch, "handoff": handoff, "barrier": barrier, "chain": chain,
+            "gather": gather,
             "what": "mx_stream_probe (per-workgroup contiguous runs, 20 launches per graph over 2 GiB), "
-                    "mx_launch_probe (graphs of 100 launches), mx_run_gather_probe / mx_kv_gather_probe over "
-                    "config 2's K/V runs (one call per layer of a 32-layer pool)"}
+                    "mx_launch_probe (graphs of 100 launches), mx_handoff_probe (graphs of 20 calls), "
+                    "mx_barrier_probe (per barrier: a 200-round launch less a 0-round one), mx_chain_probe "
+                    "(per phase, graph of one launch per phase vs one persistent launch), "
+                    "mx_run_gather_probe / mx_kv_gather_probe over config 2's K/V runs (one call per layer of "
+                    "a 32-layer pool)"}
+
+
+HANDOFF_SHAPES = ((256, 4), (512, 16), (1024, 4), (2048, 8))
+HANDOFF_MODES = ("partials alone", "+ a reduce launch", "last arriver, agent-scope release/acquire",
+                 "last arriver, seq_cst fences", "last arriver, write-through stores + ticket, no fences")
+BARRIER_MODES = ("one device-scope counter, thread 0 polls", "one flag per workgroup, one wave polls all",
+                 "8 group counters, every workgroup polls all 8",
+                 "8 group counters + 1 KiB per workgroup handed over through device-coherent stores and loads",
+                 "8 group counters + the same 1 KiB behind agent-scope release/acquire fences")
+CHAIN_PER_WG = (8 << 10, 32 << 10, 64 << 10, 128 << 10, 256 << 10)
+
+
+def handoff_probes():
+    """What handing data between the workgroups of one launch costs against a launch boundary.
+
+    * handoff: groups of G workgroups each write an 8 KiB fp32 partial that one workgroup (or a second
+      launch) must sum (``mx_handoff_probe``, five ways); per call us, graphs of 20 calls.
+    * barrier: 256 resident workgroups of 512 threads pass grid barriers of five kinds
+      (``mx_barrier_probe``); us per barrier = (200-round launch - 0-round launch) / 200.
+    * chain: phases that each stream distinct weight bytes (256 workgroups x B bytes) and hand 1 KiB per
+      workgroup to the next phase, as a graph of one launch per phase or as one persistent launch that
+      issues each phase's first loads before its barrier (``mx_chain_probe``); us per phase, enough
+      phases to read at least 512 MB (past the 256 MB MALL).
+    Every call's error word (time-outs, wrong hand-off values) and result are checked.
+    """
+    import torch
+
+    from runtime_amd.phase2 import _hip
+
+    lib = _hip.load()
+    dev = torch.device("cuda:0")
+    handoff = []
+    for wgs, g in HANDOFF_SHAPES:
+        part = torch.empty(wgs * 2048, dtype=torch.float32, device=dev)
+        out = torch.empty(wgs // g * 2048, dtype=torch.float32, device=dev)
+        tickets = torch.zeros(wgs // g, dtype=torch.int32, device=dev)
+        row = {"workgroups": wgs, "group": g}
+        for mode, name in enumerate(HANDOFF_MODES):
+            def run(mode=mode):
+                st = _hip.stream_handle(dev)
+                for _ in range(20):
+                    _hip.check(lib.mx_handoff_probe(part.data_ptr(), part.numel() * 4, out.data_ptr(), out.numel() * 4,
+                                                    tickets.data_ptr(), tickets.numel() * 4, wgs, g, mode, st),
+                               "mx_handoff_probe")
+            row[name] = round(graph_time(run, 20) * 1e6, 2)
+        if int(tickets.abs().sum()) != 0:
+            raise RuntimeError("mx_handoff_probe left a ticket set")
+        handoff.append(row)
+        del part, out, tickets
+    print("[probes] handoff done", file=sys.stderr, flush=True)
+    n = 256
+    sync = torch.zeros(16 + n, dtype=torch.int32, device=dev)
+    hand = torch.zeros(2 * n * 256, dtype=torch.int32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    barrier = []
+    for mode, name in enumerate(BARRIER_MODES):
+        t = {}
+        for rounds in (0, 200):
+            def run(rounds=rounds, mode=mode):
+                _hip.check(lib.mx_barrier_probe(sync.data_ptr(), sync.numel() * 4, hand.data_ptr(), hand.numel() * 4, n,
+                                                rounds, mode, err.data_ptr(), _hip.stream_handle(dev)),
+                           "mx_barrier_probe")
+            t[rounds] = graph_time(run, 1, reps=10)
+        if int(err) != 0:
+            raise RuntimeError(f"mx_barrier_probe mode {mode}: error word {int(err)}")
+        barrier.append({"barrier": name, "workgroups": n, "us_per_barrier": round((t[200] - t[0]) / 200 * 1e6, 2)})
+    print("[probes] barrier done", file=sys.stderr, flush=True)
+    chain = []
+    span = max(per * n * max(8, -(-(512 << 20) // (per * n))) for per in CHAIN_PER_WG)
+    src = torch.empty(span, dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for per in CHAIN_PER_WG:
+        phases = min(256, max(8, -(-(512 << 20) // (per * n))))
+        row = {"weight_bytes_per_phase": per * n, "phases": phases}
+        for persistent, name in ((0, "graph of kernels"), (1, "persistent kernel")):
+            def run(persistent=persistent, per=per, phases=phases):
+                st = _hip.stream_handle(dev)
+                calls = [(0, phases)] if persistent else [(p, 1) for p in range(phases)]
+                for p0, count in calls:
+                    _hip.check(lib.mx_chain_probe(src.data_ptr(), span, per, n, p0, count, persistent, sync.data_ptr(),
+                                                  sync.numel() * 4, hand.data_ptr(), hand.numel() * 4, err.data_ptr(),
+                                                  sink.data_ptr(), st), "mx_chain_probe")
+            row[name] = round(graph_time(run, phases) * 1e6, 2)
+            if int(err) != 0:
+                raise RuntimeError(f"mx_chain_probe ({name}, {per} bytes per workgroup): error word {int(err)}")
+        chain.append(row)
+        print(f"[probes] chain {per} bytes per workgroup done", file=sys.stderr, flush=True)
+    del src
+    torch.cuda.empty_cache()
+    return handoff, barrier, chain
 
 
 # (waves, runs in flight, streaming, load pattern: 0 1 KiB contiguous, 1/2 the attention kernel's operand loads)
@@ -1101,8 +1200,8 @@ def main() -> int:
         return 0
     if args.workload == "probes":
         pr = calibration_probes(args)
-        print(json.dumps({"metric": "calibration probes (per-CU streaming, launch floor in a HIP graph)", "n_gpus": 1,
-                          "data": DATA, **pr}), flush=True)
+        print(json.dumps({"metric": "calibration probes (per-CU streaming, launch floor in a HIP graph, in-launch "
+                                    "hand-offs, K/V gather)", "n_gpus": 1, "data": DATA, **pr}), flush=True)
         return 0
     if args.workload == "qwen":
         c3 = config3_qwen(args)

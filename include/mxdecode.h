@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 17
+#define MX_ABI_VERSION 18
 
 typedef enum mx_status {
     MX_OK = 0,
@@ -308,6 +308,53 @@ int mx_launch_probe(void* dst, int64_t dst_bytes, int64_t bytes, int32_t workgro
 int mx_run_gather_probe(const void* base, int64_t base_bytes, const int64_t* offsets, int64_t n_runs,
                         int32_t run_bytes, int32_t waves, int32_t in_flight, int32_t streaming, int32_t pattern,
                         int32_t* sink, void* stream);
+
+/* Calibration probe (no reference counterpart; used by bench.py --workload
+ * probes): what handing data between the workgroups of one launch costs
+ * against a launch boundary. `workgroups` workgroups of 256 threads each write
+ * an 8 KiB fp32 partial to part (float i of workgroup w: (31 w + i) & 1023);
+ * the partials of each group of `group` consecutive workgroups are summed in
+ * workgroup order into out[w / group] (2048 floats). Mode 0: the partials
+ * only (out untouched); 1: the partials, then a second launch that sums each
+ * group; 2: the group's last workgroup to take a ticket sums them, behind
+ * agent-scope release/acquire fences; 3: the same with sequentially
+ * consistent fences; 4: the same without fences, the partials written and
+ * read device-coherent. tickets (one int32 per group, modes 2-4) must be zero
+ * before the first call; each call leaves them zero. part and out 16-byte
+ * aligned. */
+int mx_handoff_probe(float* part, int64_t part_bytes, float* out, int64_t out_bytes, int32_t* tickets,
+                     int64_t tickets_bytes, int32_t workgroups, int32_t group, int32_t mode, void* stream);
+
+/* Calibration probe (no reference counterpart; used by bench.py --workload
+ * probes): `workgroups` workgroups of 512 threads, all resident at once (else
+ * MX_ERR_UNSUPPORTED), pass `rounds` grid barriers. Mode 0: one counter,
+ * polled by thread 0; 1: one flag per workgroup, wave 0 polls them all; 2: 8
+ * counters, polled by 8 threads; 3: as 2, with 1 KiB per workgroup handed to
+ * the next workgroup each round through device-coherent stores and loads
+ * (hand: 2 KiB per workgroup, 16-byte aligned); 4: as 3 with plain stores and
+ * loads behind agent-scope release/acquire fences. sync (16 + workgroups int32)
+ * must be zero before the first call; each call leaves it zero. Waits are
+ * bounded: a wait that times out sets err bit 1 (the launch still ends); a
+ * hand-off that reads a wrong value sets bit 2. */
+int mx_barrier_probe(int32_t* sync, int64_t sync_bytes, int32_t* hand, int64_t hand_bytes, int32_t workgroups,
+                     int32_t rounds, int32_t mode, int32_t* err, void* stream);
+
+/* Calibration probe (no reference counterpart; used by bench.py --workload
+ * probes): a chain of phases, each streaming bytes_per_wg distinct bytes per
+ * workgroup of src (phase p, workgroup w: the run at (p x workgroups + w) x
+ * bytes_per_wg) and handing 1 KiB per workgroup to the next phase (workgroup w
+ * reads what w + 1 wrote; phase p writes p + 1, a wrong value sets err bit 2).
+ * persistent == 0 runs phases [phase0, phase0 + phases) with plain hand-off
+ * stores and loads: one phase per call is the graph of kernels. persistent !=
+ * 0 runs phases [0, phases) in one launch of resident workgroups (else
+ * MX_ERR_UNSUPPORTED): each phase issues its first loads (up to 128 KiB per
+ * workgroup), waits at an 8-counter grid barrier (sync: 9 int32, zero before
+ * the first call, left zero), and hands over through device-coherent stores
+ * and loads; a wait that times out sets err bit 1. hand: 2 KiB per workgroup, 16-byte aligned. Nothing
+ * else is written except, with negligible odds, a checksum to sink[0]. */
+int mx_chain_probe(const void* src, int64_t src_bytes, int64_t bytes_per_wg, int32_t workgroups, int32_t phase0,
+                   int32_t phases, int32_t persistent, int32_t* sync, int64_t sync_bytes, int32_t* hand,
+                   int64_t hand_bytes, int32_t* err, int32_t* sink, void* stream);
 
 /* Byte offset of the int32 error word inside a paged-attention workspace
  * (nonzero after a call that met an out-of-range block id). Reading it needs a

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libmxdecode.so")
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 MX_OK = 0
 MX_ERR_INVALID = -1
@@ -98,6 +98,9 @@ SIGNATURES = {
     "mx_stream_probe": (ctypes.c_int, [_p, _i64, _i64, _i64, _i32, _i32, _p, _p]),
     "mx_launch_probe": (ctypes.c_int, [_p, _i64, _i64, _i32, _p]),
     "mx_run_gather_probe": (ctypes.c_int, [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p]),
+    "mx_handoff_probe": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p]),
+    "mx_barrier_probe": (ctypes.c_int, [_p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p]),
+    "mx_chain_probe": (ctypes.c_int, [_p, _i64, _i64, _i32, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p]),
 }
 
 _lib = None

@@ -177,6 +177,35 @@ def test_calibration_probes_reject_bad_arguments():
     _status(lib.mx_launch_probe(fake, 1 << 20, 2 << 20, 2, None), _hip.MX_ERR_INVALID)  # past the end
     _status(lib.mx_launch_probe(None, 1 << 20, 4096, 2, None), _hip.MX_ERR_NULL)
     _status(lib.mx_launch_probe(None, 0, 0, 0, None), _hip.MX_ERR_INVALID)
+    # hand-off, barrier and chain probes: argument checks that come before any device query
+    kb = 8 << 10
+    _status(lib.mx_handoff_probe(fake, 256 * kb, fake, 64 * kb, fake, 256, 256, 4, 5, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_handoff_probe(fake, 256 * kb, fake, 64 * kb, fake, 256, 250, 4, 2, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_handoff_probe(None, 256 * kb, fake, 64 * kb, fake, 256, 256, 4, 2, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_handoff_probe(fake, 256 * kb, fake, 64 * kb, None, 256, 256, 4, 2, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_handoff_probe(fake, 255 * kb, fake, 64 * kb, fake, 256, 256, 4, 2, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_handoff_probe(fake, 256 * kb, fake, 64 * kb, fake, 252, 256, 4, 2, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_handoff_probe(ctypes.c_void_p((1 << 20) + 4), 256 * kb, fake, 64 * kb, fake, 256, 256, 4, 2, None),
+            _hip.MX_ERR_ALIGNMENT)
+    _status(lib.mx_barrier_probe(fake, 4096, fake, 1 << 20, 256, 10, 5, fake, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_barrier_probe(None, 4096, fake, 1 << 20, 256, 10, 0, fake, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_barrier_probe(fake, 4096, None, 1 << 20, 256, 10, 3, fake, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_barrier_probe(fake, 4096, fake, 1 << 20, 256, 10, 0, None, None), _hip.MX_ERR_NULL)
+    _status(lib.mx_barrier_probe(fake, 4096, fake, 1 << 20, 256, -1, 0, fake, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_barrier_probe(fake, 4096, fake, 1 << 20, 0, 10, 0, fake, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_barrier_probe(fake, 4 * 271, fake, 1 << 20, 256, 10, 1, fake, None), _hip.MX_ERR_INVALID)
+    _status(lib.mx_barrier_probe(fake, 4096, fake, 256 * 2048 - 16, 256, 10, 3, fake, None), _hip.MX_ERR_INVALID)
+
+    def chain(src_bytes=8 * 256 * kb, per=kb, wgs=256, p0=0, phases=8, persistent=0, hand=fake, sync=fake):
+        return lib.mx_chain_probe(fake, src_bytes, per, wgs, p0, phases, persistent, sync, 64, hand, 256 * 2048, fake,
+                                  fake, None)
+
+    _status(chain(phases=0), _hip.MX_ERR_INVALID)
+    _status(chain(per=kb + 8), _hip.MX_ERR_INVALID)  # not 16-byte
+    _status(chain(src_bytes=8 * 256 * kb - 16), _hip.MX_ERR_INVALID)  # past the end
+    _status(chain(p0=1, phases=7, persistent=1), _hip.MX_ERR_INVALID)  # a persistent launch starts at phase 0
+    _status(chain(hand=None), _hip.MX_ERR_NULL)
+    _status(chain(sync=None, persistent=1), _hip.MX_ERR_NULL)
 
 
 def test_fused_mlp_rejects_bad_arguments():
