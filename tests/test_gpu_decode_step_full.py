@@ -21,7 +21,9 @@ Cases:
   the lengths are the bench's, the tables hold 65 steps of headroom where the bench's hold 33),
   a 16384-block pool of N(0, 1) K/V, vocabulary 128256, 64 steps from seeded random tokens. The
   layer count is 4 (the bench's 32 only repeat the same launches over other weights) so that the
-  CPU oracle finishes in about a minute.
+  CPU oracle finishes in about a minute;
+* the headline at its full depth, 32 layers, over 8 steps, against the same fp32 model run by torch
+  on the GPU (the CPU oracle would take minutes per row at this depth).
 
 Oracle: the HF model in fp32 on the CPU holding exactly the device weights
 (``oracle.model.quantized_reference``), continued from each row's K/V as the pool holds them
@@ -59,10 +61,10 @@ BLOCK_SIZE = 16
 STEPS = 64
 
 
-def _drive(native, pool, tables_d, seq_lens, tokens):
-    """STEPS steps as bench.py runs them: one eager step, then a captured step graph replayed.
+def _drive(native, pool, tables_d, seq_lens, tokens, steps=STEPS):
+    """``steps`` steps as bench.py runs them: one eager step, then a captured step graph replayed.
     ``tokens`` holds each step's input and receives its output in place. Returns the input tokens
-    ``[B, STEPS]`` and the logits ``[B, STEPS, V]`` (fp16, CPU) of every step."""
+    ``[B, steps]`` and the logits ``[B, steps, V]`` (fp16, CPU) of every step."""
     assert native.attn_plan and pool.block_size_tokens >= 16, "the tile plan must be on, as in the bench"
     seen_tokens, seen_logits = [tokens.cpu()], []
     _, logits = native.step(tokens, pool, tables_d, seq_lens, return_logits=True, out=tokens)
@@ -72,7 +74,7 @@ def _drive(native, pool, tables_d, seq_lens, tokens):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         _, logits_g = native.step(tokens, pool, tables_d, seq_lens, return_logits=True, out=tokens)
-    for _ in range(STEPS - 1):
+    for _ in range(steps - 1):
         graph.replay()
         seen_logits.append(logits_g.cpu())
         seen_tokens.append(tokens.cpu())
@@ -106,7 +108,7 @@ def _summary(results, label):
     steps = sum(r["steps"] for r in results)
     flips = sum(r["mismatches"] for r in results)
     identical = sum(r["mismatches"] == 0 for r in results)
-    return (f"[{label}] {identical}/{len(results)} rows with all {STEPS} tokens identical, {flips} near-tie flips "
+    return (f"[{label}] {identical}/{len(results)} rows with all {results[0]['steps']} tokens identical, {flips} near-tie flips "
             f"in {steps} steps (torch fp16 {sum(r['yard'] for r in results)}), largest logit error "
             f"{max(r['err'] for r in results):.3e} (torch fp16 {max(r['err16'] for r in results):.3e}), smallest "
             f"oracle top-1 margin {min(r['min_margin'] for r in results):.3e}")
@@ -247,3 +249,55 @@ def test_native_step_llama3_b32_bench_inputs():
     torch.cuda.empty_cache()
     _check_tolerance(_compare(ref, torch16, kv_rows, inputs, outputs, logits, "llama3 native"),
                      "llama3-8b dims native step, batch 32, bench contexts")
+
+
+@pytest.mark.timeout(1200)
+def test_native_step_llama3_b32_bench_inputs_all_32_layers():
+    """The headline step at its full depth: all 32 layers of Llama-3-8B dims, batch 32, the bench's
+    contexts and tables, vocabulary 128256, one eager step and 7 graph replays with the tile plan.
+    The fp32 CPU oracle would take minutes per row at this depth, so the reference here is the same
+    fp32 HF model holding exactly the device weights (``oracle.model.quantized_reference``), run in
+    fp32 by torch on the GPU and continued from each row's K/V as the pool holds them; the yardstick
+    is that model in fp16. Same rules as above. The 4-layer test checks 64 steps against the CPU
+    oracle; this one checks that 28 more layers of the same launches keep the error in bounds."""
+    from runtime_amd.phase2.decode_step import Int8DecodeModel, make_contexts
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+
+    layers, batch, pool_blocks, steps = 32, 32, 16384, 8
+    print(f"[llama32 native] building the {layers}-layer Llama-3-8B-dims model (vocab 128256) on the CPU", flush=True)
+    hf = om.random_llama(seed=0, parallel=True, num_hidden_layers=layers)
+    cfg = hf.config
+    assert (cfg.num_hidden_layers, cfg.hidden_size, cfg.vocab_size) == (32, 4096, 128256)
+    print("[llama32 native] quantizing the reference on the CPU", flush=True)
+    ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
+    print("[llama32 native] quantizing the native model on the GPU", flush=True)
+    native = Int8DecodeModel.from_hf(hf, device=DEV)
+    del hf
+    print("[llama32 native] moving the fp32 reference and its fp16 copy to the GPU", flush=True)
+    ref = om.to_device_dtype(ref, DEV, torch.float32).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), DEV, torch.float16).eval()
+    s = native.shape
+    lens, tables = make_contexts(batch, 128, 4096, BLOCK_SIZE, pool_blocks, headroom=steps + 1, seed=0)
+    lens = lens.tolist()
+    pool = GpuKVBlockPool(num_blocks=pool_blocks, block_size_tokens=BLOCK_SIZE, num_layers=layers,
+                          num_kv_heads=s.kv_heads, head_dim=s.head_dim, dtype=torch.float16, device=DEV)
+    pool._ensure_pools()
+    g = torch.Generator(device=DEV).manual_seed(1)
+    rows = [tables[b, :math.ceil(lens[b] / BLOCK_SIZE)].long().to(DEV) for b in range(batch)]
+    kv_rows = [[] for _ in range(batch)]
+    for li in range(layers):
+        pair = []
+        for view in (pool.k_layer_view(li), pool.v_layer_view(li)):
+            view.copy_(torch.randn(view.shape, generator=g, device=DEV).half())
+            pair.append([view[ids].permute(1, 0, 2, 3).reshape(s.kv_heads, -1, s.head_dim)[:, :lens[b]]
+                         for b, ids in enumerate(rows)])
+        for b in range(batch):
+            kv_rows[b].append((pair[0][b], pair[1][b]))  # fp16 copies of the pool's values, on the GPU
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    tokens = torch.randint(0, cfg.vocab_size, (batch,), generator=torch.Generator().manual_seed(2)).to(DEV)
+    print(f"[llama32 native] {steps} steps, batch {batch}, contexts {min(lens)}..{max(lens)}, graph replay with the "
+          f"tile plan", flush=True)
+    inputs, logits, outputs = _drive(native, pool, tables.to(DEV), seq_lens, tokens, steps=steps)
+    assert seq_lens.cpu().tolist() == [n + steps for n in lens]
+    results = _compare(ref, torch16, kv_rows, inputs, outputs, logits, "llama3 native, 32 layers")
+    _check_tolerance(results, "llama3-8b dims native step, 32 layers, batch 32, bench contexts")
