@@ -22,7 +22,7 @@ Cases:
   a 16384-block pool of N(0, 1) K/V, vocabulary 128256, 64 steps from seeded random tokens. The
   layer count is 4 (the bench's 32 only repeat the same launches over other weights) so that the
   CPU oracle finishes in about a minute;
-* the headline at its full depth, 32 layers, over 8 steps, against the same fp32 model run by torch
+* the headline at its full depth, 32 layers, over the same 64 steps, against the same fp32 model run by torch
   on the GPU (the CPU oracle would take minutes per row at this depth).
 
 Oracle: the HF model in fp32 on the CPU holding exactly the device weights
@@ -254,16 +254,18 @@ def test_native_step_llama3_b32_bench_inputs():
 @pytest.mark.timeout(1200)
 def test_native_step_llama3_b32_bench_inputs_all_32_layers():
     """The headline step at its full depth: all 32 layers of Llama-3-8B dims, batch 32, the bench's
-    contexts and tables, vocabulary 128256, one eager step and 7 graph replays with the tile plan.
+    contexts and tables, vocabulary 128256, one eager step and 63 graph replays with the tile plan.
     The fp32 CPU oracle would take minutes per row at this depth, so the reference here is the same
     fp32 HF model holding exactly the device weights (``oracle.model.quantized_reference``), run in
     fp32 by torch on the GPU and continued from each row's K/V as the pool holds them; the yardstick
-    is that model in fp16. Same rules as above. The 4-layer test checks 64 steps against the CPU
-    oracle; this one checks that 28 more layers of the same launches keep the error in bounds."""
+    is that model in fp16. Same rules as above. The 4-layer test checks the same 64 steps against the
+    CPU oracle; this one checks that 28 more layers of the same launches keep the error in bounds
+    (measured on MI355X: 15/32 rows with all 64 tokens identical, 29 near-tie flips in 2048 steps
+    against torch fp16's 44, largest logit error 7.0e-2 against torch fp16's 1.1e-1)."""
     from runtime_amd.phase2.decode_step import Int8DecodeModel, make_contexts
     from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
 
-    layers, batch, pool_blocks, steps = 32, 32, 16384, 8
+    layers, batch, pool_blocks, steps = 32, 32, 16384, STEPS
     print(f"[llama32 native] building the {layers}-layer Llama-3-8B-dims model (vocab 128256) on the CPU", flush=True)
     hf = om.random_llama(seed=0, parallel=True, num_hidden_layers=layers)
     cfg = hf.config
