@@ -23,7 +23,9 @@ Cases:
   layer count is 4 (the bench's 32 only repeat the same launches over other weights) so that the
   CPU oracle finishes in about a minute;
 * the headline at its full depth, 32 layers, over the same 64 steps, against the same fp32 model run by torch
-  on the GPU (the CPU oracle would take minutes per row at this depth).
+  on the GPU (the CPU oracle would take minutes per row at this depth);
+* config 5 as the bench times it at full depth (128 rows on shared prefixes, contexts U[1, 8192]), the
+  same way.
 
 Oracle: the HF model in fp32 on the CPU holding exactly the device weights
 (``oracle.model.quantized_reference``), continued from each row's K/V as the pool holds them
@@ -61,11 +63,12 @@ BLOCK_SIZE = 16
 STEPS = 64
 
 
-def _drive(native, pool, tables_d, seq_lens, tokens, steps=STEPS):
+def _drive(native, pool, tables_d, seq_lens, tokens, steps=STEPS, plan=True):
     """``steps`` steps as bench.py runs them: one eager step, then a captured step graph replayed.
     ``tokens`` holds each step's input and receives its output in place. Returns the input tokens
     ``[B, steps]`` and the logits ``[B, steps, V]`` (fp16, CPU) of every step."""
-    assert native.attn_plan and pool.block_size_tokens >= 16, "the tile plan must be on, as in the bench"
+    if plan:
+        assert native.attn_plan and pool.block_size_tokens >= 16, "the tile plan must be on, as in the bench"
     seen_tokens, seen_logits = [tokens.cpu()], []
     _, logits = native.step(tokens, pool, tables_d, seq_lens, return_logits=True, out=tokens)
     seen_logits.append(logits.cpu())
@@ -83,9 +86,11 @@ def _drive(native, pool, tables_d, seq_lens, tokens, steps=STEPS):
 
 
 def _compare(ref, torch16, kv_rows, inputs, outputs, logits, label):
-    """Per row: oracle and yardstick continued from the row's K/V over its input tokens."""
+    """Per row: oracle and yardstick continued from the row's K/V over its input tokens. ``kv_rows``
+    is a list of per-row K/V or a function of the row that returns it."""
     results = []
-    for b, kv in enumerate(kv_rows):
+    for b in range(inputs.shape[0]):
+        kv = kv_rows(b) if callable(kv_rows) else kv_rows[b]
         ref_logits = om.continue_logits(ref, kv, inputs[b])
         t16 = om.continue_logits(torch16, kv, inputs[b])
         mine = logits[b].float()
@@ -303,3 +308,61 @@ def test_native_step_llama3_b32_bench_inputs_all_32_layers():
     assert seq_lens.cpu().tolist() == [n + steps for n in lens]
     results = _compare(ref, torch16, kv_rows, inputs, outputs, logits, "llama3 native, 32 layers")
     _check_tolerance(results, "llama3-8b dims native step, 32 layers, batch 32, bench contexts")
+
+
+@pytest.mark.timeout(1200)
+def test_native_step_config5_bench_inputs_all_32_layers():
+    """Config 5 as the bench times it, at full depth: Llama-3-8B dims, 32 layers, vocabulary 128256,
+    128 rows in 16 groups whose rows alias their group's 1024-token prefix blocks (contexts U[1, 8192],
+    the bench's PrefixBatch seed and 40960-block pool of N(0, 1) K/V), attention with shared block ids
+    (``shared_kv_blocks``), one eager step and 63 graph replays. Reference and rules as in the 32-layer
+    headline test; each row's K/V is gathered from the pool below its starting length when it is
+    compared (decode only appends past it, and shared prefix blocks are never written). Rows joining
+    and finishing between replays are checked against the CPU oracle in test_gpu_prefix_batch.py.
+    Measured on MI355X: 37/128 rows with all 64 tokens identical, 138 near-tie flips in 8192 steps
+    against torch fp16's 192, largest logit error 7.2e-2 against torch fp16's 1.17e-1."""
+    from runtime_amd.phase2.decode_step import Int8DecodeModel
+    from runtime_amd.phase2.paged_kv_kernel import GpuKVBlockPool
+    from runtime_amd.phase2.prefix_batch import PrefixBatch
+
+    layers, batch, num_blocks = 32, 128, 40960
+    print(f"[config5 32 layers] building the {layers}-layer Llama-3-8B-dims model on the CPU", flush=True)
+    hf = om.random_llama(seed=0, parallel=True, num_hidden_layers=layers)
+    cfg = hf.config
+    assert (cfg.num_hidden_layers, cfg.hidden_size, cfg.vocab_size) == (32, 4096, 128256)
+    print("[config5 32 layers] quantizing the reference on the CPU", flush=True)
+    ref = om.quantized_reference(hf, targets=om.PROJECTIONS + ("lm_head",))
+    native = Int8DecodeModel.from_hf(hf, device=DEV)
+    native.shared_kv_blocks = True
+    del hf
+    print("[config5 32 layers] moving the fp32 reference and its fp16 copy to the GPU", flush=True)
+    ref = om.to_device_dtype(ref, DEV, torch.float32).eval()
+    torch16 = om.to_device_dtype(copy.deepcopy(ref), DEV, torch.float16).eval()
+    s = native.shape
+    pb = PrefixBatch(batch=batch, groups=16, prefix_tokens=1024, lo=1, hi=8192, block_size=BLOCK_SIZE,
+                     num_blocks=num_blocks, headroom=STEPS + 1, seed=0)
+    shared = sum(r.shared > 0 for r in pb.rows)
+    pool = GpuKVBlockPool(num_blocks=num_blocks, block_size_tokens=BLOCK_SIZE, num_layers=layers,
+                          num_kv_heads=s.kv_heads, head_dim=s.head_dim, dtype=torch.float16, device=DEV)
+    pool._ensure_pools()
+    g = torch.Generator(device=DEV).manual_seed(1)
+    for li in range(layers):
+        for view in (pool.k_layer_view(li), pool.v_layer_view(li)):
+            view.copy_(torch.randn(view.shape, generator=g, device=DEV).half())
+    tables = pb.tables
+    lens = pb.lens.tolist()
+    tables_d = tables.to(DEV)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    tokens = torch.randint(0, cfg.vocab_size, (batch,), generator=torch.Generator().manual_seed(2)).to(DEV)
+    print(f"[config5 32 layers] {STEPS} steps, {batch} rows ({shared} on shared prefixes), contexts "
+          f"{min(lens)}..{max(lens)}, unique K/V tokens {pb.unique_tokens()} of {pb.logical_tokens()}", flush=True)
+    inputs, logits, outputs = _drive(native, pool, tables_d, seq_lens, tokens, plan=False)
+    assert seq_lens.cpu().tolist() == [n + STEPS for n in lens]
+
+    def row_kv(b):
+        ids = tables[b, :math.ceil(lens[b] / BLOCK_SIZE)].long().to(DEV)
+        return [tuple(view[ids].permute(1, 0, 2, 3).reshape(s.kv_heads, -1, s.head_dim)[:, :lens[b]]
+                      for view in (pool.k_layer_view(li), pool.v_layer_view(li))) for li in range(layers)]
+
+    results = _compare(ref, torch16, row_kv, inputs, outputs, logits, "config5 native, 32 layers")
+    _check_tolerance(results, "config5 native step, 32 layers, 128 rows on shared prefixes, bench contexts")
