@@ -43,6 +43,7 @@ Each test reports rows with every token identical, flips and errors (``ParityRep
 from __future__ import annotations
 
 import copy
+import gc
 import math
 
 import pytest
@@ -61,6 +62,16 @@ MAX_TIE_FRACTION = 0.02
 MARGIN_MULTIPLE = 10.0
 BLOCK_SIZE = 16
 STEPS = 64
+
+
+@pytest.fixture(autouse=True)
+def _release_device_memory():
+    """These tests hold tens to a hundred and more GB of device memory (full-depth models, 16384- and
+    40960-block pools): hand it back to the device after each one, pass or fail, so that the tests
+    after them start from an empty caching allocator."""
+    yield
+    gc.collect()
+    torch.cuda.empty_cache()
 
 
 def _drive(native, pool, tables_d, seq_lens, tokens, steps=STEPS, plan=True):
