@@ -296,7 +296,7 @@ __device__ __forceinline__ void gemm_body(const int gx, const int ks, const int 
     constexpr int RS = kTileK + 8;  // LDS row stride (halfs): 144 bytes, rows start 4 banks apart
     constexpr int WN = WAVES / (KW * MW);  // waves along N per k part, each owning NPW n-tiles
     constexpr int WP = WN * MW;            // waves per k part
-    static_assert(WN * KW * MW == WAVES && (KW == 1 || !GU), "k parts split only partial launches");
+    static_assert(WN * KW * MW == WAVES, "waves: k parts x m groups x n groups");
     constexpr int XCH = ROWS * 8;   // 16-byte chunks of one x k-tile
     constexpr int XC = (XCH + WP * 64 - 1) / (WP * 64);
     static_assert(NJX == 0 || (!SW && MW == 1), "whole-range x staging: plain x, one m group");
@@ -519,6 +519,25 @@ __device__ __forceinline__ void gemm_body(const int gx, const int ks, const int 
     if constexpr (kRaw) convert_epilogue();
 #undef MX_NJX_HOOK
     const int N = NT * kTileN;
+    if constexpr (KW > 1) {
+        // Parts 1.. hand their accumulators to part 0 through LDS; every wave reaches this
+        // barrier (out-of-range waves too) before any of them leaves.
+        __shared__ float4v red[KW - 1][WP][NPW][MT][64];
+        if (kw > 0) {
+#pragma unroll
+            for (int p = 0; p < NPW; ++p)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) red[kw - 1][wm][p][mt][lane] = acc[p][mt];
+        }
+        __syncthreads();
+        if (kw > 0) return;
+#pragma unroll
+        for (int q = 0; q < KW - 1; ++q)
+#pragma unroll
+            for (int p = 0; p < NPW; ++p)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) acc[p][mt] += red[q][wm][p][mt][lane];
+    }
     if (GU) {
         // FUSE == 1: the workgroup's [ROWS, 64] activation tile is gathered in LDS first and stored
         // as whole 128-byte lines of each row (write-through, see below).
@@ -562,25 +581,6 @@ __device__ __forceinline__ void gemm_body(const int gx, const int ks, const int 
             }
         }
         return;
-    }
-    if constexpr (KW > 1) {
-        // Parts 1.. hand their accumulators to part 0 through LDS; every wave reaches this
-        // barrier (out-of-range waves too) before any of them leaves.
-        __shared__ float4v red[KW - 1][WP][NPW][MT][64];
-        if (kw > 0) {
-#pragma unroll
-            for (int p = 0; p < NPW; ++p)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) red[kw - 1][wm][p][mt][lane] = acc[p][mt];
-        }
-        __syncthreads();
-        if (kw > 0) return;
-#pragma unroll
-        for (int q = 0; q < KW - 1; ++q)
-#pragma unroll
-            for (int p = 0; p < NPW; ++p)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) acc[p][mt] += red[q][wm][p][mt][lane];
     }
     if (!valid) return;
 #pragma unroll
@@ -837,6 +837,13 @@ struct WideShape {
     int waves, npw;
 };
 constexpr int kOneRoundLo = 240, kOneRoundHi = 256;
+// gate||up with the SwiGLU epilogue at most this many k-tiles long (whole-range x staging, one
+// round of workgroups) runs as 8-wave workgroups of two k parts x 4 n-tiles, the parts summed in LDS
+// before the epilogue: each wave's dependent chain of k-tiles is half as long. Measured on MI355X
+// (Qwen2-0.5B gate||up, 4864 x 2 channels, 14 k-tiles, 16 rows; three interleaved rounds): 5.80-5.81 ->
+// 5.36-5.39 us, the config-3 step 0.949-0.950 -> 0.941-0.942 ms. 4-wave workgroups of two k parts x 2
+// n-tiles (twice the workgroups) measured no gain, 5.85-5.88 us.
+constexpr int kGuShortKT = 32;
 static WideShape wide_shape(int NT, bool npw1_only) {
     const WideShape cands[] = {{8, 4}, {8, 2}, {8, 1}, {7, 1}, {6, 1}, {5, 1}};
     for (const WideShape& c : cands) {
@@ -914,6 +921,16 @@ static void launch_mfma(const uint16_t* x, int64_t xs, int M, const uint8_t* w, 
                 MX_WIDE(8, 4)
             }
 #undef MX_WIDE
+        }
+    }
+    // gate||up with the SwiGLU epilogue on short K: two k parts per workgroup (see kGuShortKT).
+    if constexpr (MT <= 2 && !SW && GU) {
+        if (KS == 1 && KW == 1 && KT <= kGuShortKT && KT % 2 == 0) {
+            if (KT / 2 <= 8)
+                launch_shape<MT, 1, 2 * kMfmaWaves, SW, GU, 2, 1, 8>(x, xs, M, w, s, b, y, ys, NT, KT, 1, partial, st);
+            else
+                launch_shape<MT, 1, 2 * kMfmaWaves, SW, GU, 2, 1, 16>(x, xs, M, w, s, b, y, ys, NT, KT, 1, partial, st);
+            return;
         }
     }
     if constexpr (MT <= 2 && !SW) {

@@ -241,15 +241,17 @@ def test_swiglu_linear_equals_silu_mul_then_linear(m, n, k):
 @pytest.mark.parametrize("m,inter,k", [(32, 14336, 4096), (7, 4864, 896), (64, 1024, 256), (128, 1024, 256),
                                         (70, 4864, 896), (100, 14336, 4096), (1, 4864, 896), (3, 4864, 896),
                                         (4, 4864, 896), (1, 14336, 4096), (4, 14336, 4096),
-                                        (49, 14336, 4096), (64, 14336, 4096)])
+                                        (49, 14336, 4096), (64, 14336, 4096), (16, 8192, 1024)])
 def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     """gate||up with interleaved rows and the SwiGLU product in the epilogue equals the plain
     [gate | up] projection followed by mx_silu_mul, bit for bit where both take the same K
-    accumulation (within fp16 rounding where the plain projection splits K). At M <= 4 on the Qwen2-0.5B
+    accumulation (within fp16 rounding where the plain projection splits K, or where the fused launch
+    sums two k parts: its MFMA launch at up to 32 rows and an even count of at most 32 k-tiles). At M <= 4 on the Qwen2-0.5B
     MLP (a shape whose MFMA launch splits K) the VALU GEMV takes both, with the product in
     the GEMV's own epilogue; the Llama MLP at M <= 4 runs the unsplit MFMA kernel, and shapes whose
-    plain projection splits K (the Qwen2 MLP at 7 and 70 rows) run one unsplit MFMA launch. The Llama
-    MLP at 49-64 rows takes the instance with two m-tiles per wave and the SwiGLU epilogue."""
+    plain projection splits K (the Qwen2 MLP at 7 and 70 rows) run one unsplit MFMA launch, in two k
+    parts at 7 rows. (16, 8192, 1024): an unsplit plain projection beside the two-part fused launch.
+    The Llama MLP at 49-64 rows takes the instance with two m-tiles per wave and the SwiGLU epilogue."""
     from runtime_amd.phase2.decode_glue import silu_mul
     from runtime_amd.phase2.int8_linear import (gateup_deinterleave, gateup_interleave, int8_gateup_swiglu,
                                                 linear_splits)
@@ -265,11 +267,13 @@ def test_gateup_swiglu_epilogue_equals_separate_ops(m, inter, k):
     assert torch.equal(gateup_interleave(plain_s[:inter], plain_s[inter:]), iscale)  # row-wise quantization
     want = silu_mul(int8_linear(x, pack_weight(plain_q), plain_s, None, 2 * inter))
     got = int8_gateup_swiglu(x, pack_weight(iq), iscale, None, inter)
-    if linear_splits(min(m, 128), 2 * inter, k) == 1:
+    kt = k // 64
+    two_parts = m <= 32 and kt <= 32 and kt % 2 == 0  # the fused MFMA launch's short-K shape
+    if linear_splits(min(m, 128), 2 * inter, k) == 1 and not two_parts:
         assert torch.equal(got, want)
     else:
-        # The plain projection sums two scaled split partials; the fused launch scales one sum over
-        # the whole K: the same value up to fp32 rounding, so g and u may differ by an fp16 ulp.
+        # The plain projection sums scaled split partials, or the fused launch sums two k parts
+        # before scaling: the same value up to fp32 rounding, so g and u may differ by an fp16 ulp.
         torch.testing.assert_close(got, want, atol=1e-2, rtol=1e-2)
         assert (got.float() - want.float()).abs().max() <= 4e-3 * want.float().abs().max()
 
