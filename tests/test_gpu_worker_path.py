@@ -196,6 +196,58 @@ def test_hip_graph_decode_matches_eager():
            f"{diff:.2e}, {five['replays']} + {four['replays']} replays of two captured steps")
 
 
+def test_hip_graph_manager_keeps_max_graphs_and_declines_when_off():
+    """``max_graphs=1``: five rows, then four after one finishes, then three: each row count gets its
+    own graph and the older one is dropped (least recently used), tokens equal eager decoding over the
+    same sequence. A manager that is not enabled (and not opted in by the environment) declines every
+    step, so the decoder runs eagerly and no graph is built."""
+    import os
+
+    from runtime_amd.phase2.hf_decode import PagedDecoder
+    from runtime_amd.phase2.hip_graph_decode import CudaGraphDecodeManager
+
+    model, _, _ = _model(seed=23)
+    g = torch.Generator().manual_seed(23)
+    lens = [40, 75, 120, 33, 90]
+    prompts = [torch.randint(0, 32768, (n,), generator=g) for n in lens]
+    phase = 4
+    need = [math.ceil((n + 3 * phase + 1) / BS) for n in lens]
+    rows, at = [], 0
+    for n in need:
+        rows.append(list(range(at, at + n))[::-1])
+        at += n
+    runs = {}
+    for mode in ("eager", "lru", "off"):
+        pool = _pool(at)
+        states = [_admit(model, pool, f"r{i}", prompts[i], rows[i]) for i in range(len(lens))]
+        if mode == "lru":
+            mgr = CudaGraphDecodeManager(model=model, device=DEV, warmup_steps=1, enabled=True, max_graphs=1)
+        elif mode == "off":
+            assert os.environ.get("PHASE2_CUDA_GRAPH", "0").strip() != "1", "the environment opts graphs in"
+            mgr = CudaGraphDecodeManager(model=model, device=DEV, warmup_steps=1, enabled=False)
+        else:
+            mgr = None
+        dec = PagedDecoder(model, pool, max_active=8, graph_mgr=mgr)
+        seen = []
+        for finish in (None, 1, 3):
+            if finish is not None:
+                done = states.pop(finish)
+                dec.release(done.req.request_id)
+                seen.append(done.generated_token_ids)
+            for _ in range(phase):
+                dec.decode_step(states)
+            if mode == "lru":
+                print(f"[hip graph lru] {len(states)} rows: {mgr.stats()['graphs']}", flush=True)
+                graphs = mgr.stats()["graphs"]
+                assert len(graphs) == 1 and graphs[0]["rows"] == len(states), graphs
+                assert graphs[0]["state"] == "captured" and graphs[0]["replays"] == phase - 1, graphs
+        seen += [s.generated_token_ids for s in states]
+        runs[mode] = seen
+        if mode == "off":
+            assert mgr.stats()["graphs"] == [] and not mgr.stats()["enabled"], mgr.stats()
+    assert runs["lru"] == runs["eager"], "graph replay tokens differ from eager decode"
+    assert runs["off"] == runs["eager"]
+
 def test_kv_write_overrun_raises_at_check():
     """write_tokens_batch queues the write without a host sync; a slot past the table is skipped
     and ``check_write_errors`` raises the reference's IndexError, once; with ``sync_write_checks`` the
