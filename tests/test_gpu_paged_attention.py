@@ -222,6 +222,29 @@ def test_config2_full_shape_and_repeatability():
     assert workspace_error_flag() == 0
 
 
+
+def test_config2_full_shape_bf16_plain_and_tile_plan():
+    """Config 2's shape (B 32, Hq 32, Hkv 8, D 128, block 16, contexts U[128, 4096], 16384-block pool)
+    with bf16 q and K/V (MX_PA_BF16): the plain call, the recording call and the plan-reading call give
+    the same bits, and match the fp32 oracle on the same bf16 values within BF16_TOL."""
+    from runtime_amd.phase2.paged_attention_hip import MX_PA_PLAN_READ, MX_PA_PLAN_WRITE
+
+    q, k, v, tables, lens, grp, scale = _config2(seed=3)
+    q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    dev = q.device
+    before = workspace_error_flag(dev)
+    plain = _decode(q, k, v, tables, lens, scale, grp)
+    from runtime_amd.phase2.paged_attention_hip import _decode as hip_decode
+    rec = hip_decode(q, k, v, tables, lens, scale, grp, plan=MX_PA_PLAN_WRITE)
+    read = hip_decode(q, k, v, tables, lens, scale, grp, plan=MX_PA_PLAN_READ)
+    torch.cuda.synchronize()
+    assert plain.dtype == torch.bfloat16
+    assert torch.equal(rec.view(torch.int16), plain.view(torch.int16))
+    assert torch.equal(read.view(torch.int16), plain.view(torch.int16))
+    assert (workspace_error_flag(dev) & ~before) == 0
+    want = oracle_out(q, k, v, tables, lens, scale, grp)
+    np.testing.assert_allclose(plain.float().cpu().numpy(), want.numpy(), atol=BF16_TOL, rtol=BF16_TOL)
+
 def _abi_decode(q, k, v, tables, lens, scale, grp, chunk_tokens, num_pool_blocks=None, flags=0):
     lib = _hip.load()
     bsz, hq, _, d = q.shape
