@@ -837,9 +837,10 @@ struct WideShape {
     int waves, npw;
 };
 constexpr int kOneRoundLo = 240, kOneRoundHi = 256;
-// gate||up with the SwiGLU epilogue at most this many k-tiles long (whole-range x staging, one
-// round of workgroups) runs as 8-wave workgroups of two k parts x 4 n-tiles, the parts summed in LDS
-// before the epilogue: each wave's dependent chain of k-tiles is half as long. Measured on MI355X
+// gate||up with the SwiGLU epilogue at most this many k-tiles long (an even count, up to 32 rows,
+// where no wide shape fits) runs as 8-wave workgroups of two k parts x 4 n-tiles with whole-range x
+// staging, the parts summed in LDS before the epilogue: each wave's dependent chain of k-tiles is half
+// as long. Measured on MI355X
 // (Qwen2-0.5B gate||up, 4864 x 2 channels, 14 k-tiles, 16 rows; three interleaved rounds): 5.80-5.81 ->
 // 5.36-5.39 us, the config-3 step 0.949-0.950 -> 0.941-0.942 ms. 4-wave workgroups of two k parts x 2
 // n-tiles (twice the workgroups) measured no gain, 5.85-5.88 us.
