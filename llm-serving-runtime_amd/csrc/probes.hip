@@ -308,8 +308,12 @@ __global__ __launch_bounds__(kBarrierThreads) void barrier_kernel(int32_t* sync,
         } else if (tid == 0) {
             __hip_atomic_fetch_add(sync + (MODE == 0 ? 0 : wg % kCounters), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        // A wait that gives up sets err bit 1 once; that thread waits no more.
         if (MODE == 0) {
-            if (tid == 0 && ok && !poll_at_least(sync, (r + 1) * N)) ok = false;
+            if (tid == 0 && ok && !poll_at_least(sync, (r + 1) * N)) {
+                ok = false;
+                atomicOr(err, 1);
+            }
         } else if (MODE == 1) {
             if (tid < 64 && ok) {
                 for (int polls = 0;; ++polls) {
@@ -319,15 +323,18 @@ __global__ __launch_bounds__(kBarrierThreads) void barrier_kernel(int32_t* sync,
                     if (__all(mine)) break;
                     if (polls >= kSpinLimit) {
                         ok = false;
+                        if (tid == 0) atomicOr(err, 1);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
                 }
             }
         } else {
-            if (tid < kCounters && ok && !poll_at_least(sync + tid, (r + 1) * counter_members(tid, N))) ok = false;
+            if (tid < kCounters && ok && !poll_at_least(sync + tid, (r + 1) * counter_members(tid, N))) {
+                ok = false;
+                atomicOr(err, 1);
+            }
         }
-        if (!ok && (tid == 0 || (MODE == 1 && tid < 64) || (MODE >= 2 && tid < kCounters))) atomicOr(err, 1);
         __syncthreads();
         if constexpr (MODE >= 3) {
             if (tid < 64) {
